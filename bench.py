@@ -1,0 +1,147 @@
+"""Benchmark: perturbed member-tokens/s of one MI355X on the full EGGROLL population step.
+
+    python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
+
+Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
+antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
+embedding and eps on the mixing scalars, sigma = 1e-3, one 2048-token Zipf(1.1) sequence -- then
+the fitness, the rank-1 gradient rebuild and an AdamW update of all weights. A step is one
+`Eggroll.step`. Weights are the seeded initialisation; tokens are synthetic.
+
+Printed: one JSON line. `value` = members * tokens * steps / wall time of the timed steps (inputs
+resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (c_fc GEMM with the
+rank-1 + relu^2 epilogue, then the c_proj GEMM with the rank-1 + residual epilogue): algorithmic
+FLOPs per launch pair / its mean duration, timed live with HIP events on the launch stream.
+`cpu_baseline` times the CPU oracle (oracle/model_ref.py, float32) on a bounded sample of the same
+workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+PEAK_BF16 = 2.5e15  # dense bf16 MFMA, MI355X
+
+
+def mlp_flops(rows, d=512, f=2048):
+    """Algorithmic FLOPs of one fused-MLP launch pair over `rows` member-token rows: both GEMMs
+    (2 d f each) plus the two rank-1 epilogues (2 f + 2 d), per row."""
+    return rows * (4 * d * f + 2 * (d + f))
+
+
+def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 1024, 1024, 2048) * 2):
+    """Algorithmic FLOPs of the population forward per step (fp32-accurate head counted once)."""
+    per_tok = 0
+    for w in windows[:layers]:
+        keys = sum(min(t, w) + 1 for t in range(T)) / T
+        per_tok += 2 * d * 3 * d + 2 * d * d + 4 * d * f + 4 * 64 * 8 * keys
+    per_tok += 2 * d * V
+    return members * T * per_tok
+
+
+def cpu_baseline(seconds_budget=20.0):
+    from noise_amd.synthetic import antithetic, pair_noise, sequence
+    from oracle import model_ref as R
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    params = R.init_params(0)
+    idx, targets = sequence(2048, seed=0)
+    noise, sign = antithetic(pair_noise(1, seed=1), 1e-3)
+    t0 = time.perf_counter()
+    R.population_loss(params, noise, sign, idx, targets, policy='fp32')  # warmup
+    first = time.perf_counter() - t0
+    reps = max(1, min(5, int(seconds_budget / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        R.population_loss(params, noise, sign, idx, targets, policy='fp32')
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {'value': 2 * 2048 / med, 'unit': 'member-tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': f'oracle population_loss fp32 on CPU, 2 members (1 antithetic pair) x 2048 tokens, '
+                      f'median of {reps} after 1 warmup'}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=3)
+    ap.add_argument('--warmup', type=int, default=1)
+    ap.add_argument('--members', type=int, default=3072)
+    ap.add_argument('--tokens', type=int, default=2048)
+    ap.add_argument('--chunk', type=int, default=256, help='pairs per batched forward')
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
+              'Run with --gpus 1.', file=sys.stderr)
+        sys.exit(2)
+
+    import noise_amd
+    from noise_amd.synthetic import sequence
+
+    device = torch.device('cuda', 0)
+    torch.cuda.set_device(device)
+    pairs = args.members // 2
+    T = args.tokens
+    model = noise_amd.make_model(device, 0)
+    opt = noise_amd.AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    es = noise_amd.Eggroll(model, pairs, sigma=1e-3, chunk=args.chunk)
+    idx, targets = sequence(T, seed=0)
+    x, y = idx[None].to(device), targets[None].to(device)
+
+    for s in range(args.warmup):
+        es.step(x, y, opt, s + 1)
+    es.engine.probe = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    losses = []
+    for s in range(args.steps):
+        losses.append(es.step(x, y, opt, args.warmup + s + 1))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    probe, es.engine.probe = es.engine.probe, None
+
+    fc_ms = sum(a.elapsed_time(b) for a, b, _, _ in probe) / len(probe)
+    mp_ms = sum(b.elapsed_time(c) for _, b, c, _ in probe) / len(probe)
+    rows = probe[0][3]
+    flops = mlp_flops(rows)
+    pair_s = (fc_ms + mp_ms) / 1e3
+    achieved = flops / pair_s / 1e12
+    members = 2 * pairs
+    value = members * T * args.steps / elapsed
+    out = {
+        'metric': 'perturbed member-tokens/sec on 1 GPU; fused-MLP MFMA % of bf16 peak',
+        'value': value,
+        'unit': 'member-tokens/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': elapsed / args.steps * 1e3,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'bf16',
+        'data': 'synthetic (Zipf(1.1) tokens, seed-0 weights, N(0,1) noise buffer)',
+        'config': {'workload': 'config 4: full EGGROLL population step (forward + fitness + rank-1 gradient + AdamW)',
+                   'members': members, 'pairs': pairs, 'seq_len': T, 'sigma': 1e-3, 'model': '37.7M (8x512, V=4096)',
+                   'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
+        'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
+                     'frac': achieved * 1e12 / PEAK_BF16, 'traffic': None,
+                     'kernel': 'fused relu^2 MLP: lowrank_gemm<RELU2> (c_fc) + lowrank_gemm<ADD_F32,K=2048> (c_proj)',
+                     'flops_per_launch': flops, 'rows_per_launch': rows,
+                     'launch_ms': {'c_fc': fc_ms, 'c_proj': mp_ms}},
+        'step_tflops': step_flops(members, T) / (elapsed / args.steps) / 1e12,
+        'mean_loss': losses[-1],
+    }
+    if not args.no_cpu:
+        out['cpu_baseline'] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,197 @@
+/* libnoise_amd -- C ABI of the MI355X (gfx950) kernels behind Noise's population-perturbed
+ * forward pass and its EGGROLL update.
+ *
+ * Conventions shared by every entry point:
+ *  - all pointers are device pointers owned by the caller; the library never frees them;
+ *  - bf16 tensors are passed as uint16_t bit patterns, row-major, with explicit row strides
+ *    (in elements);
+ *  - rows of a population activation are member-major: row = member * T + token;
+ *  - `stream` is a hipStream_t passed as an opaque pointer (NULL = the default stream);
+ *    launches are asynchronous and nothing synchronises the device;
+ *  - the return value is a status (NOISE_OK on success); noise_last_error() describes the
+ *    most recent failure of the calling thread.
+ *
+ * A member p evaluates the weights W + sign[p] * a_p b_p^T of every matrix (a_p in R^out,
+ * b_p in R^in; train/val/eggroll.py:56-58), so x (W + s a b^T)^T = x W^T + s (x . b) a^T.
+ * The dot products u = x . b are produced by the kernel that writes x (a norm, the attention
+ * or the relu^2 epilogue) and consumed by the epilogue of the GEMM that reads x. Perturbation
+ * vectors of member p live at row (p >> member_shift) of their arrays: shift 0 for one row per
+ * member, 1 for one row per antithetic pair.
+ */
+#ifndef NOISE_AMD_H
+#define NOISE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NOISE_OK 0
+#define NOISE_EINVAL 1     /* shape / argument error (Python: ValueError) */
+#define NOISE_EHIP 2       /* HIP runtime error (Python: RuntimeError) */
+#define NOISE_ENONFINITE 3 /* non-finite value (Python: FloatingPointError) */
+
+const char* noise_last_error(void);
+int noise_abi_version(void);
+
+/* ---- rank-1 perturbation of a GEMM's output columns ---------------------------------- */
+typedef struct {
+  const float* sign;    /* [members] +-sigma; NULL = unperturbed (no rank-1 term) */
+  int rows_per_member;  /* T: row r belongs to member r / T */
+  int member_shift;     /* noise row of member p = p >> member_shift */
+  int seg_cols;         /* output columns per segment (a multiple of 256) */
+  int nseg;             /* 1..3 segments side by side (e.g. q | k | v) */
+  int u_parts;          /* u of a row = sum of u_parts consecutive floats */
+  int64_t lda;          /* row stride of every a[s] (floats) */
+  int64_t ldu;          /* row stride of every u[s] (floats) */
+  const float* a[3];    /* segment s: a [noise rows, seg_cols] */
+  const float* u[3];    /* segment s: u [M, ...], the dots x . b of the GEMM input rows */
+} noise_rank1_t;
+
+#define NOISE_EPI_BF16 0       /* C (bf16)  = A W^T + rank-1 */
+#define NOISE_EPI_F32 1        /* C (fp32)  = A W^T + rank-1 */
+#define NOISE_EPI_ADD_F32 2    /* C (fp32) += A W^T + rank-1          (residual add) */
+#define NOISE_EPI_RELU2_BF16 3 /* C (bf16)  = relu(A W^T + rank-1)^2, and
+                                  u_next[r, c / 128] = sum over that 128-column group of
+                                  bf16(C[r, c]) * b_next[member(r), c] */
+
+/* x W^T + sign (x . b) a^T for A [M, K] bf16 and W [N, K] bf16 (the bf16 weight copy).
+ * Replaces `lowrank` (train/val/eggroll.py:56-58) together with the ops fused around it:
+ * the residual adds of eggroll.py:92-93 (NOISE_EPI_ADD_F32) and the relu^2 of eggroll.py:93
+ * (NOISE_EPI_RELU2_BF16). Requires N % 256 == 0 and K % 64 == 0. */
+int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
+                       int M, int N, int K, const noise_rank1_t* r1, int mode,
+                       void* C, int64_t ldc, const float* b_next, int64_t ld_bnext,
+                       float* u_next, int64_t ld_unext, void* stream);
+
+/* ---- embedding ------------------------------------------------------------------------ */
+/* x0[p*T + t] = norm(W[i] + sign[p] a_p[i] b_p) with i = idx[p*idx_stride + t] (idx_stride 0:
+ * one sequence shared by every member), fp32 [members*T, d]; x (if not NULL) receives a copy.
+ * An id outside [0, vocab) yields a NaN row. Replaces `lowrank_embed` + `norm` (train/val/eggroll.py:61-63, 74;
+ * utils/model.py:46-47). d must be 512. */
+int noise_embed_norm(const float* table, int64_t ld_table, int vocab, int d,
+                     const int64_t* idx, int64_t idx_stride, int T, int members, const float* sign,
+                     const float* a, int64_t lda, const float* b, int64_t ldb, int member_shift,
+                     float* x0, float* x, void* stream);
+
+/* ---- residual mixing + RMSNorm + the dots of the consuming GEMMs ------------------------ */
+typedef struct {
+  float* x;             /* [M, 512] fp32 stream (updated in place when mixing) */
+  const float* x0;      /* [M, 512] fp32 normalised embedding; NULL = no mixing */
+  int M, T, member_shift;
+  const float* sign;    /* [members]; NULL = unperturbed */
+  const float* resid;   /* device scalar lambda_r[i] (resid_lambdas + i) */
+  const float* mix;     /* device scalar lambda_0[i] (x0_lambdas + i) */
+  const float* eps_resid; /* eps of resid_lambdas at layer i: eps_resid[(p>>shift)*ld_eps] */
+  const float* eps_mix;
+  int64_t ld_eps;
+  uint16_t* h;          /* out: bf16(norm(x)) [M, 512] */
+  int nb;               /* 0..3 vectors b to dot with bf16(h) */
+  const float* b[3];    /* b[j]: [noise rows, 512] */
+  int64_t ldb;
+  float* u;             /* out: u[r * ldu + j] = bf16(h_r) . b_j */
+  int64_t ldu;
+  const float* gate_w;  /* ve_gate W [8, 32] fp32, NULL = no gate */
+  const float* gate_a;  /* [noise rows, 8] */
+  const float* gate_b;  /* [noise rows, 32] */
+  int64_t ld_gate_a, ld_gate_b;
+  float* gate;          /* out: 2 sigmoid(h[:32] (Wg + s a b^T)^T) [M, 8] */
+} noise_mixnorm_t;
+
+/* Replaces the per-layer mixing (train/val/eggroll.py:77-79), `norm` (eggroll.py:81, 93, 94),
+ * the x @ b halves of `lowrank` (eggroll.py:58) and the value-embedding gate
+ * (eggroll.py:88; utils/model.py:89). */
+int noise_mix_norm(const noise_mixnorm_t* args, void* stream);
+
+/* ---- rotary + q/k RMSNorm + value embedding --------------------------------------------- */
+typedef struct {
+  const float* qkv;     /* [M, 1536] fp32: q | k | v from noise_lowrank_gemm */
+  uint16_t* out;        /* [M, 1536] bf16: norm(rot(q)) | norm(rot(k)) | v + gate * ve */
+  int M, T, member_shift;
+  const float* cos;     /* [T, 32] fp32 holding the bf16 rotary table values */
+  const float* sin;
+  const float* gate;    /* [M, 8] or NULL (no value embedding at this layer) */
+  const float* ve_table; /* [vocab, 512] fp32 */
+  const int64_t* idx;   /* token of row p*T + t: idx[p * idx_stride + t] */
+  int64_t idx_stride;
+  int vocab;
+  const float* sign;
+  const float* ve_a;    /* [noise rows, vocab] */
+  const float* ve_b;    /* [noise rows, 512] */
+  int64_t ld_ve_a, ld_ve_b;
+} noise_rope_t;
+
+/* Replaces apply_rotary_emb + norm on q, k (utils/model.py:55-58; eggroll.py:90) and
+ * v + gate * lowrank_embed(value_embeds) (eggroll.py:85-89). */
+int noise_rope_norm_ve(const noise_rope_t* args, void* stream);
+
+/* ---- windowed causal attention ---------------------------------------------------------- */
+typedef struct {
+  const uint16_t* qkv;  /* [M, ldqkv] bf16, q at column 0, k at 512, v at 1024 (head h at h*64) */
+  int64_t ldqkv;
+  uint16_t* y;          /* out [M, 512] bf16 */
+  int members, T, heads, window;
+  float scale;          /* 1/sqrt(64) */
+  const float* b_proj;  /* c_proj b [noise rows, 512] or NULL: u_proj[r*8 + h] = y_h . b_h */
+  int64_t ld_b_proj;
+  int member_shift;
+  float* u_proj;        /* [M, heads] */
+  float* moments;       /* NULL or [members, heads, 2, 64]: mean over t of y and y^2 */
+  float* scratch;       /* moments partials: [members*heads*ceil(T/128), 2, 64] floats */
+} noise_attention_t;
+
+/* Softmax(q k^T * scale) v over keys s - window .. s (utils/model.py:17-31; eggroll.py:91),
+ * plus the per-(member, head) first and second moments of the output over tokens. */
+int noise_window_attention(const noise_attention_t* args, void* stream);
+
+/* ---- RMSNorm'd hidden -> perturbed fp32 head -> soft-cap -> cross-entropy --------------- */
+typedef struct {
+  const uint16_t* h;     /* [M, 512] bf16 norm(x) */
+  const uint16_t* w_hi;  /* [V, 512] bf16(W) */
+  const uint16_t* w_lo;  /* [V, 512] bf16(W - bf16(W)): W ~ w_hi + w_lo to ~2^-17 */
+  int M, V, T, member_shift;
+  const float* sign;
+  const float* a;        /* [noise rows, V] */
+  int64_t lda;
+  const float* u;        /* [M] h . b */
+  const int64_t* targets; /* target of row p*T + t: targets[p * targets_stride + t] */
+  int64_t targets_stride;
+  float* ce;             /* out [M] per-token cross-entropy */
+} noise_head_t;
+
+/* logits = h (W + s a b^T)^T in fp32 accuracy, 15 tanh(logits / 15), cross-entropy against
+ * the target (train/val/eggroll.py:94-102; utils/model.py:203-209). V % 256 == 0. */
+int noise_head_ce(const noise_head_t* args, void* stream);
+
+/* out[p] = mean over t of ce[p*T + t] (eggroll.py:102). */
+int noise_member_mean(const float* ce, int members, int T, float* out, void* stream);
+
+/* ---- EGGROLL update -------------------------------------------------------------------- */
+/* f_j = L[2j+1] - L[2j], f /= (std(f) + 1e-8) (unbiased std), weight[i] = sum_{j = i mod pairs}
+ * f_j (train/val/eggroll.py:151-154). n_losses even; weight [pairs]. Raises NOISE_ENONFINITE
+ * through *status_out (device int) if a loss is not finite. */
+int noise_fitness(const float* losses, int n_losses, int pairs, float* weight,
+                  int* status_out, void* stream);
+
+/* G[o, i] (+)= scale * sum_j w[j] a_j[o] b_j[i], with a_j = a_base + a_off[j],
+ * b_j = b_base + b_off[j] (train/val/eggroll.py:155-163 with scale = -1/n; a vector
+ * parameter is out = L, in = 1 with b_j = 1 when b_base is NULL). */
+int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t* a_off,
+                      const float* b_base, const int64_t* b_off, int out, int in, float scale,
+                      int accumulate, float* G, void* stream);
+
+/* AdamW over a flat fp32 buffer (torch.optim.AdamW semantics, eggroll.py:164-167, 205):
+ * param *= 1 - lr wd; m = lerp(m, g, 1 - b1); v = b2 v + (1 - b2) g^2;
+ * param -= lr / (1 - b1^t) * m / (sqrt(v) / sqrt(1 - b2^t) + eps). */
+int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                void* stream);
+
+/* bf16 copy of an fp32 buffer (hi), and optionally the residual bf16(x - hi) (lo). */
+int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,108 @@
+"""ctypes binding of libnoise_amd.so (declarations in include/noise_amd.h).
+
+The library is loaded from this package directory only. There is no fallback: if the library is
+missing or fails to load, every entry point raises, so the population forward never silently runs
+anywhere but the HIP kernels.
+"""
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / 'libnoise_amd.so'
+
+NOISE_OK, NOISE_EINVAL, NOISE_EHIP, NOISE_ENONFINITE = 0, 1, 2, 3
+EPI_BF16, EPI_F32, EPI_ADD_F32, EPI_RELU2_BF16 = 0, 1, 2, 3
+
+P = C.c_void_p
+I64 = C.c_int64
+INT = C.c_int
+F32 = C.c_float
+
+
+class Rank1(C.Structure):
+    _fields_ = [('sign', P), ('rows_per_member', INT), ('member_shift', INT), ('seg_cols', INT),
+                ('nseg', INT), ('u_parts', INT), ('lda', I64), ('ldu', I64),
+                ('a', P * 3), ('u', P * 3)]
+
+
+class MixNorm(C.Structure):
+    _fields_ = [('x', P), ('x0', P), ('M', INT), ('T', INT), ('member_shift', INT), ('sign', P),
+                ('resid', P), ('mix', P), ('eps_resid', P), ('eps_mix', P), ('ld_eps', I64),
+                ('h', P), ('nb', INT), ('b', P * 3), ('ldb', I64), ('u', P), ('ldu', I64),
+                ('gate_w', P), ('gate_a', P), ('gate_b', P), ('ld_gate_a', I64), ('ld_gate_b', I64),
+                ('gate', P)]
+
+
+class Rope(C.Structure):
+    _fields_ = [('qkv', P), ('out', P), ('M', INT), ('T', INT), ('member_shift', INT), ('cos', P),
+                ('sin', P), ('gate', P), ('ve_table', P), ('idx', P), ('idx_stride', I64), ('vocab', INT), ('sign', P),
+                ('ve_a', P), ('ve_b', P), ('ld_ve_a', I64), ('ld_ve_b', I64)]
+
+
+class Attention(C.Structure):
+    _fields_ = [('qkv', P), ('ldqkv', I64), ('y', P), ('members', INT), ('T', INT), ('heads', INT),
+                ('window', INT), ('scale', F32), ('b_proj', P), ('ld_b_proj', I64), ('member_shift', INT),
+                ('u_proj', P), ('moments', P), ('scratch', P)]
+
+
+class Head(C.Structure):
+    _fields_ = [('h', P), ('w_hi', P), ('w_lo', P), ('M', INT), ('V', INT), ('T', INT),
+                ('member_shift', INT), ('sign', P), ('a', P), ('lda', I64), ('u', P), ('targets', P),
+                ('targets_stride', I64), ('ce', P)]
+
+
+# name -> (restype, argtypes); every function returns an int status.
+SIGNATURES = {
+    'noise_abi_version': [],
+    'noise_lowrank_gemm': [P, I64, P, I64, INT, INT, INT, C.POINTER(Rank1), INT, P, I64, P, I64, P, I64, P],
+    'noise_embed_norm': [P, I64, INT, INT, P, I64, INT, INT, P, P, I64, P, I64, INT, P, P, P],
+    'noise_mix_norm': [C.POINTER(MixNorm), P],
+    'noise_rope_norm_ve': [C.POINTER(Rope), P],
+    'noise_window_attention': [C.POINTER(Attention), P],
+    'noise_head_ce': [C.POINTER(Head), P],
+    'noise_member_mean': [P, INT, INT, P, P],
+    'noise_fitness': [P, INT, INT, P, P, P],
+    'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
+    'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],
+    'noise_cast_bf16': [P, I64, P, P, P],
+}
+
+_lib = None
+
+
+def load():
+    """Load (once) and return the CDLL; raises ImportError if the library is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(f'{LIB_PATH} is not built; run `python -m noise_amd.build`')
+    lib = C.CDLL(str(LIB_PATH))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = INT
+    lib.noise_last_error.argtypes = []
+    lib.noise_last_error.restype = C.c_char_p
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return ['noise_last_error', *SIGNATURES]
+
+
+def check(status, what=''):
+    if status == NOISE_OK:
+        return
+    msg = load().noise_last_error().decode(errors='replace')
+    if what:
+        msg = f'{what}: {msg}'
+    if status == NOISE_EINVAL:
+        raise ValueError(msg)
+    if status == NOISE_ENONFINITE:
+        raise FloatingPointError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name, *args):
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,178 @@
+// EGGROLL update kernels: fitness -> rank-1 gradient rebuild -> AdamW.
+//
+// * fitness (train/val/eggroll.py:151-154): f_j = L[2j+1] - L[2j], f /= unbiased std(f) + 1e-8,
+//   weight[i] = sum over j with j % pairs == i of f_j. One workgroup, fixed reduction order, so
+//   every process that holds the same losses computes bit-identical weights.
+// * es_gradient (eggroll.py:155-163): G = scale * sum_j w_j a_j b_j^T, an fp32 GEMM whose
+//   reduction dimension is the pair index; a_j and b_j are addressed through per-pair offsets, so
+//   the same kernel reads materialised [pairs, out] noise or slices of one shared noise buffer.
+// * adamw (eggroll.py:164-167 with the torch.optim.AdamW of eggroll.py:205): one pass over a flat
+//   fp32 parameter buffer.
+#include "common.h"
+
+namespace {
+
+constexpr int FT = 1024;
+
+NOISE_DEV float block_sum(float v, float* red) {
+  const int tid = threadIdx.x;
+  red[tid] = v;
+  __syncthreads();
+  for (int o = FT / 2; o > 0; o >>= 1) {
+    if (tid < o) red[tid] += red[tid + o];
+    __syncthreads();
+  }
+  const float r = red[0];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(FT) void fitness_kernel(const float* __restrict__ losses, int n, int pairs,
+                                                     float* __restrict__ weight, int* status) {
+  __shared__ float red[FT];
+  const int tid = threadIdx.x;
+  float s = 0.f, bad = 0.f;
+  for (int j = tid; j < n; j += FT) {
+    const float lp = losses[2 * j], lm = losses[2 * j + 1];
+    if (!isfinite(lp) || !isfinite(lm)) bad = 1.f;
+    s += lm - lp;
+  }
+  const float mean = block_sum(s, red) / (float)n;
+  const float nbad = block_sum(bad, red);
+  float q = 0.f;
+  for (int j = tid; j < n; j += FT) {
+    const float d = (losses[2 * j + 1] - losses[2 * j]) - mean;
+    q += d * d;
+  }
+  const float var = block_sum(q, red) / (float)(n - 1);
+  const float inv = 1.0f / (sqrtf(var) + 1e-8f);
+  for (int i = tid; i < pairs; i += FT) {
+    float acc = 0.f;
+    for (int j = i; j < n; j += pairs) acc += (losses[2 * j + 1] - losses[2 * j]) * inv;
+    weight[i] = acc;
+  }
+  if (tid == 0 && status) *status = nbad > 0.f ? NOISE_ENONFINITE : NOISE_OK;
+}
+
+// 64 x 64 output tile per workgroup of 256 threads, 4 x 4 outputs per thread, 16 pairs per stage.
+__global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restrict__ w, int n,
+                                                          const float* __restrict__ a_base,
+                                                          const int64_t* __restrict__ a_off,
+                                                          const float* __restrict__ b_base,
+                                                          const int64_t* __restrict__ b_off, int out,
+                                                          int in, float scale, int accumulate,
+                                                          float* __restrict__ G) {
+  __shared__ float As[16][64];
+  __shared__ float Bs[16][64];
+  const int tid = threadIdx.x;
+  const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
+  const int tx = tid & 15, ty = tid >> 4;
+  float acc[4][4] = {};
+  const int lj = tid >> 4, lc = (tid & 15) * 4;
+  for (int j0 = 0; j0 < n; j0 += 16) {
+    const int j = j0 + lj;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int o = o0 + lc + e, i = i0 + lc + e;
+      float av = 0.f, bv = 0.f;
+      if (j < n) {
+        if (o < out) av = w[j] * a_base[a_off[j] + o];
+        if (i < in) bv = b_base ? b_base[b_off[j] + i] : 1.0f;
+      }
+      As[lj][lc + e] = av;
+      Bs[lj][lc + e] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      float ar[4], br[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ar[r] = As[jj][ty * 4 + r];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) br[c] = Bs[jj][tx * 4 + c];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] += ar[r] * br[c];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int o = o0 + ty * 4 + r;
+    if (o >= out) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = i0 + tx * 4 + c;
+      if (i >= in) continue;
+      float* dst = G + (int64_t)o * in + i;
+      const float v = scale * acc[r][c];
+      *dst = accumulate ? *dst + v : v;
+    }
+  }
+}
+
+NOISE_DEV float lerp_torch(float start, float end, float weight) {
+  const float diff = end - start;
+  return weight < 0.5f ? start + weight * diff : end - diff * (1.0f - weight);
+}
+
+__global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ param, const float* __restrict__ grad,
+                                                    float* __restrict__ m, float* __restrict__ v, int64_t n,
+                                                    float decay, float w1, float beta2, float w2,
+                                                    float step_size, float bc2_sqrt, float eps) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const float g = grad[i];
+    float p = param[i] * decay;
+    const float mi = lerp_torch(m[i], g, w1);
+    const float vi = v[i] * beta2 + w2 * g * g;
+    const float denom = sqrtf(vi) / bc2_sqrt + eps;
+    p = p - step_size * (mi / denom);
+    param[i] = p;
+    m[i] = mi;
+    v[i] = vi;
+  }
+}
+
+}  // namespace
+
+extern "C" int noise_fitness(const float* losses, int n_losses, int pairs, float* weight, int* status_out,
+                             void* stream) {
+  NOISE_REQUIRE(losses && weight && pairs > 0, "fitness: bad arguments");
+  NOISE_REQUIRE(n_losses >= 2 && n_losses % 2 == 0, "fitness: n_losses=%d must be even and >= 2", n_losses);
+  fitness_kernel<<<1, FT, 0, (hipStream_t)stream>>>(losses, n_losses / 2, pairs, weight, status_out);
+  return noise::check_launch("fitness");
+}
+
+extern "C" int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t* a_off,
+                                 const float* b_base, const int64_t* b_off, int out, int in, float scale,
+                                 int accumulate, float* G, void* stream) {
+  NOISE_REQUIRE(w && a_base && a_off && G && n >= 0 && out > 0 && in > 0, "es_gradient: bad arguments");
+  NOISE_REQUIRE(!b_base || b_off, "es_gradient: b_base needs b_off");
+  NOISE_REQUIRE(b_base || in == 1, "es_gradient: a vector parameter (no b) needs in == 1");
+  dim3 grid((in + 63) / 64, (out + 63) / 64);
+  NOISE_REQUIRE(grid.y < 65536, "es_gradient: out=%d too large", out);
+  es_gradient_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(w, n, a_base, a_off, b_base, b_off, out, in, scale,
+                                                            accumulate, G);
+  return noise::check_launch("es_gradient");
+}
+
+extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                           float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                           void* stream) {
+  NOISE_REQUIRE(param && grad && exp_avg && exp_avg_sq && n >= 0, "adamw: bad arguments");
+  NOISE_REQUIRE(step >= 1, "adamw: step=%d must count from 1", step);
+  if (n == 0) return NOISE_OK;
+  const double bias1 = 1.0 - __builtin_pow((double)beta1, step);
+  const double bias2 = 1.0 - __builtin_pow((double)beta2, step);
+  const float step_size = (float)(lr / bias1);
+  const float bc2_sqrt = (float)__builtin_sqrt(bias2);
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  adamw_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(param, grad, exp_avg, exp_avg_sq, n,
+                                                              1.0f - lr * weight_decay, 1.0f - beta1, beta2,
+                                                              1.0f - beta2, step_size, bc2_sqrt, eps);
+  return noise::check_launch("adamw");
+}

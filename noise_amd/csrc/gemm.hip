@@ -1,0 +1,208 @@
+// Perturbed GEMM of the population forward: C = A W^T + sign (A . b) a^T with fused epilogues.
+//
+// Reference semantics: `lowrank` (train/val/eggroll.py:56-58) for every block matrix, with the
+// residual adds (eggroll.py:92-93) and relu^2 (eggroll.py:93; utils/model.py:107) folded into the
+// epilogue. The dot products u = A . b arrive precomputed per row (written by the producer of A),
+// so the rank-1 term costs one FMA per output element.
+//
+// Tiling for gfx950: a 256x256 output tile per workgroup of 4 waves (2 x 2), each wave owning a
+// 128x128 sub-tile as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane,
+// one wave per SIMD). K advances 64 at a time through a double-buffered LDS stage (2 x 72 KB,
+// rows padded to 144 B so the 16-byte fragment reads are bank-conflict free); the next stage's
+// global loads are issued before the current stage's MFMAs. Workgroups are renumbered so that
+// each XCD walks a contiguous run of tiles (neighbouring N tiles share the A rows in that XCD's L2).
+#include "mma_tile.h"
+
+namespace {
+
+constexpr int BM = noise::TILE, BN = noise::TILE, BK = noise::TBK;
+
+struct GemmArgs {
+  const uint16_t* A;
+  int64_t lda;
+  const uint16_t* W;
+  int64_t ldw;
+  int M, N, K;
+  noise_rank1_t r1;
+  void* C;
+  int64_t ldc;
+  const float* b_next;
+  int64_t ld_bnext;
+  float* u_next;
+  int64_t ld_unext;
+};
+
+// LONGK marks the K >= 1024 instantiation (the MLP down-projection, K = 2048) so that it is a
+// kernel of its own in profiles; the code is the same.
+template <int MODE, bool LONGK>
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+lowrank_gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
+  __shared__ float su_s[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ntn = g.N / BN;
+  const int ntiles = gridDim.x;
+  int bid = blockIdx.x;
+  if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);  // XCD-contiguous runs
+  const int m0 = (bid / ntn) * BM, n0 = (bid % ntn) * BN;
+  const int T = g.r1.rows_per_member;
+  const bool perturbed = g.r1.sign != nullptr;
+
+  // Per-row sign * u, staged once per tile (visible after the main loop's first barrier).
+  const int seg = perturbed ? n0 / g.r1.seg_cols : 0;
+  {
+    const int row = m0 + tid;
+    float su = 0.f;
+    if (perturbed && row < g.M) {
+      const float* up = g.r1.u[seg] + (int64_t)row * g.r1.ldu;
+      float u = 0.f;
+      for (int j = 0; j < g.r1.u_parts; ++j) u += up[j];
+      su = g.r1.sign[row / T] * u;
+    }
+    su_s[tid] = su;
+  }
+
+  floatx16 acc[4][4];
+  noise::zero_acc(acc);
+  noise::mma_tile_256(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
+                      smem, acc);
+
+  // ---- epilogue ----
+  const int last_row = (m0 + BM < g.M ? m0 + BM : g.M) - 1;
+  const bool uniform = (m0 / T) == (last_row / T);
+  const int p0 = m0 / T;
+  const int shift = g.r1.member_shift;
+  const float* aseg = perturbed ? g.r1.a[seg] : nullptr;
+  const int seg_base = perturbed ? seg * g.r1.seg_cols : 0;
+  const int colbase = n0 + wn * 128 + (lane & 31);
+
+  float a_val[4] = {0.f, 0.f, 0.f, 0.f}, bn_val[4] = {0.f, 0.f, 0.f, 0.f};
+  if (uniform) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const int col = colbase + ni * 32;
+      if (perturbed) a_val[ni] = aseg[(int64_t)(p0 >> shift) * g.r1.lda + (col - seg_base)];
+      if (MODE == NOISE_EPI_RELU2_BF16 && g.b_next)
+        bn_val[ni] = g.b_next[(int64_t)(p0 >> shift) * g.ld_bnext + col];
+    }
+  }
+
+  float pd[64];
+  if (MODE == NOISE_EPI_RELU2_BF16) {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) pd[i] = 0.f;
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+      const int row = m0 + rl;
+      if (row >= g.M) continue;
+      const float su = su_s[rl];
+      const int pn = (row / T) >> shift;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const int col = colbase + ni * 32;
+        float av = a_val[ni];
+        if (!uniform && perturbed) av = aseg[(int64_t)pn * g.r1.lda + (col - seg_base)];
+        const float v = acc[mi][ni][j] + su * av;
+        const int64_t off = (int64_t)row * g.ldc + col;
+        if (MODE == NOISE_EPI_BF16) {
+          reinterpret_cast<uint16_t*>(g.C)[off] = f2bf(v);
+        } else if (MODE == NOISE_EPI_F32) {
+          reinterpret_cast<float*>(g.C)[off] = v;
+        } else if (MODE == NOISE_EPI_ADD_F32) {
+          reinterpret_cast<float*>(g.C)[off] += v;
+        } else {
+          const float r = v > 0.f ? v * v : 0.f;
+          const uint16_t hb = f2bf(r);
+          reinterpret_cast<uint16_t*>(g.C)[off] = hb;
+          float bn = bn_val[ni];
+          if (!uniform && g.b_next) bn = g.b_next[(int64_t)pn * g.ld_bnext + col];
+          pd[mi * 16 + j] += bf2f(hb) * bn;
+        }
+      }
+    }
+  }
+
+  if (MODE == NOISE_EPI_RELU2_BF16 && g.u_next) {
+    halfwave_transpose_sum(pd, lane);
+    const int part = (n0 + wn * 128) / 128;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = 2 * (lane & 31) + e;
+      const int mi = i >> 4, j = i & 15;
+      const int row = m0 + wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+      if (row < g.M) g.u_next[(int64_t)row * g.ld_unext + part] = pd[e];
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
+                                  int M, int N, int K, const noise_rank1_t* r1, int mode, void* C,
+                                  int64_t ldc, const float* b_next, int64_t ld_bnext, float* u_next,
+                                  int64_t ld_unext, void* stream) {
+  NOISE_REQUIRE(A && W && C, "lowrank_gemm: null A, W or C");
+  NOISE_REQUIRE(M >= 0 && N > 0 && K > 0, "lowrank_gemm: bad sizes M=%d N=%d K=%d", M, N, K);
+  NOISE_REQUIRE(N % BN == 0, "lowrank_gemm: N=%d must be a multiple of %d", N, BN);
+  NOISE_REQUIRE(K % BK == 0, "lowrank_gemm: K=%d must be a multiple of %d", K, BK);
+  NOISE_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0,
+                "lowrank_gemm: lda=%lld ldw=%lld must be >= K and multiples of 8", (long long)lda,
+                (long long)ldw);
+  NOISE_REQUIRE(ldc >= N, "lowrank_gemm: ldc=%lld < N=%d", (long long)ldc, N);
+  NOISE_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0,
+                "lowrank_gemm: A and W must be 16-byte aligned");
+  NOISE_REQUIRE(mode >= NOISE_EPI_BF16 && mode <= NOISE_EPI_RELU2_BF16, "lowrank_gemm: bad mode %d", mode);
+  if (M == 0) return NOISE_OK;
+  GemmArgs g;
+  g.A = A; g.lda = lda; g.W = W; g.ldw = ldw; g.M = M; g.N = N; g.K = K;
+  g.C = C; g.ldc = ldc; g.b_next = b_next; g.ld_bnext = ld_bnext; g.u_next = u_next;
+  g.ld_unext = ld_unext;
+  noise_rank1_t none = {};
+  none.rows_per_member = M;
+  none.seg_cols = N;
+  none.nseg = 1;
+  none.u_parts = 1;
+  g.r1 = r1 ? *r1 : none;
+  if (g.r1.sign) {
+    NOISE_REQUIRE(g.r1.rows_per_member > 0, "lowrank_gemm: rows_per_member must be > 0");
+    NOISE_REQUIRE(g.r1.nseg >= 1 && g.r1.nseg <= 3 && g.r1.seg_cols % BN == 0 &&
+                      g.r1.seg_cols * g.r1.nseg == N,
+                  "lowrank_gemm: segments (%d x %d) must tile N=%d in multiples of %d", g.r1.nseg,
+                  g.r1.seg_cols, N, BN);
+    NOISE_REQUIRE(g.r1.u_parts >= 1 && g.r1.ldu >= g.r1.u_parts, "lowrank_gemm: bad u_parts/ldu");
+    NOISE_REQUIRE(g.r1.member_shift >= 0 && g.r1.member_shift < 31, "lowrank_gemm: bad member_shift");
+    for (int s = 0; s < g.r1.nseg; ++s)
+      NOISE_REQUIRE(g.r1.a[s] && g.r1.u[s], "lowrank_gemm: null a/u for segment %d", s);
+    NOISE_REQUIRE(g.r1.lda >= g.r1.seg_cols, "lowrank_gemm: r1.lda < seg_cols");
+  } else {
+    g.r1.rows_per_member = M;
+  }
+  NOISE_REQUIRE(!b_next == !u_next, "lowrank_gemm: b_next and u_next go together");
+  if (b_next) {
+    NOISE_REQUIRE(mode == NOISE_EPI_RELU2_BF16, "lowrank_gemm: b_next/u_next only apply to the relu2 epilogue");
+    NOISE_REQUIRE(ld_unext >= N / 128 && ld_bnext >= N, "lowrank_gemm: ld_unext/ld_bnext too small");
+  }
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / BN);
+  NOISE_REQUIRE(tiles < (1ll << 31), "lowrank_gemm: too many tiles");
+  hipStream_t st = (hipStream_t)stream;
+  const bool longk = K >= 1024;
+  switch (mode) {
+    case NOISE_EPI_BF16: lowrank_gemm_kernel<NOISE_EPI_BF16, false><<<(int)tiles, 256, 0, st>>>(g); break;
+    case NOISE_EPI_F32: lowrank_gemm_kernel<NOISE_EPI_F32, false><<<(int)tiles, 256, 0, st>>>(g); break;
+    case NOISE_EPI_ADD_F32:
+      if (longk)
+        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, true><<<(int)tiles, 256, 0, st>>>(g);
+      else
+        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, false><<<(int)tiles, 256, 0, st>>>(g);
+      break;
+    default: lowrank_gemm_kernel<NOISE_EPI_RELU2_BF16, false><<<(int)tiles, 256, 0, st>>>(g); break;
+  }
+  return noise::check_launch("lowrank_gemm");
+}

@@ -1,0 +1,113 @@
+// Perturbed fp32-accurate head + soft-cap + cross-entropy, logits never leave the chip.
+//
+// Reference semantics (train/val/eggroll.py:94-102; utils/model.py:203-209): for every member
+// row r, z = h_r (W + s a b^T)^T over the whole vocabulary, z' = 15 tanh(z / 15), and
+// ce_r = logsumexp(z') - z'[target]. The reference materialises [32, T, V] fp32 logits per slice;
+// here a workgroup owns 256 rows and sweeps the vocabulary in 256-column tiles, keeping only
+// per-row running sums of exp(z') (the soft-cap bounds z' to [-15, 15], so no running max is
+// needed in fp32) and the target's z'.
+//
+// fp32 weight accuracy on bf16 MFMA: W is split once into w_hi = bf16(W) and
+// w_lo = bf16(W - w_hi), and every tile accumulates h w_hi^T + h w_lo^T, which reproduces
+// h W^T to about 2^-17 relative (h itself is the bf16 GEMM input, as in the reference).
+#include "mma_tile.h"
+
+namespace {
+
+__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+head_ce_kernel(const noise_head_t g) {
+  __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
+  __shared__ float su_s[256];
+  __shared__ int tgt_s[256];
+  __shared__ float tz_s[256];
+  __shared__ float sum_s[2][256];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.x * 256;
+  const int T = g.T;
+  const bool perturbed = g.sign != nullptr;
+  {
+    const int row = m0 + tid;
+    float su = 0.f;
+    int tg = -1;
+    if (row < g.M) {
+      if (perturbed) su = g.sign[row / T] * g.u[row];
+      const int64_t t = g.targets[(int64_t)(row / T) * g.targets_stride + row % T];
+      tg = (t >= 0 && t < g.V) ? (int)t : -1;
+    }
+    su_s[tid] = su;
+    tgt_s[tid] = tg;
+    tz_s[tid] = __builtin_nanf("");  // stays NaN for a row whose target is out of range
+  }
+  const int last_row = (m0 + 256 < g.M ? m0 + 256 : g.M) - 1;
+  const bool uniform = (m0 / T) == (last_row / T);
+  const int64_t pn0 = (int64_t)(m0 / T) >> g.member_shift;
+
+  float rsum[2] = {0.f, 0.f};
+  const uint16_t* A = g.h + (int64_t)m0 * 512;
+  for (int n0 = 0; n0 < g.V; n0 += 256) {
+    floatx16 acc[4][4];
+    noise::zero_acc(acc);
+    noise::mma_tile_256(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc);
+    noise::mma_tile_256(A, 512, g.M - m0, g.w_lo + (int64_t)n0 * 512, 512, 512, smem, acc);
+    const int colbase = n0 + wn * 128 + (lane & 31);
+    float a_val[4] = {0.f, 0.f, 0.f, 0.f};
+    if (perturbed && uniform) {
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) a_val[ni] = g.a[pn0 * g.lda + colbase + ni * 32];
+    }
+    float es[64];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const float su = su_s[rl];
+        const int tg = tgt_s[rl];
+        float e = 0.f;
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          const int col = colbase + ni * 32;
+          float av = a_val[ni];
+          if (perturbed && !uniform) {
+            const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
+            av = g.a[((int64_t)(row / T) >> g.member_shift) * g.lda + col];
+          }
+          const float z = acc[mi][ni][j] + su * av;
+          const float c = 15.0f * tanhf(z * (1.0f / 15.0f));
+          e += expf(c);
+          if (col == tg) tz_s[rl] = c;
+        }
+        es[mi * 16 + j] = e;
+      }
+    halfwave_transpose_sum(es, lane);
+    rsum[0] += es[0];
+    rsum[1] += es[1];
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int i = 2 * (lane & 31) + e;
+    const int mi = i >> 4, j = i & 15;
+    const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+    sum_s[wn][rl] = rsum[e];
+  }
+  __syncthreads();
+  const int row = m0 + tid;
+  if (row < g.M) g.ce[row] = logf(sum_s[0][tid] + sum_s[1][tid]) - tz_s[tid];
+}
+
+}  // namespace
+
+extern "C" int noise_head_ce(const noise_head_t* args, void* stream) {
+  NOISE_REQUIRE(args && args->h && args->w_hi && args->w_lo && args->targets && args->ce,
+                "head_ce: null argument");
+  const noise_head_t& g = *args;
+  NOISE_REQUIRE(g.M >= 0 && g.T > 0 && g.V > 0 && g.V % 256 == 0, "head_ce: V=%d must be a positive multiple of 256", g.V);
+  NOISE_REQUIRE(!g.sign || (g.a && g.u && g.lda >= g.V), "head_ce: perturbation needs a [*, V] and u");
+  NOISE_REQUIRE(((uintptr_t)g.h % 16) == 0 && ((uintptr_t)g.w_hi % 16) == 0 && ((uintptr_t)g.w_lo % 16) == 0,
+                "head_ce: h and weights must be 16-byte aligned");
+  if (g.M == 0) return NOISE_OK;
+  head_ce_kernel<<<(g.M + 255) / 256, 256, 0, (hipStream_t)stream>>>(g);
+  return noise::check_launch("head_ce");
+}

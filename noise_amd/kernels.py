@@ -1,0 +1,192 @@
+"""Thin torch-tensor wrappers over the C ABI of libnoise_amd (include/noise_amd.h).
+
+Every wrapper checks devices, dtypes, shapes and strides on the host, then passes raw device
+pointers and the current HIP stream. Launches are asynchronous; no wrapper synchronises.
+"""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import Attention, Head, MixNorm, Rank1, Rope
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(*ts):
+    for t in ts:
+        if t is not None:
+            _need(t.is_cuda, 'libnoise_amd kernels take device tensors')
+
+
+def _rows(t, width, dtype, name):
+    """A 2-D (or row-strided) tensor whose rows are contiguous; returns its row stride."""
+    _need(t.dtype == dtype, f'{name}: expected {dtype}, got {t.dtype}')
+    _need(t.dim() == 2 and t.shape[1] >= width and t.stride(1) == 1,
+          f'{name}: expected rows of {width} contiguous elements, got shape {tuple(t.shape)} '
+          f'strides {t.stride()}')
+    return t.stride(0)
+
+
+class NoiseRows:
+    """Perturbation vectors of one parameter for a chunk of members: a [rows, out] and b [rows, in]
+    (row r of member p is p >> shift), or eps [rows, L] for a mixing-scalar vector."""
+
+    __slots__ = ('a', 'b', 'eps', 'shift')
+
+    def __init__(self, a=None, b=None, eps=None, shift=0):
+        self.a, self.b, self.eps, self.shift = a, b, eps, shift
+
+
+def rank1(sign, T, a_list, u_list, u_parts, ldu, shift):
+    r = Rank1()
+    if sign is None:
+        return None
+    r.sign = sign.data_ptr()
+    r.rows_per_member = T
+    r.member_shift = shift
+    r.nseg = len(a_list)
+    lda = a_list[0].stride(0)
+    for s, (a, u) in enumerate(zip(a_list, u_list)):
+        _need(a.dtype == torch.float32 and a.stride(1) == 1 and a.stride(0) == lda, 'rank1: a rows')
+        r.a[s] = a.data_ptr()
+        r.u[s] = u.data_ptr()
+    r.seg_cols = a_list[0].shape[1]
+    r.u_parts = u_parts
+    r.lda = lda
+    r.ldu = ldu
+    r._keep = (sign, tuple(a_list), tuple(u_list))  # the struct holds raw pointers into these
+    return r
+
+
+def lowrank_gemm(A, W, r1, mode, C_out, b_next=None, u_next=None):
+    """C = A W^T + rank-1 (see NOISE_EPI_*); A [M, K] bf16, W [N, K] bf16."""
+    _on_gpu(A, W, C_out, b_next, u_next)
+    M, K = A.shape
+    N = W.shape[0]
+    lda = _rows(A, K, torch.bfloat16, 'A')
+    ldw = _rows(W, K, torch.bfloat16, 'W')
+    cdt = torch.bfloat16 if mode in (_lib.EPI_BF16, _lib.EPI_RELU2_BF16) else torch.float32
+    ldc = _rows(C_out, N, cdt, 'C')
+    _need(C_out.shape[0] >= M, 'C has too few rows')
+    ldb = b_next.stride(0) if b_next is not None else 0
+    ldun = u_next.stride(0) if u_next is not None else 0
+    _lib.call('noise_lowrank_gemm', _ptr(A), lda, _ptr(W), ldw, M, N, K,
+              C.byref(r1) if r1 is not None else None, mode, _ptr(C_out), ldc,
+              _ptr(b_next), ldb, _ptr(u_next), ldun, _stream())
+
+
+def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0):
+    _on_gpu(table, idx, x0, x)
+    _need(idx.dtype == torch.int64, 'idx must be int64')
+    a = b = None
+    lda = ldb = 0
+    shift = 0
+    if sign is not None:
+        a, b, shift = nz.a, nz.b, nz.shift
+        lda, ldb = a.stride(0), b.stride(0)
+    _lib.call('noise_embed_norm', _ptr(table), table.stride(0), table.shape[0], table.shape[1], _ptr(idx),
+              idx_stride, T, members, _ptr(sign), _ptr(a), lda, _ptr(b), ldb, shift, _ptr(x0), _ptr(x),
+              _stream())
+
+
+def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,
+             bs=(), u=None, gate_w=None, gate_nz=None, gate=None):
+    g = MixNorm()
+    g.x, g.x0, g.M, g.T, g.member_shift = x.data_ptr(), _ptr(x0), x.shape[0], T, shift
+    g.sign = _ptr(sign)
+    g.resid, g.mix = _ptr(resid), _ptr(mix)
+    if x0 is not None and sign is not None:
+        g.eps_resid, g.eps_mix, g.ld_eps = eps_r.data_ptr(), eps_m.data_ptr(), eps_r.stride(0)
+    g.h = h.data_ptr()
+    g.nb = len(bs)
+    for j, b in enumerate(bs):
+        g.b[j] = b.data_ptr()
+    if bs:
+        g.ldb = bs[0].stride(0)
+        g.u, g.ldu = u.data_ptr(), u.stride(0) if u.dim() == 2 else 1
+    if gate_w is not None:
+        g.gate_w, g.gate = gate_w.data_ptr(), gate.data_ptr()
+        if sign is not None:
+            g.gate_a, g.gate_b = gate_nz.a.data_ptr(), gate_nz.b.data_ptr()
+            g.ld_gate_a, g.ld_gate_b = gate_nz.a.stride(0), gate_nz.b.stride(0)
+    _lib.call('noise_mix_norm', C.byref(g), _stream())
+
+
+def rope_norm_ve(qkv32, out16, T, cos, sin, sign=None, gate=None, ve_table=None, idx=None, ve_nz=None,
+                 idx_stride=0):
+    g = Rope()
+    g.qkv, g.out, g.M, g.T = qkv32.data_ptr(), out16.data_ptr(), qkv32.shape[0], T
+    g.cos, g.sin = cos.data_ptr(), sin.data_ptr()
+    if gate is not None:
+        g.gate, g.ve_table, g.idx, g.idx_stride, g.vocab = (gate.data_ptr(), ve_table.data_ptr(),
+                                                            idx.data_ptr(), idx_stride, ve_table.shape[0])
+        if sign is not None:
+            g.sign = sign.data_ptr()
+            g.member_shift = ve_nz.shift
+            g.ve_a, g.ve_b = ve_nz.a.data_ptr(), ve_nz.b.data_ptr()
+            g.ld_ve_a, g.ld_ve_b = ve_nz.a.stride(0), ve_nz.b.stride(0)
+    _lib.call('noise_rope_norm_ve', C.byref(g), _stream())
+
+
+def window_attention(qkv16, y, members, T, window, b_proj=None, shift=0, u_proj=None, moments=None,
+                     scratch=None):
+    g = Attention()
+    g.qkv, g.ldqkv, g.y = qkv16.data_ptr(), qkv16.stride(0), y.data_ptr()
+    g.members, g.T, g.heads, g.window, g.scale = members, T, 8, window, 0.125
+    if b_proj is not None:
+        g.b_proj, g.ld_b_proj, g.u_proj = b_proj.data_ptr(), b_proj.stride(0), u_proj.data_ptr()
+    g.member_shift = shift
+    g.moments, g.scratch = _ptr(moments), _ptr(scratch)
+    _lib.call('noise_window_attention', C.byref(g), _stream())
+
+
+def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_stride=0):
+    g = Head()
+    g.h, g.w_hi, g.w_lo = h.data_ptr(), w_hi.data_ptr(), w_lo.data_ptr()
+    g.M, g.V, g.T = h.shape[0], w_hi.shape[0], T
+    if sign is not None:
+        g.sign, g.a, g.lda, g.u, g.member_shift = (sign.data_ptr(), nz.a.data_ptr(), nz.a.stride(0),
+                                                   u.data_ptr(), nz.shift)
+    g.targets, g.targets_stride, g.ce = targets.data_ptr(), targets_stride, ce.data_ptr()
+    _lib.call('noise_head_ce', C.byref(g), _stream())
+
+
+def member_mean(ce, members, T, out):
+    _lib.call('noise_member_mean', _ptr(ce), members, T, _ptr(out), _stream())
+
+
+def cast_bf16(x, hi, lo=None):
+    _need(x.dtype == torch.float32 and x.is_contiguous() and hi.is_contiguous(), 'cast_bf16: contiguous fp32')
+    _need(hi.numel() == x.numel() and (lo is None or lo.numel() == x.numel()), 'cast_bf16: sizes')
+    _lib.call('noise_cast_bf16', _ptr(x), x.numel(), _ptr(hi), _ptr(lo), _stream())
+
+
+def fitness(losses, pairs, weight, status):
+    _on_gpu(losses, weight, status)
+    _need(losses.dtype == torch.float32 and losses.is_contiguous(), 'fitness: fp32 losses')
+    _lib.call('noise_fitness', _ptr(losses), losses.numel(), pairs, _ptr(weight), _ptr(status), _stream())
+
+
+def es_gradient(w, a_base, a_off, b_base, b_off, out, inn, scale, G, accumulate=False):
+    _on_gpu(w, a_base, a_off, G)
+    _lib.call('noise_es_gradient', _ptr(w), w.numel(), _ptr(a_base), _ptr(a_off), _ptr(b_base), _ptr(b_off),
+              out, inn, scale, int(accumulate), _ptr(G), _stream())
+
+
+def adamw(param, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, step):
+    for t in (param, grad, exp_avg, exp_avg_sq):
+        _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), 'adamw: contiguous fp32 device tensors')
+    _lib.call('noise_adamw', _ptr(param), _ptr(grad), _ptr(exp_avg), _ptr(exp_avg_sq), param.numel(), lr, beta1,
+              beta2, eps, weight_decay, step, _stream())

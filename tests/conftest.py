@@ -1,0 +1,42 @@
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+GOLDEN = ROOT / 'tests' / 'golden'
+
+
+def pytest_configure(config):
+    config.addinivalue_line('markers', 'gpu: needs a HIP device (MI355X) and the built libnoise_amd.so')
+
+
+@pytest.fixture(scope='session')
+def golden():
+    with np.load(GOLDEN / 'golden.npz', allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope='session')
+def golden_json():
+    import json
+    return json.loads((GOLDEN / 'golden.json').read_text())
+
+
+@pytest.fixture(scope='session')
+def init_params():
+    from oracle.model_ref import init_params as ip
+    return ip(0)
+
+
+@pytest.fixture(scope='session')
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip('no HIP device')
+    from noise_amd import _lib
+    _lib.load()  # fails loudly if the library is missing
+    return torch.device('cuda', 0)

@@ -1,0 +1,127 @@
+"""Writes the golden vectors of tests/golden/ from the reference implementation itself.
+
+Run once, in the build container only (the reference is not present on GPU machines):
+
+    python tests/golden/make_golden.py /root/reference
+
+The reference has no tests, fixtures or known-answer vectors, so nothing else pins its
+`population_loss` *as written* (train/val/eggroll.py:66-103), its seeded initialisation
+(train/val/eggroll.py:38-53 over utils/model.py:149-175) or its flex-attention window semantics
+(utils/model.py:17-31). This script imports those functions from the reference checkout, runs them
+eagerly on the CPU in float32 on seeded synthetic inputs, and stores inputs and outputs as plain
+arrays (`golden.npz`, loaded with allow_pickle=False) plus a JSON summary. Nothing of the
+reference's source is stored.
+"""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1]))
+
+from noise_amd.synthetic import antithetic, pair_noise, sequence  # noqa: E402
+
+CONFIG0 = dict(length=256, pairs=4, sigma=1e-3, token_seed=0, noise_seed=1)
+SENSITIVE = dict(length=128, pairs=2, sigma=2e-2, token_seed=3, noise_seed=4, weight_seed=5)
+
+
+def sensitive_weights(params, seed):
+    """Init weights moved away from the init's degenerate points so that the loss depends on
+    every upstream op: logits of order one, open value-embedding gates, varied mixing scalars."""
+    g = torch.Generator().manual_seed(seed)
+    p = {k: v.clone() for k, v in params.items()}
+    p['lm_head.weight'] = torch.randn(p['lm_head.weight'].shape, generator=g) * 0.05
+    for k in list(p):
+        if k.endswith('ve_gate.weight'):
+            p[k] = (torch.rand(p[k].shape, generator=g) - 0.5)
+    p['resid_lambdas'] = 1.0 + 0.1 * torch.randn(p['resid_lambdas'].shape, generator=g)
+    p['x0_lambdas'] = 0.1 + 0.05 * torch.randn(p['x0_lambdas'].shape, generator=g)
+    return p
+
+
+def main(ref_root):
+    sys.path.insert(0, str(ref_root))
+    from utils.model import GPT, GPTConfig, apply_rotary_emb, attention, norm
+    from train.val.eggroll import lowrank, lowrank_embed, make_model, population_loss
+
+    torch.set_grad_enabled(False)
+    arrays, summary = {}, {}
+
+    # Parameter order/shapes of the fixed module (strict state-dict keys, RNG order of offsets).
+    with torch.device('meta'):
+        meta = GPT(GPTConfig())
+    summary['named_parameters'] = [[n, list(p.shape)] for n, p in meta.named_parameters()]
+    summary['window_sizes'] = [w for w, _ in meta.window_sizes]
+
+    model = make_model(torch.device('cpu'), 0)
+    params = dict(model.named_parameters())
+    summary['init'] = {n: dict(sum=float(p.double().sum()), sumsq=float(p.double().square().sum()),
+                               head=[float(v) for v in p.flatten()[:4]])
+                       for n, p in params.items()}
+    for n in ('transformer.h.0.attn.c_q.weight', 'transformer.h.3.attn.c_proj.weight',
+              'transformer.h.7.mlp.c_proj.weight', 'lm_head.weight', 'value_embeds.5.weight'):
+        arrays['init/' + n] = p_np = params[n][:8, :16].numpy().copy()
+        assert p_np.dtype == np.float32
+    # bfloat16 rotary tables as raw bit patterns (uint16), first 2048 positions.
+    arrays['cos_bits'] = model.cos[0, :2048, 0, :].contiguous().view(torch.int16).numpy().view(np.uint16)
+    arrays['sin_bits'] = model.sin[0, :2048, 0, :].contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    # Config 0: population of 4 antithetic pairs on a 256-token Zipf sequence, seed-0 weights.
+    idx, targets = sequence(CONFIG0['length'], seed=CONFIG0['token_seed'])
+    noise, sign = antithetic(pair_noise(CONFIG0['pairs'], seed=CONFIG0['noise_seed']), CONFIG0['sigma'])
+    arrays['config0/idx'], arrays['config0/targets'] = idx.numpy(), targets.numpy()
+    arrays['config0/losses'] = population_loss(model, params, noise, sign, idx, targets).numpy()
+    arrays['config0/clean'] = model(idx[None], targets[None], loss_reduction='none').numpy()
+
+    # Sensitive variant: same forward, weights/sigma where every term moves the loss.
+    sp = sensitive_weights(params, SENSITIVE['weight_seed'])
+    idx, targets = sequence(SENSITIVE['length'], seed=SENSITIVE['token_seed'])
+    noise, sign = antithetic(pair_noise(SENSITIVE['pairs'], seed=SENSITIVE['noise_seed']), SENSITIVE['sigma'])
+    arrays['sensitive/idx'], arrays['sensitive/targets'] = idx.numpy(), targets.numpy()
+    arrays['sensitive/losses'] = population_loss(model, sp, noise, sign, idx, targets).numpy()
+    model.load_state_dict({k: v for k, v in sp.items()}, strict=True)
+    arrays['sensitive/clean'] = model(idx[None], targets[None], loss_reduction='none').numpy()
+    arrays['sensitive/logits'] = model(idx[None])[0, :2].numpy()
+
+    # Per-function vectors on small seeded inputs.
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 24, 3, 64, generator=g)
+    cos = model.cos[:, :24]
+    sin = model.sin[:, :24]
+    arrays['fn/rotary_in'] = x.numpy()
+    arrays['fn/rotary_out'] = apply_rotary_emb(x, cos, sin).numpy()
+    y = torch.randn(5, 512, generator=g) * 3.0
+    arrays['fn/norm_in'], arrays['fn/norm_out'] = y.numpy(), norm(y).numpy()
+    for window, length in ((16, 96), (64, 96), (1024, 128)):
+        q, k, v = (torch.randn(2, length, 2, 64, generator=g) for _ in range(3))
+        tag = f'fn/attn_w{window}_t{length}'
+        arrays[tag + '/q'], arrays[tag + '/k'], arrays[tag + '/v'] = q.numpy(), k.numpy(), v.numpy()
+        arrays[tag + '/out'] = attention(q, k, v, window).numpy()
+    m, t, din, dout = 4, 6, 32, 24
+    xi = torch.randn(m, t, din, generator=g)
+    w = torch.randn(dout, din, generator=g)
+    a, b = torch.randn(m, dout, generator=g), torch.randn(m, din, generator=g)
+    s = torch.tensor([0.5, -0.5, 0.25, -0.25])
+    arrays.update({'fn/lowrank_x': xi.numpy(), 'fn/lowrank_w': w.numpy(), 'fn/lowrank_a': a.numpy(),
+                   'fn/lowrank_b': b.numpy(), 'fn/lowrank_s': s.numpy(),
+                   'fn/lowrank_out': lowrank(xi, w, a, b, s).numpy()})
+    ew = torch.randn(10, 8, generator=g)
+    ea, eb = torch.randn(m, 10, generator=g), torch.randn(m, 8, generator=g)
+    eidx = torch.tensor([3, 0, 9, 3, 7])
+    arrays.update({'fn/embed_w': ew.numpy(), 'fn/embed_a': ea.numpy(), 'fn/embed_b': eb.numpy(),
+                   'fn/embed_idx': eidx.numpy(), 'fn/embed_s': s.numpy(),
+                   'fn/embed_out': lowrank_embed(ew, ea, eb, eidx, s).numpy()})
+
+    summary['config0'] = dict(CONFIG0, losses=[float(v) for v in arrays['config0/losses']])
+    summary['sensitive'] = dict(SENSITIVE, losses=[float(v) for v in arrays['sensitive/losses']])
+    summary['torch'] = torch.__version__
+    np.savez_compressed(HERE / 'golden.npz', **arrays)
+    (HERE / 'golden.json').write_text(json.dumps(summary, indent=1) + '\n')
+    print(json.dumps({k: summary[k] for k in ('config0', 'sensitive', 'window_sizes')}, indent=1))
+
+
+if __name__ == '__main__':
+    main(Path(sys.argv[1] if len(sys.argv) > 1 else '/root/reference'))

@@ -1,0 +1,283 @@
+"""Kernel-level parity of libnoise_amd on the GPU against float64 references of the same op on the
+same (bf16-rounded) inputs. Tolerances: fp32 outputs to accumulation-order error; bf16 outputs
+within 1e-2 relative (and almost all elements bit-identical to the rounded reference)."""
+import math
+
+import pytest
+import torch
+
+from noise_amd import _lib
+from noise_amd import kernels as nk
+from noise_amd.kernels import NoiseRows
+from oracle import model_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _bf(x):
+    return x.to(torch.bfloat16)
+
+
+def _close_bf16(got, ref, rtol=1e-2, exact_frac=0.99):
+    got = got.double().cpu()
+    ref_r = ref.to(torch.bfloat16).double()
+    err = (got - ref).abs()
+    assert (err <= rtol * ref.abs() + 1e-2 * rtol * ref.abs().max()).all(), float(err.max())
+    assert (got == ref_r).double().mean() >= exact_frac
+
+
+GEMM_CASES = [
+    # M, N, K, T, nseg, parts, shift
+    (512, 256, 64, 256, 1, 1, 0),
+    (1000, 512, 512, 256, 1, 8, 0),      # row tail
+    (768, 1536, 512, 100, 3, 1, 1),      # 3 segments, tiles straddling members, pair rows
+    (512, 2048, 512, 512, 1, 1, 0),
+    (256, 512, 2048, 128, 1, 16, 1),
+]
+
+
+@pytest.mark.parametrize('M,N,K,T,nseg,parts,shift', GEMM_CASES)
+@pytest.mark.parametrize('mode', [_lib.EPI_BF16, _lib.EPI_F32, _lib.EPI_ADD_F32, _lib.EPI_RELU2_BF16])
+def test_lowrank_gemm(device, M, N, K, T, nseg, parts, shift, mode):
+    g = _gen(M + N + K + mode)
+    members = (M + T - 1) // T
+    rows = (members >> shift) + 1
+    A = _bf(torch.randn(M, K, generator=g))
+    W = _bf(torch.randn(N, K, generator=g) / math.sqrt(K))
+    sign = torch.randn(members, generator=g) * 0.1
+    seg = N // nseg
+    a = [torch.randn(rows, seg, generator=g) for _ in range(nseg)]
+    u = [torch.randn(M, parts, generator=g) for _ in range(nseg)]
+    p = torch.arange(M) // T
+    ref = A.double() @ W.double().t()
+    for s in range(nseg):
+        ref[:, s * seg:(s + 1) * seg] += (sign[p] * u[s].sum(1)).double()[:, None] * a[s][p >> shift].double()
+    dA, dW, dsign = A.to(device), W.to(device), sign.to(device)
+    da = [x.to(device) for x in a]
+    du = [x.to(device) for x in u]
+    r1 = nk.rank1(dsign, T, da, du, parts, parts, shift)
+    if mode == _lib.EPI_F32:
+        C = torch.empty(M, N, device=device)
+        nk.lowrank_gemm(dA, dW, r1, mode, C)
+        torch.testing.assert_close(C.cpu().double(), ref, rtol=1e-5, atol=1e-4)
+    elif mode == _lib.EPI_ADD_F32:
+        C0 = torch.randn(M, N, generator=g)
+        C = C0.to(device)
+        nk.lowrank_gemm(dA, dW, r1, mode, C)
+        torch.testing.assert_close(C.cpu().double(), ref + C0.double(), rtol=1e-5, atol=1e-4)
+    elif mode == _lib.EPI_BF16:
+        C = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+        nk.lowrank_gemm(dA, dW, r1, mode, C)
+        _close_bf16(C, ref)
+    else:
+        bnext = torch.randn(rows, N, generator=g)
+        C = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+        un = torch.full((M, N // 128), float('nan'), device=device)
+        nk.lowrank_gemm(dA, dW, r1, mode, C, bnext.to(device), un)
+        hid = torch.relu(ref).square()
+        _close_bf16(C, hid)
+        got = C.cpu().double()  # the partial dots use the stored bf16 values
+        want = (got * bnext[p >> shift].double()).view(M, N // 128, 128).sum(-1)
+        torch.testing.assert_close(un.cpu().double(), want, rtol=1e-5, atol=1e-3)
+
+
+def test_lowrank_gemm_unperturbed_and_errors(device):
+    g = _gen(3)
+    A = _bf(torch.randn(300, 128, generator=g)).to(device)
+    W = _bf(torch.randn(256, 128, generator=g)).to(device)
+    C = torch.empty(300, 256, device=device)
+    nk.lowrank_gemm(A, W, None, _lib.EPI_F32, C)
+    torch.testing.assert_close(C.cpu().double(), A.cpu().double() @ W.cpu().double().t(), rtol=1e-5, atol=1e-4)
+    with pytest.raises(ValueError):
+        nk.lowrank_gemm(A, W[:100], None, _lib.EPI_F32, C)     # N not a multiple of 256
+    with pytest.raises(ValueError):
+        nk.lowrank_gemm(A[:, :100], W[:, :100], None, _lib.EPI_F32, C)  # K not a multiple of 64
+
+
+def test_embed_norm(device):
+    g = _gen(4)
+    V, T, m = 4096, 96, 6
+    table = torch.randn(V, 512, generator=g)
+    idx = torch.randint(0, V, (T,), generator=g)
+    a, b = torch.randn(3, V, generator=g), torch.randn(3, 512, generator=g)
+    sign = torch.tensor([0.5, -0.5, 0.1, -0.1, 0.02, -0.02])
+    x0 = torch.empty(m * T, 512, device=device)
+    x = torch.empty_like(x0)
+    nk.embed_norm(table.to(device), idx.to(device), T, m, sign.to(device),
+                 NoiseRows(a=a.to(device), b=b.to(device), shift=1), x0, x)
+    ref = R.rms_norm(R.lowrank_embed(table.double(), a.double().repeat_interleave(2, 0),
+                                     b.double().repeat_interleave(2, 0), idx, sign.double())).reshape(m * T, 512)
+    torch.testing.assert_close(x0.cpu().double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.equal(x0, x)
+    bad = idx.clone()
+    bad[5] = V
+    nk.embed_norm(table.to(device), bad.to(device), T, m, None, None, x0)
+    rows = x0.cpu().view(m, T, 512)
+    assert torch.isnan(rows[:, 5]).all() and not torch.isnan(rows[:, 4]).any()
+
+
+def test_mix_norm(device):
+    g = _gen(5)
+    T, m = 64, 4
+    M = T * m
+    x, x0 = torch.randn(M, 512, generator=g), torch.randn(M, 512, generator=g)
+    lam = torch.tensor([1.1, 0.2])
+    eps_r, eps_m = torch.randn(2, 8, generator=g), torch.randn(2, 8, generator=g)
+    sign = torch.tensor([0.3, -0.3, 0.05, -0.05])
+    bs = [torch.randn(2, 512, generator=g) for _ in range(3)]
+    gw = torch.randn(8, 32, generator=g)
+    ga, gb = torch.randn(2, 8, generator=g), torch.randn(2, 32, generator=g)
+    dx = x.to(device)
+    h = torch.empty(M, 512, dtype=torch.bfloat16, device=device)
+    u = torch.empty(M, 3, device=device)
+    gate = torch.empty(M, 8, device=device)
+    dl = lam.to(device)
+    nk.mix_norm(dx, h, T, sign.to(device), x0.to(device), dl[0], dl[1], eps_r.to(device)[:, 3], eps_m.to(device)[:, 3], 1,
+               bs=tuple(b.to(device) for b in bs), u=u, gate_w=gw.to(device),
+               gate_nz=NoiseRows(a=ga.to(device), b=gb.to(device), shift=1), gate=gate)
+    p = torch.arange(M) // T
+    s = sign[p].double()[:, None]
+    mixed = (lam[0] + s * eps_r[p >> 1, 3, None]) * x.double() + (lam[1] + s * eps_m[p >> 1, 3, None]) * x0.double()
+    torch.testing.assert_close(dx.cpu().double(), mixed, rtol=1e-6, atol=1e-5)
+    hn = R.rms_norm(mixed)
+    _close_bf16(h, hn)
+    hb = h.cpu().double()
+    for j in range(3):
+        torch.testing.assert_close(u[:, j].cpu().double(), (hb * bs[j][p >> 1].double()).sum(1), rtol=1e-5, atol=1e-4)
+    z = hb[:, :32] @ gw.double().t() + s * (hb[:, :32] * gb[p >> 1].double()).sum(1, keepdim=True) * ga[p >> 1].double()
+    torch.testing.assert_close(gate.cpu().double(), 2 * torch.sigmoid(z), rtol=1e-5, atol=1e-5)
+
+
+def test_rope_norm_ve(device):
+    g = _gen(6)
+    T, m, V = 48, 4, 4096
+    M = T * m
+    qkv = torch.randn(M, 1536, generator=g)
+    gate = torch.rand(M, 8, generator=g) * 2
+    table = torch.randn(V, 512, generator=g)
+    idx = torch.randint(0, V, (T,), generator=g)
+    a, b = torch.randn(m, V, generator=g), torch.randn(m, 512, generator=g)
+    sign = torch.tensor([0.2, -0.2, 0.7, -0.7])
+    cos, sin = R.rotary_tables(T)
+    out = torch.empty(M, 1536, dtype=torch.bfloat16, device=device)
+    nk.rope_norm_ve(qkv.to(device), out, T, cos.to(device), sin.to(device), sign.to(device), gate.to(device),
+                   table.to(device), idx.to(device), NoiseRows(a=a.to(device), b=b.to(device), shift=0))
+    q = qkv[:, :512].double().view(m, T, 8, 64)
+    k = qkv[:, 512:1024].double().view(m, T, 8, 64)
+    rq = R.rms_norm(R.rotary(q, cos.double(), sin.double())).reshape(M, 512)
+    rk = R.rms_norm(R.rotary(k, cos.double(), sin.double())).reshape(M, 512)
+    ve = R.lowrank_embed(table.double(), a.double(), b.double(), idx, sign.double()).reshape(M, 512)
+    v = qkv[:, 1024:].double() + gate.double().repeat_interleave(64, 1) * ve
+    got = out.cpu()
+    _close_bf16(got[:, :512], rq)
+    _close_bf16(got[:, 512:1024], rk)
+    _close_bf16(got[:, 1024:], v)
+
+
+@pytest.mark.parametrize('T,window,members', [(96, 16, 2), (128, 64, 3), (256, 1024, 2), (300, 100, 2), (2048, 1024, 1)])
+def test_window_attention(device, T, window, members):
+    g = _gen(T + window)
+    M = members * T
+    q = R.rms_norm(torch.randn(M, 8, 64, generator=g)).reshape(M, 512)
+    k = R.rms_norm(torch.randn(M, 8, 64, generator=g)).reshape(M, 512)
+    v = torch.randn(M, 512, generator=g)
+    qkv = _bf(torch.cat([q, k, v], 1))
+    bp = torch.randn(members, 512, generator=g)
+    y = torch.empty(M, 512, dtype=torch.bfloat16, device=device)
+    uproj = torch.empty(M, 8, device=device)
+    mom = torch.empty(members, 8, 2, 64, device=device)
+    scratch = torch.empty(members * 8 * ((T + 127) // 128) * 128, device=device)
+    nk.window_attention(qkv.to(device), y, members, T, window, bp.to(device), 0, uproj, mom, scratch)
+    qd, kd, vd = (qkv[:, i * 512:(i + 1) * 512].double().view(members, T, 8, 64) for i in range(3))
+    ref = R.window_attention(qd, kd, vd, window).reshape(M, 512)
+    got = y.cpu().double()
+    err = (got - ref).abs()
+    assert float(err.max()) < 2e-2 * max(1.0, float(ref.abs().max())), float(err.max())
+    assert float(err.mean()) < 2e-3
+    p = torch.arange(M) // T
+    torch.testing.assert_close(uproj.cpu().double(), (got * bp[p].double()).view(M, 8, 64).sum(-1), rtol=1e-5, atol=1e-4)
+    gy = got.view(members, T, 8, 64)
+    want = torch.stack([gy.mean(1), gy.square().mean(1)], 2)  # [members, 8, 2, 64]
+    torch.testing.assert_close(mom.cpu().double(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_head_ce(device):
+    g = _gen(7)
+    T, m, V = 64, 4, 4096
+    M = T * m
+    h = _bf(R.rms_norm(torch.randn(M, 512, generator=g)))
+    W = torch.randn(V, 512, generator=g) * 0.06
+    a = torch.randn(m, V, generator=g)
+    u = torch.randn(M, generator=g)
+    sign = torch.tensor([0.01, -0.01, 0.002, -0.002])
+    targets = torch.randint(0, V, (T,), generator=g)
+    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi)
+    nk.cast_bf16(W.to(device), hi, lo)
+    ce = torch.empty(M, device=device)
+    nk.head_ce(h.to(device), hi, lo, T, targets.to(device), ce, sign.to(device),
+              NoiseRows(a=a.to(device), shift=0), u.to(device))
+    p = torch.arange(M) // T
+    z = h.double() @ W.double().t() + (sign[p] * u).double()[:, None] * a[p].double()
+    ref = R.softcap_ce(z, targets.repeat(m))
+    torch.testing.assert_close(ce.cpu().double(), ref, rtol=0, atol=2e-5)
+    losses = torch.empty(m, device=device)
+    nk.member_mean(ce, m, T, losses)
+    torch.testing.assert_close(losses.cpu().double(), ce.cpu().double().view(m, T).mean(1), rtol=1e-6, atol=1e-6)
+
+
+def test_cast_bf16_round_to_nearest_even(device):
+    g = _gen(8)
+    x = torch.randn(100003, generator=g) * 10
+    x[:4] = torch.tensor([1.00390625, 1.01171875, -3.0078125, 0.0])  # exact ties
+    hi = torch.empty(x.numel(), dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi)
+    nk.cast_bf16(x.to(device), hi, lo)
+    assert torch.equal(hi.cpu(), x.to(torch.bfloat16))
+    assert torch.equal(lo.cpu(), (x - x.to(torch.bfloat16).float()).to(torch.bfloat16))
+
+
+def test_fitness_gradient_adamw(device):
+    from oracle import es_ref
+    g = _gen(9)
+    pairs, out, inn = 37, 70, 90
+    losses = torch.randn(2 * pairs, generator=g) + 8
+    w_ref, n = es_ref.fitness(losses.double(), pairs)
+    w = torch.empty(pairs, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    nk.fitness(losses.to(device), pairs, w, status)
+    torch.testing.assert_close(w.cpu().double(), w_ref, rtol=1e-5, atol=1e-5)
+    assert int(status.item()) == 0
+    bad = losses.clone()
+    bad[3] = float('inf')
+    nk.fitness(bad.to(device), pairs, w, status)
+    assert int(status.item()) == _lib.NOISE_ENONFINITE
+
+    buf = torch.randn(10000, generator=g)
+    off = torch.randint(0, 10000 - out - inn, (pairs,), generator=g)
+    w_in = torch.randn(pairs, generator=g)
+    a = torch.stack([buf[o:o + out] for o in off.tolist()])
+    b = torch.stack([buf[o + out:o + out + inn] for o in off.tolist()])
+    ref = es_ref.gradient(w_in.double(), {'m': (a, b), 'v': a[:, :8]}, n)
+    G = torch.empty(out, inn, device=device)
+    dbuf, doff = buf.to(device), off.to(device)
+    nk.es_gradient(w_in.to(device), dbuf, doff, dbuf, doff + out, out, inn, -1.0 / n, G)
+    torch.testing.assert_close(G.cpu().double(), ref['m'], rtol=1e-5, atol=1e-6)
+    Gv = torch.empty(8, device=device)
+    nk.es_gradient(w_in.to(device), dbuf, doff, None, None, 8, 1, -1.0 / n, Gv)
+    torch.testing.assert_close(Gv.cpu().double(), ref['v'], rtol=1e-5, atol=1e-6)
+
+    p0 = torch.randn(1000, generator=g)
+    refp = p0.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([refp], lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    dp, dm, dv = p0.to(device), torch.zeros(1000, device=device), torch.zeros(1000, device=device)
+    for step in range(1, 4):
+        grad = torch.randn(1000, generator=g) * 1e-3
+        refp.grad = grad.clone()
+        opt.step()
+        nk.adamw(dp, grad.to(device), dm, dv, 1e-3, 0.5, 0.95, 1e-8, 0.0, step)
+    torch.testing.assert_close(dp.cpu(), refp.detach(), rtol=0, atol=1e-6)

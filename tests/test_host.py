@@ -1,0 +1,86 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports what include/noise_amd.h
+declares, argument validation rejects bad shapes before anything is launched, and the parameter
+container round-trips the fixed model's strict state dict (utils/eval.py:24-31)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import noise_amd
+from noise_amd import _lib
+from noise_amd.config import param_shapes
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    text = (ROOT / 'include' / 'noise_amd.h').read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'^\s*(?:const\s+)?\w+\*?\s+\*?(noise_\w+)\s*\(', text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.exported_symbols())
+    assert lib.noise_abi_version() == 1
+
+
+def test_argument_errors_raise_before_launch():
+    lib = _lib.load()
+    # N = 100 is not a multiple of 256: rejected on the host with a ValueError.
+    fake = C.c_void_p(256)
+    st = lib.noise_lowrank_gemm(fake, 64, fake, 64, 10, 100, 64, None, 0, fake, 100, None, 0, None, 0, None)
+    assert st == _lib.NOISE_EINVAL
+    with pytest.raises(ValueError, match='multiple of 256'):
+        _lib.check(st)
+    st = lib.noise_embed_norm(fake, 500, 4096, 500, fake, 0, 8, 1, None, None, 0, None, 0, 0, fake, None, None)
+    assert st == _lib.NOISE_EINVAL
+    st = lib.noise_fitness(fake, 7, 3, fake, None, None)
+    assert st == _lib.NOISE_EINVAL
+    st = lib.noise_adamw(fake, fake, fake, fake, 10, 1e-3, 0.9, 0.99, 1e-8, 0.0, 0, None)
+    assert st == _lib.NOISE_EINVAL
+    with pytest.raises(FloatingPointError):
+        _lib.check(_lib.NOISE_ENONFINITE)
+
+
+def test_state_dict_strict_round_trip():
+    a = noise_amd.make_model('cpu', 0)
+    sd = a.state_dict()
+    assert [(k, tuple(v.shape)) for k, v in sd.items()] == [(n, tuple(s)) for n, s in param_shapes()]
+    b = noise_amd.GPT()
+    b.load_state_dict(sd, strict=True)
+    assert all(torch.equal(b.state_dict()[k], v) for k, v in sd.items())
+    assert torch.equal(a.flat, b.flat)
+    bad = dict(sd)
+    bad.pop('lm_head.weight')
+    with pytest.raises(RuntimeError):
+        b.load_state_dict(bad, strict=True)
+    bad = dict(sd)
+    bad['extra.weight'] = torch.zeros(1)
+    with pytest.raises(RuntimeError):
+        b.load_state_dict(bad, strict=True)
+
+
+def test_params_tile_one_flat_buffer():
+    m = noise_amd.make_model('cpu', 1)
+    off = 0
+    for name, p in m.named_parameters():
+        assert p.data_ptr() == m.flat.data_ptr() + 4 * off, name
+        off += p.numel()
+    assert off == m.flat.numel() == 37_749_776
+    from noise_amd.optim import _flat_base
+    base = _flat_base(list(m.parameters()))
+    assert base is not None and base.numel() == off and base.data_ptr() == m.flat.data_ptr()
+
+
+def test_population_loss_rejects_cpu_tensors():
+    p = {n: torch.zeros(s) for n, s in param_shapes()}
+    with pytest.raises(ValueError, match='GPU'):
+        noise_amd.population_loss(None, p, {}, torch.zeros(2), torch.zeros(4, dtype=torch.long),
+                                  torch.zeros(4, dtype=torch.long))

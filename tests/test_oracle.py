@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (oracle/) before anything is compared with it.
+
+1. Against the reference's own outputs (tests/golden/, written by tests/golden/make_golden.py from
+   the reference's make_model / population_loss / GPT.forward / attention / apply_rotary_emb / norm /
+   lowrank / lowrank_embed on CPU in float32).
+2. Against what the mathematics fixes: the materialised rank-1 weight, the sigma = 0 population,
+   the sign flip, ln(V) at init, the fp64 directional derivative, library routines (SDPA with an
+   explicit mask, F.rms_norm, F.cross_entropy, torch.optim.AdamW) and brute-force loops.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from noise_amd.config import GPTConfig, n_params, noise_floats_per_pair, param_shapes, window_sizes
+from noise_amd.synthetic import antithetic, pair_noise
+from oracle import es_ref
+from oracle import model_ref as R
+
+t = torch.from_numpy
+
+
+# ---------------------------------------------------------------- 1. reference goldens
+
+def test_param_layout_matches_reference(golden_json):
+    assert [[n, list(s)] for n, s in param_shapes()] == golden_json['named_parameters']
+    assert n_params() == 37_749_776
+    assert noise_floats_per_pair() == 101_552
+    assert window_sizes(GPTConfig()) == golden_json['window_sizes']
+
+
+def test_init_matches_reference(init_params, golden, golden_json):
+    for name, p in init_params.items():
+        ref = golden_json['init'][name]
+        assert [float(v) for v in p.flatten()[:4]] == ref['head'], name
+        assert abs(float(p.double().sum()) - ref['sum']) <= 1e-9 * max(1.0, abs(ref['sum'])) + 1e-6, name
+        assert abs(float(p.double().square().sum()) - ref['sumsq']) <= 1e-9 * ref['sumsq'] + 1e-9, name
+    for key in golden:
+        if key.startswith('init/'):
+            assert torch.equal(init_params[key[5:]][:8, :16], t(golden[key])), key
+
+
+def test_rotary_tables_bit_exact(golden):
+    cos, sin = R.rotary_tables(2048)
+    bits = lambda x: x.bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert (bits(cos) == golden['cos_bits']).all()
+    assert (bits(sin) == golden['sin_bits']).all()
+
+
+def test_rotary_norm_fns(golden):
+    x = t(golden['fn/rotary_in'])
+    cos, sin = R.rotary_tables(24)
+    torch.testing.assert_close(R.rotary(x, cos, sin), t(golden['fn/rotary_out']), rtol=0, atol=1e-6)
+    torch.testing.assert_close(R.rms_norm(t(golden['fn/norm_in'])), t(golden['fn/norm_out']), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize('window,length', [(16, 96), (64, 96), (1024, 128)])
+def test_window_attention_matches_flex(golden, window, length):
+    tag = f'fn/attn_w{window}_t{length}'
+    q, k, v = (t(golden[f'{tag}/{n}']) for n in 'qkv')
+    torch.testing.assert_close(R.window_attention(q, k, v, window), t(golden[tag + '/out']), rtol=1e-5, atol=2e-6)
+
+
+def test_lowrank_fns(golden):
+    g = {k[3:]: t(v) for k, v in golden.items() if k.startswith('fn/')}
+    out = R.lowrank(g['lowrank_x'], g['lowrank_w'], g['lowrank_a'], g['lowrank_b'], g['lowrank_s'])
+    torch.testing.assert_close(out, g['lowrank_out'], rtol=1e-6, atol=1e-5)
+    out = R.lowrank_embed(g['embed_w'], g['embed_a'], g['embed_b'], g['embed_idx'], g['embed_s'])
+    torch.testing.assert_close(out, g['embed_out'], rtol=0, atol=1e-6)
+
+
+def _config_inputs(golden, tag, pairs, sigma, noise_seed):
+    idx, targets = t(golden[f'{tag}/idx']), t(golden[f'{tag}/targets'])
+    noise, sign = antithetic(pair_noise(pairs, seed=noise_seed), sigma)
+    return idx, targets, noise, sign
+
+
+def sensitive_params(init_params, seed=5):
+    """Same construction as tests/golden/make_golden.py:sensitive_weights."""
+    g = torch.Generator().manual_seed(seed)
+    p = {k: v.clone() for k, v in init_params.items()}
+    p['lm_head.weight'] = torch.randn(p['lm_head.weight'].shape, generator=g) * 0.05
+    for k in list(p):
+        if k.endswith('ve_gate.weight'):
+            p[k] = (torch.rand(p[k].shape, generator=g) - 0.5)
+    p['resid_lambdas'] = 1.0 + 0.1 * torch.randn(p['resid_lambdas'].shape, generator=g)
+    p['x0_lambdas'] = 0.1 + 0.05 * torch.randn(p['x0_lambdas'].shape, generator=g)
+    return p
+
+
+def test_population_loss_matches_reference_config0(init_params, golden, golden_json):
+    c = golden_json['config0']
+    idx, targets, noise, sign = _config_inputs(golden, 'config0', c['pairs'], c['sigma'], c['noise_seed'])
+    losses = R.population_loss(init_params, noise, sign, idx, targets, policy='fp32')
+    torch.testing.assert_close(losses, t(golden['config0/losses']), rtol=0, atol=5e-6)
+    # The build's bf16 cast points stay inside the 1e-4 per-member budget on these inputs.
+    build = R.population_loss(init_params, noise, sign, idx, targets, policy='build')
+    assert (build.float() - t(golden['config0/losses'])).abs().max() < 1e-4
+
+
+def test_population_loss_matches_reference_sensitive(init_params, golden, golden_json):
+    c = golden_json['sensitive']
+    p = sensitive_params(init_params, c['weight_seed'])
+    idx, targets, noise, sign = _config_inputs(golden, 'sensitive', c['pairs'], c['sigma'], c['noise_seed'])
+    losses = R.population_loss(p, noise, sign, idx, targets, policy='fp32')
+    torch.testing.assert_close(losses, t(golden['sensitive/losses']), rtol=0, atol=2e-5)
+    clean = R.clean_loss(p, idx[None], targets[None], policy='fp32')[0]
+    torch.testing.assert_close(clean, t(golden['sensitive/clean']), rtol=0, atol=5e-5)
+
+
+def test_clean_forward_matches_reference(init_params, golden):
+    idx, targets = t(golden['config0/idx']), t(golden['config0/targets'])
+    clean = R.clean_loss(init_params, idx[None], targets[None], policy='fp32')[0]
+    torch.testing.assert_close(clean, t(golden['config0/clean']), rtol=0, atol=5e-6)
+
+
+# ---------------------------------------------------------------- 2. closed forms
+
+def test_rank1_identity_fp64():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 5, 7, generator=g, dtype=torch.float64)
+    w = torch.randn(4, 7, generator=g, dtype=torch.float64)
+    a, b = torch.randn(3, 4, generator=g, dtype=torch.float64), torch.randn(3, 7, generator=g, dtype=torch.float64)
+    s = torch.tensor([0.3, -0.3, 0.1], dtype=torch.float64)
+    dense = torch.stack([x[j] @ (w + s[j] * torch.outer(a[j], b[j])).t() for j in range(3)])
+    torch.testing.assert_close(R.lowrank(x, w, a, b, s), dense)
+    we = torch.randn(6, 7, generator=g, dtype=torch.float64)
+    ae = torch.randn(3, 6, generator=g, dtype=torch.float64)
+    idx = torch.tensor([5, 0, 0, 2])
+    dense = torch.stack([(we + s[j] * torch.outer(ae[j], b[j]))[idx] for j in range(3)])
+    torch.testing.assert_close(R.lowrank_embed(we, ae, b, idx, s), dense)
+
+
+def test_window_attention_matches_sdpa():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(2, 40, 3, 64, generator=g, dtype=torch.float64) for _ in range(3))
+    for w in (0, 5, 39, 100):
+        i, j = torch.arange(40)[:, None], torch.arange(40)[None, :]
+        mask = (i >= j) & (i - j <= w)
+        ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                             attn_mask=mask).transpose(1, 2)
+        torch.testing.assert_close(R.window_attention(q, k, v, w), ref)
+
+
+def test_norm_and_ce_match_library():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(4, 512, generator=g) * 5
+    torch.testing.assert_close(R.rms_norm(x), F.rms_norm(x, (512,)), rtol=1e-6, atol=1e-6)
+    z = torch.randn(6, 4096, generator=g, dtype=torch.float64) * 20
+    tg = torch.randint(0, 4096, (6,), generator=g)
+    ref = F.cross_entropy(15 * torch.tanh(z / 15), tg, reduction='none')
+    torch.testing.assert_close(R.softcap_ce(z, tg), ref)
+
+
+@pytest.fixture(scope='module')
+def small_inputs(init_params):
+    from noise_amd.synthetic import sequence
+    idx, targets = sequence(32, seed=7)
+    return idx, targets
+
+
+def test_sigma_zero_members_equal_clean(init_params, small_inputs):
+    idx, targets = small_inputs
+    noise, sign = antithetic(pair_noise(2, seed=3), 0.0)
+    losses = R.population_loss(init_params, noise, sign, idx, targets, policy='fp64')
+    clean = R.clean_loss(init_params, idx[None], targets[None], policy='fp64').mean()
+    torch.testing.assert_close(losses, clean.expand(4), rtol=0, atol=1e-12)
+
+
+def test_sign_flip_swaps_pair(init_params, small_inputs):
+    idx, targets = small_inputs
+    noise, sign = antithetic(pair_noise(2, seed=4), 0.01)
+    a = R.population_loss(init_params, noise, sign, idx, targets, policy='fp64')
+    b = R.population_loss(init_params, noise, -sign, idx, targets, policy='fp64')
+    torch.testing.assert_close(a.view(2, 2).flip(1).reshape(-1), b, rtol=0, atol=1e-12)
+
+
+def test_init_loss_is_ln_vocab(init_params, small_inputs):
+    idx, targets = small_inputs
+    clean = R.clean_loss(init_params, idx[None], targets[None], policy='fp64').mean()
+    assert abs(float(clean) - math.log(4096)) < 5e-3
+
+
+def test_antithetic_difference_is_directional_derivative(init_params, small_inputs):
+    """(L+ - L-) / (2 sigma) -> dL/dt of L(theta + t E) at t = 0, the fp64 JVP."""
+    idx, targets = small_inputs
+    p = sensitive_params(init_params)
+    pn = pair_noise(1, seed=9, dtype=torch.float64)
+    sigma = 1e-5
+    noise, sign = antithetic(pn, sigma)
+    lp, lm = R.population_loss(p, noise, sign, idx, targets, policy='fp64').tolist()
+    fd = (lp - lm) / (2 * sigma)
+
+    names = list(p)
+
+    def loss_of(tv):
+        q = {}
+        for n in names:
+            v = pn[n]
+            pert = torch.outer(v[0][0], v[1][0]) if isinstance(v, tuple) else v[0]
+            q[n] = p[n].double() + tv * pert
+        return R.clean_loss(q, idx[None], targets[None], policy='fp64').mean()
+
+    _, jvp = torch.func.jvp(loss_of, (torch.tensor(0.0, dtype=torch.float64),),
+                            (torch.tensor(1.0, dtype=torch.float64),))
+    assert abs(fd - float(jvp)) <= 1e-5 * max(1.0, abs(float(jvp)))
+
+
+# ---------------------------------------------------------------- ES update
+
+def test_fitness_matches_brute_force():
+    g = torch.Generator().manual_seed(5)
+    losses = torch.randn(12, generator=g, dtype=torch.float64)
+    w, n = es_ref.fitness(losses, 6)
+    f = [losses[2 * j + 1] - losses[2 * j] for j in range(6)]
+    mean = sum(f) / 6
+    std = math.sqrt(sum((x - mean) ** 2 for x in f) / 5)
+    torch.testing.assert_close(w, torch.tensor([x / (std + 1e-8) for x in f], dtype=torch.float64))
+    assert n == 6
+    # more differences than pairs wrap around with index_add (eggroll.py:153-154)
+    w2, n2 = es_ref.fitness(losses, 4)
+    full = torch.tensor([x / (std + 1e-8) for x in f], dtype=torch.float64)
+    torch.testing.assert_close(w2, torch.stack([full[0] + full[4], full[1] + full[5], full[2], full[3]]))
+
+
+def test_gradient_matches_brute_force():
+    g = torch.Generator().manual_seed(6)
+    w = torch.randn(5, generator=g, dtype=torch.float64)
+    a, b = torch.randn(5, 3, generator=g, dtype=torch.float64), torch.randn(5, 4, generator=g, dtype=torch.float64)
+    eps = torch.randn(5, 2, generator=g, dtype=torch.float64)
+    grads = es_ref.gradient(w, {'m': (a, b), 'v': eps}, 7)
+    dense = -sum(w[j] * torch.outer(a[j], b[j]) for j in range(5)) / 7
+    torch.testing.assert_close(grads['m'], dense)
+    torch.testing.assert_close(grads['v'], -sum(w[j] * eps[j] for j in range(5)) / 7)
+
+
+def test_adamw_matches_torch():
+    g = torch.Generator().manual_seed(7)
+    p0 = torch.randn(50, generator=g)
+    ref = p0.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([ref], lr=1e-2, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.1)
+    mine, m, v = p0.clone(), torch.zeros(50), torch.zeros(50)
+    for step in range(1, 6):
+        grad = torch.randn(50, generator=g)
+        ref.grad = grad.clone()
+        opt.step()
+        es_ref.adamw_step(mine, grad, m, v, step, 1e-2, (0.5, 0.95), 1e-8, 0.1)
+    torch.testing.assert_close(mine, ref.detach(), rtol=0, atol=1e-6)
+
+
+def test_centred_ranks_stable():
+    f = torch.tensor([0.5, -1.0, 0.5, 2.0])
+    torch.testing.assert_close(es_ref.centred_ranks(f), torch.tensor([1 / 3, 0.0, 2 / 3, 1.0]) - 0.5)
