@@ -53,7 +53,7 @@ typedef struct {
 #define NOISE_EPI_F32 1        /* C (fp32)  = A W^T + rank-1 */
 #define NOISE_EPI_ADD_F32 2    /* C (fp32) += A W^T + rank-1          (residual add) */
 #define NOISE_EPI_RELU2_BF16 3 /* C (bf16)  = relu(A W^T + rank-1)^2, and
-                                  u_next[r, c / 128] = sum over that 128-column group of
+                                  u_next[r, c / 64] = sum over that 64-column group of
                                   bf16(C[r, c]) * b_next[member(r), c] */
 
 /* x W^T + sign (x . b) a^T for A [M, K] bf16 and W [N, K] bf16 (the bf16 weight copy).

@@ -5,17 +5,22 @@
 // epilogue. The dot products u = A . b arrive precomputed per row (written by the producer of A),
 // so the rank-1 term costs one FMA per output element.
 //
-// Tiling for gfx950: a 256x256 output tile per workgroup of 4 waves (2 x 2), each wave owning a
-// 128x128 sub-tile as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane,
-// one wave per SIMD). K advances 64 at a time through a double-buffered LDS stage (2 x 72 KB,
-// rows padded to 144 B so the 16-byte fragment reads are bank-conflict free); the next stage's
-// global loads are issued before the current stage's MFMAs. Workgroups are renumbered so that
-// each XCD walks a contiguous run of tiles (neighbouring N tiles share the A rows in that XCD's L2).
+// Tiling for gfx950: a 256x256 output tile per workgroup of 8 waves (2 x 4, two per SIMD), each
+// wave owning a 128x64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32
+// accumulators per lane); the K loop is mma_tile_256 (two-stage-ahead global prefetch,
+// double-buffered LDS and fragments). The epilogue runs in four rounds of 32 rows per wave: the
+// rank-1 term and the mode's transform are applied to one accumulator block, the block is staged
+// through LDS as fp32 and written out with 16-byte coalesced accesses (a wave moves 1 KB of
+// contiguous output per instruction). Workgroups are renumbered so that each XCD walks a
+// contiguous run of tiles (neighbouring N tiles share the A rows in that XCD's L2).
 #include "mma_tile.h"
 
 namespace {
 
-constexpr int BM = noise::TILE, BN = noise::TILE, BK = noise::TBK;
+constexpr int BM = noise::TILE, BN = noise::TILE, BK = 2 * noise::TBK;
+constexpr int NT = noise::TILE_THREADS;
+constexpr int SLD = 72;  // epilogue staging row stride (floats): the two half-waves of a store
+                         // are 4 rows apart = 288 floats = 32 banks apart
 
 struct GemmArgs {
   const uint16_t* A;
@@ -35,13 +40,13 @@ struct GemmArgs {
 // LONGK marks the K >= 1024 instantiation (the MLP down-projection, K = 2048) so that it is a
 // kernel of its own in profiles; the code is the same.
 template <int MODE, bool LONGK>
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ void __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2, 2)))
 lowrank_gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
   __shared__ float su_s[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int ntn = g.N / BN;
   const int ntiles = gridDim.x;
   int bid = blockIdx.x;
@@ -52,7 +57,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
 
   // Per-row sign * u, staged once per tile (visible after the main loop's first barrier).
   const int seg = perturbed ? n0 / g.r1.seg_cols : 0;
-  {
+  if (tid < BM) {
     const int row = m0 + tid;
     float su = 0.f;
     if (perturbed && row < g.M) {
@@ -64,7 +69,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
     su_s[tid] = su;
   }
 
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];
   noise::zero_acc(acc);
   noise::mma_tile_256(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
                       smem, acc);
@@ -76,69 +81,98 @@ lowrank_gemm_kernel(const GemmArgs g) {
   const int shift = g.r1.member_shift;
   const float* aseg = perturbed ? g.r1.a[seg] : nullptr;
   const int seg_base = perturbed ? seg * g.r1.seg_cols : 0;
-  const int colbase = n0 + wn * 128 + (lane & 31);
+  const int colbase = n0 + wn * 64 + (lane & 31);
+  const bool want_u = MODE == NOISE_EPI_RELU2_BF16 && g.u_next != nullptr;
 
-  float a_val[4] = {0.f, 0.f, 0.f, 0.f}, bn_val[4] = {0.f, 0.f, 0.f, 0.f};
+  float a_val[2] = {0.f, 0.f}, bn_val[2] = {0.f, 0.f};
   if (uniform) {
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
+    for (int ni = 0; ni < 2; ++ni) {
       const int col = colbase + ni * 32;
       if (perturbed) a_val[ni] = aseg[(int64_t)(p0 >> shift) * g.r1.lda + (col - seg_base)];
-      if (MODE == NOISE_EPI_RELU2_BF16 && g.b_next)
-        bn_val[ni] = g.b_next[(int64_t)(p0 >> shift) * g.ld_bnext + col];
+      if (want_u) bn_val[ni] = g.b_next[(int64_t)(p0 >> shift) * g.ld_bnext + col];
     }
   }
 
-  float pd[64];
-  if (MODE == NOISE_EPI_RELU2_BF16) {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) pd[i] = 0.f;
-  }
+  float* stage = reinterpret_cast<float*>(&smem[0][0][0][0]);  // [8 waves][32 rows][SLD] fp32
+  float* wstage = stage + wave * 32 * SLD;
+  constexpr bool OUT_BF16 = MODE == NOISE_EPI_BF16 || MODE == NOISE_EPI_RELU2_BF16;
 
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
+    // (1) rank-1 term + transform of block row mi, staged as fp32 in this wave's LDS slice.
+    float pd[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      const int row = m0 + rl;
-      if (row >= g.M) continue;
+      const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
       const float su = su_s[rl];
       const int pn = (row / T) >> shift;
+      pd[j] = 0.f;
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) {
+      for (int ni = 0; ni < 2; ++ni) {
         const int col = colbase + ni * 32;
         float av = a_val[ni];
         if (!uniform && perturbed) av = aseg[(int64_t)pn * g.r1.lda + (col - seg_base)];
-        const float v = acc[mi][ni][j] + su * av;
-        const int64_t off = (int64_t)row * g.ldc + col;
-        if (MODE == NOISE_EPI_BF16) {
-          reinterpret_cast<uint16_t*>(g.C)[off] = f2bf(v);
-        } else if (MODE == NOISE_EPI_F32) {
-          reinterpret_cast<float*>(g.C)[off] = v;
-        } else if (MODE == NOISE_EPI_ADD_F32) {
-          reinterpret_cast<float*>(g.C)[off] += v;
-        } else {
-          const float r = v > 0.f ? v * v : 0.f;
-          const uint16_t hb = f2bf(r);
-          reinterpret_cast<uint16_t*>(g.C)[off] = hb;
-          float bn = bn_val[ni];
-          if (!uniform && g.b_next) bn = g.b_next[(int64_t)pn * g.ld_bnext + col];
-          pd[mi * 16 + j] += bf2f(hb) * bn;
+        float v = acc[mi][ni][j] + su * av;
+        if (MODE == NOISE_EPI_RELU2_BF16) {
+          v = bf2f(f2bf(v > 0.f ? v * v : 0.f));
+          if (want_u) {
+            float bn = bn_val[ni];
+            if (!uniform) bn = g.b_next[(int64_t)pn * g.ld_bnext + col];
+            pd[j] += v * bn;
+          }
         }
+        wstage[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] = v;
       }
     }
-  }
-
-  if (MODE == NOISE_EPI_RELU2_BF16 && g.u_next) {
-    halfwave_transpose_sum(pd, lane);
-    const int part = (n0 + wn * 128) / 128;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int i = 2 * (lane & 31) + e;
-      const int mi = i >> 4, j = i & 15;
-      const int row = m0 + wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      if (row < g.M) g.u_next[(int64_t)row * g.ld_unext + part] = pd[e];
+    if (want_u) {
+      const float tot = noise::halfwave_transpose_sum16(pd, lane);
+      const int jj = (lane & 31) >> 1;
+      const int row = m0 + wm * 128 + mi * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+      if ((lane & 1) == 0 && row < g.M) g.u_next[(int64_t)row * g.ld_unext + (n0 + wn * 64) / 64] = tot;
     }
+    __syncthreads();
+    // (2) copy-out: this round covers rows wm*128 + mi*32 .. +32 of both row halves, all 256
+    // columns. Chunk id -> (row half h, row r, column c); wave (h, c / 64) staged it.
+    if (OUT_BF16) {
+      uint16_t* C16 = reinterpret_cast<uint16_t*>(g.C);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // 64 rows x 32 chunks of 8 columns
+        const int id = q * NT + tid, rr = id >> 5, c8 = (id & 31) * 8;
+        const int h = rr >> 5, r = rr & 31;
+        const int row = m0 + h * 128 + mi * 32 + r;
+        const float* src = stage + ((h * 4 + (c8 >> 6)) * 32 + r) * SLD + (c8 & 63);
+        const float4 lo = *reinterpret_cast<const float4*>(src);
+        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+        if (row < g.M)
+          *reinterpret_cast<uint4*>(C16 + (int64_t)row * g.ldc + n0 + c8) =
+              make_uint4(pack_bf2(lo.x, lo.y), pack_bf2(lo.z, lo.w), pack_bf2(hi.x, hi.y), pack_bf2(hi.z, hi.w));
+      }
+    } else {
+      float* C32 = reinterpret_cast<float*>(g.C);
+      float4 prev[8];
+      if (MODE == NOISE_EPI_ADD_F32) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {  // 64 rows x 64 chunks of 4 columns
+          const int id = q * NT + tid, rr = id >> 6, c4 = (id & 63) * 4;
+          const int row = m0 + (rr >> 5) * 128 + mi * 32 + (rr & 31);
+          prev[q] = *reinterpret_cast<const float4*>(C32 + (int64_t)(row < g.M ? row : g.M - 1) * g.ldc + n0 + c4);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int id = q * NT + tid, rr = id >> 6, c4 = (id & 63) * 4;
+        const int h = rr >> 5, r = rr & 31;
+        const int row = m0 + h * 128 + mi * 32 + r;
+        float4 v = *reinterpret_cast<const float4*>(stage + ((h * 4 + (c4 >> 6)) * 32 + r) * SLD + (c4 & 63));
+        if (MODE == NOISE_EPI_ADD_F32) {
+          v.x += prev[q].x; v.y += prev[q].y; v.z += prev[q].z; v.w += prev[q].w;
+        }
+        if (row < g.M) *reinterpret_cast<float4*>(C32 + (int64_t)row * g.ldc + n0 + c4) = v;
+      }
+    }
+    if (mi < 3) __syncthreads();  // the copy-out reads are done before the next round writes
   }
 }
 
@@ -156,6 +190,8 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
                 "lowrank_gemm: lda=%lld ldw=%lld must be >= K and multiples of 8", (long long)lda,
                 (long long)ldw);
   NOISE_REQUIRE(ldc >= N, "lowrank_gemm: ldc=%lld < N=%d", (long long)ldc, N);
+  NOISE_REQUIRE(ldc % 8 == 0 && ((uintptr_t)C % 16) == 0,
+                "lowrank_gemm: C must be 16-byte aligned with ldc a multiple of 8");
   NOISE_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0,
                 "lowrank_gemm: A and W must be 16-byte aligned");
   NOISE_REQUIRE(mode >= NOISE_EPI_BF16 && mode <= NOISE_EPI_RELU2_BF16, "lowrank_gemm: bad mode %d", mode);
@@ -187,22 +223,22 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
   NOISE_REQUIRE(!b_next == !u_next, "lowrank_gemm: b_next and u_next go together");
   if (b_next) {
     NOISE_REQUIRE(mode == NOISE_EPI_RELU2_BF16, "lowrank_gemm: b_next/u_next only apply to the relu2 epilogue");
-    NOISE_REQUIRE(ld_unext >= N / 128 && ld_bnext >= N, "lowrank_gemm: ld_unext/ld_bnext too small");
+    NOISE_REQUIRE(ld_unext >= N / 64 && ld_bnext >= N, "lowrank_gemm: ld_unext/ld_bnext too small");
   }
   const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / BN);
   NOISE_REQUIRE(tiles < (1ll << 31), "lowrank_gemm: too many tiles");
   hipStream_t st = (hipStream_t)stream;
   const bool longk = K >= 1024;
   switch (mode) {
-    case NOISE_EPI_BF16: lowrank_gemm_kernel<NOISE_EPI_BF16, false><<<(int)tiles, 256, 0, st>>>(g); break;
-    case NOISE_EPI_F32: lowrank_gemm_kernel<NOISE_EPI_F32, false><<<(int)tiles, 256, 0, st>>>(g); break;
+    case NOISE_EPI_BF16: lowrank_gemm_kernel<NOISE_EPI_BF16, false><<<(int)tiles, NT, 0, st>>>(g); break;
+    case NOISE_EPI_F32: lowrank_gemm_kernel<NOISE_EPI_F32, false><<<(int)tiles, NT, 0, st>>>(g); break;
     case NOISE_EPI_ADD_F32:
       if (longk)
-        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, true><<<(int)tiles, 256, 0, st>>>(g);
+        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, true><<<(int)tiles, NT, 0, st>>>(g);
       else
-        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, false><<<(int)tiles, 256, 0, st>>>(g);
+        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, false><<<(int)tiles, NT, 0, st>>>(g);
       break;
-    default: lowrank_gemm_kernel<NOISE_EPI_RELU2_BF16, false><<<(int)tiles, 256, 0, st>>>(g); break;
+    default: lowrank_gemm_kernel<NOISE_EPI_RELU2_BF16, false><<<(int)tiles, NT, 0, st>>>(g); break;
   }
   return noise::check_launch("lowrank_gemm");
 }

@@ -14,20 +14,21 @@
 
 namespace {
 
-__global__ void __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ void __attribute__((amdgpu_flat_work_group_size(noise::TILE_THREADS, noise::TILE_THREADS),
+                              amdgpu_waves_per_eu(2, 2)))
 head_ce_kernel(const noise_head_t g) {
   __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
   __shared__ float su_s[256];
   __shared__ int tgt_s[256];
   __shared__ float tz_s[256];
-  __shared__ float sum_s[2][256];
+  __shared__ float sum_s[4][256];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int m0 = blockIdx.x * 256;
   const int T = g.T;
   const bool perturbed = g.sign != nullptr;
-  {
+  if (tid < 256) {
     const int row = m0 + tid;
     float su = 0.f;
     int tg = -1;
@@ -44,22 +45,22 @@ head_ce_kernel(const noise_head_t g) {
   const bool uniform = (m0 / T) == (last_row / T);
   const int64_t pn0 = (int64_t)(m0 / T) >> g.member_shift;
 
-  float rsum[2] = {0.f, 0.f};
+  float rsum[4] = {0.f, 0.f, 0.f, 0.f};
   const uint16_t* A = g.h + (int64_t)m0 * 512;
   for (int n0 = 0; n0 < g.V; n0 += 256) {
-    floatx16 acc[4][4];
+    floatx16 acc[4][2];
     noise::zero_acc(acc);
     noise::mma_tile_256(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc);
     noise::mma_tile_256(A, 512, g.M - m0, g.w_lo + (int64_t)n0 * 512, 512, 512, smem, acc);
-    const int colbase = n0 + wn * 128 + (lane & 31);
-    float a_val[4] = {0.f, 0.f, 0.f, 0.f};
+    const int colbase = n0 + wn * 64 + (lane & 31);
+    float a_val[2] = {0.f, 0.f};
     if (perturbed && uniform) {
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) a_val[ni] = g.a[pn0 * g.lda + colbase + ni * 32];
+      for (int ni = 0; ni < 2; ++ni) a_val[ni] = g.a[pn0 * g.lda + colbase + ni * 32];
     }
-    float es[64];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi) {
+      float es[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
@@ -67,7 +68,7 @@ head_ce_kernel(const noise_head_t g) {
         const int tg = tgt_s[rl];
         float e = 0.f;
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
+        for (int ni = 0; ni < 2; ++ni) {
           const int col = colbase + ni * 32;
           float av = a_val[ni];
           if (perturbed && !uniform) {
@@ -79,22 +80,22 @@ head_ce_kernel(const noise_head_t g) {
           e += expf(c);
           if (col == tg) tz_s[rl] = c;
         }
-        es[mi * 16 + j] = e;
+        es[j] = e;
       }
-    halfwave_transpose_sum(es, lane);
-    rsum[0] += es[0];
-    rsum[1] += es[1];
+      rsum[mi] += noise::halfwave_transpose_sum16(es, lane);
+    }
   }
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int i = 2 * (lane & 31) + e;
-    const int mi = i >> 4, j = i & 15;
-    const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    sum_s[wn][rl] = rsum[e];
+  for (int mi = 0; mi < 4; ++mi) {
+    const int jj = (lane & 31) >> 1;
+    const int rl = wm * 128 + mi * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+    if ((lane & 1) == 0) sum_s[wn][rl] = rsum[mi];
   }
   __syncthreads();
-  const int row = m0 + tid;
-  if (row < g.M) g.ce[row] = logf(sum_s[0][tid] + sum_s[1][tid]) - tz_s[tid];
+  if (tid < 256) {
+    const int row = m0 + tid;
+    if (row < g.M) g.ce[row] = logf((sum_s[0][tid] + sum_s[1][tid]) + (sum_s[2][tid] + sum_s[3][tid])) - tz_s[tid];
+  }
 }
 
 }  // namespace
@@ -108,6 +109,6 @@ extern "C" int noise_head_ce(const noise_head_t* args, void* stream) {
   NOISE_REQUIRE(((uintptr_t)g.h % 16) == 0 && ((uintptr_t)g.w_hi % 16) == 0 && ((uintptr_t)g.w_lo % 16) == 0,
                 "head_ce: h and weights must be 16-byte aligned");
   if (g.M == 0) return NOISE_OK;
-  head_ce_kernel<<<(g.M + 255) / 256, 256, 0, (hipStream_t)stream>>>(g);
+  head_ce_kernel<<<(g.M + 255) / 256, noise::TILE_THREADS, 0, (hipStream_t)stream>>>(g);
   return noise::check_launch("head_ce");
 }

@@ -1,87 +1,160 @@
 // 256 x 256 bf16 MFMA tile main loop shared by the perturbed GEMM and the head kernel.
 //
-// acc += A[0:256, 0:K] * B[0:256, 0:K]^T for A, B row-major bf16 with K contiguous. 256 threads
-// (4 waves, 2 x 2); wave (wm, wn) owns rows wm*128.. and columns wn*128.. as 4 x 4 blocks of
-// v_mfma_f32_32x32x16_bf16. Block (mi, ni), accumulator j of lane l holds
-//   row = wm*128 + mi*32 + 8*(j/4) + 4*(l/32) + j%4,   col = wn*128 + ni*32 + l%32.
-// K steps by 64 through two LDS stages with rows padded to 144 B; the next stage's global loads
-// are in flight while the current stage feeds the MFMAs. Rows of A at or beyond `a_rows` are read
-// from row a_rows - 1 (their results are discarded by the caller).
+// acc += A[0:256, 0:K] * B[0:256, 0:K]^T for A, B row-major bf16 with K contiguous. 512 threads
+// = 8 waves (2 x 4), two per SIMD; wave (wm, wn) owns rows wm*128.. and columns wn*64.. as 4 x 2
+// blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane). Block (mi, ni),
+// accumulator j of lane l holds
+//   row = wm*128 + mi*32 + 8*(j/4) + 4*(l/32) + j%4,   col = wn*64 + ni*32 + l%32.
+//
+// Pipeline (measured on MI355X: under load a stage's global loads take longer than its MFMAs,
+// so loads run two stages ahead):
+//   * K advances 32 per stage through two LDS buffers (rows padded to 80 B: the 16-byte
+//     fragment reads of 16 consecutive lanes hit 16 distinct 4-bank groups);
+//   * global loads for stage s+2 are issued at the start of stage s into one of two register
+//     staging sets (16 VGPRs each; the sets alternate by name, never copied: a copy would wait
+//     for the loads in flight) while the other set (stage s+1) drains into LDS at the end of
+//     stage s;
+//   * fragments for k-step 1 are read while the 8 MFMAs of k-step 0 issue; the second wave on
+//     each SIMD fills the MFMA pipe while one waits.
+// Rows of A at or beyond `a_rows` are read from row a_rows - 1 (their results are discarded).
+// K must be a multiple of 64.
 #pragma once
 #include "common.h"
 
 namespace noise {
 
-constexpr int TILE = 256, TBK = 64, TLDK = TBK + 8;
-typedef uint16_t TileSmem[2][2][TILE][TLDK];  // [stage][A|B][row][k]
+constexpr int TILE = 256, TBK = 32, TLDK = TBK + 8;  // 80-byte LDS rows
+constexpr int TILE_THREADS = 512;
+typedef uint16_t TileSmem[2][2][TILE][TLDK];         // [stage][A|B][row][k], 80 KB
 
 NOISE_DEV void mma_tile_256(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
                             const uint16_t* __restrict__ B, int64_t ldb, int K, TileSmem& smem,
-                            floatx16 (&acc)[4][4]) {
+                            floatx16 (&acc)[4][2]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int KT = K / TBK;
-  const int lr = tid >> 3, lc = (tid & 7) * 8;
-  u32x4 ra[8], rb[8];
-  const uint16_t* arow_ptr[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int r = i * 32 + lr;
-    r = r < a_rows ? r : a_rows - 1;
-    arow_ptr[i] = A + (int64_t)r * lda + lc;
+  const int lr = tid >> 2, lc = (tid & 3) * 8;  // 128 rows x 4 chunks of 16 B per pass
+  const uint16_t* arow0;
+  const uint16_t* arow1;
+  {
+    int r0 = lr, r1 = 128 + lr;
+    r0 = r0 < a_rows ? r0 : a_rows - 1;
+    r1 = r1 < a_rows ? r1 : a_rows - 1;
+    arow0 = A + (int64_t)r0 * lda + lc;
+    arow1 = A + (int64_t)r1 * lda + lc;
   }
-  auto gload = [&](int kt) {
-    const int k0 = kt * TBK;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(arow_ptr[i] + k0);
-      rb[i] = *reinterpret_cast<const u32x4*>(B + (int64_t)(i * 32 + lr) * ldb + lc + k0);
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<u32x4*>(&smem[buf][0][i * 32 + lr][lc]) = ra[i];
-      *reinterpret_cast<u32x4*>(&smem[buf][1][i * 32 + lr][lc]) = rb[i];
-    }
-  };
-  gload(0);
+  const uint16_t* brow0 = B + (int64_t)lr * ldb + lc;
+  const uint16_t* brow1 = B + (int64_t)(128 + lr) * ldb + lc;
+  const int arow = wm * 128 + (lane & 31), brow = wn * 64 + (lane & 31), kofs = (lane >> 5) * 8;
+  const uint16_t* fa_base = &smem[0][0][arow][kofs];
+  const uint16_t* fb_base = &smem[0][1][brow][kofs];
+  uint16_t* st_base = &smem[0][0][lr][lc];
+  constexpr int BUF = 2 * TILE * TLDK;  // elements between the two stage buffers
+  constexpr int BOFS = TILE * TLDK;     // elements between the A and B halves of a buffer
+  constexpr int HALF = 128 * TLDK;      // elements between row 0 and row 128
+  bf16x8 a0[4], b0[2], a1[4], b1[2];
+  u32x4 s0[4], s1[4];  // staging sets: [A row lr, A row 128+lr, B row lr, B row 128+lr]
+
+// Unconditional (past the end it re-reads the last stage, in bounds): a guarded load would make
+// the wait before the LDS store conservative on the merged path and drain the prefetch.
+#define NOISE_GLOAD(S, KT_)                                                                   \
+  {                                                                                         \
+    const int k0_ = ((KT_) < KT ? (KT_) : KT - 1) * TBK;                                    \
+    S[0] = *reinterpret_cast<const u32x4*>(arow0 + k0_);                                    \
+    S[1] = *reinterpret_cast<const u32x4*>(arow1 + k0_);                                    \
+    S[2] = *reinterpret_cast<const u32x4*>(brow0 + k0_);                                    \
+    S[3] = *reinterpret_cast<const u32x4*>(brow1 + k0_);                                    \
+  }
+#define NOISE_SSTORE(S, BUF_)                                                                 \
+  {                                                                                         \
+    uint16_t* d_ = st_base + (BUF_) * BUF;                                                  \
+    *reinterpret_cast<u32x4*>(d_) = S[0];                                                   \
+    *reinterpret_cast<u32x4*>(d_ + HALF) = S[1];                                            \
+    *reinterpret_cast<u32x4*>(d_ + BOFS) = S[2];                                            \
+    *reinterpret_cast<u32x4*>(d_ + BOFS + HALF) = S[3];                                     \
+  }
+#define NOISE_FLOAD(FA, FB, BUF_, KOFF)                                                       \
+  {                                                                                         \
+    const uint16_t* pa_ = fa_base + (BUF_) * BUF + (KOFF);                                  \
+    const uint16_t* pb_ = fb_base + (BUF_) * BUF + (KOFF);                                  \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                           \
+      FA[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pa_ + i * 32 * TLDK)); \
+    _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
+      FB[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pb_ + i * 32 * TLDK)); \
+  }
+#define NOISE_MFMA8(FA, FB)                                                                   \
+  _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                          \
+    _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                        \
+      acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FA[mi], FB[ni], acc[mi][ni], 0, 0, 0);
+// Stage KS from LDS buffer CUR (k-step-0 fragments already in a0/b0): stage KS + 2 loads into
+// the free set L; the set S holding stage KS + 1 drains into buffer CUR ^ 1 after the MFMAs.
+#define NOISE_STAGE(KS, CUR, L, S)                                                            \
+  NOISE_GLOAD(L, (KS) + 2)                                                                  \
+  NOISE_FLOAD(a1, b1, CUR, 16)                                                              \
+  NOISE_MFMA8(a0, b0)                                                                       \
+  NOISE_MFMA8(a1, b1)                                                                       \
+  if ((KS) + 1 < KT) NOISE_SSTORE(S, (CUR) ^ 1)                                             \
+  __syncthreads();                                                                          \
+  if ((KS) + 1 < KT) NOISE_FLOAD(a0, b0, (CUR) ^ 1, 0)
+
+  NOISE_GLOAD(s0, 0)
+  NOISE_GLOAD(s1, 1)
   __syncthreads();  // the previous user of smem is done
-  sstore(0);
+  NOISE_SSTORE(s0, 0)
   __syncthreads();
-  const int arow = wm * 128 + (lane & 31), brow = wn * 128 + (lane & 31), kofs = (lane >> 5) * 8;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-#pragma unroll
-    for (int kk = 0; kk < TBK / 16; ++kk) {
-      bf16x8 fa[4], fb[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        fa[mi] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(&smem[cur][0][arow + mi * 32][kk * 16 + kofs]));
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
-        fb[ni] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(&smem[cur][1][brow + ni * 32][kk * 16 + kofs]));
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[mi], fb[ni], acc[mi][ni], 0, 0, 0);
-    }
-    if (kt + 1 < KT) sstore(cur ^ 1);
-    __syncthreads();
+  NOISE_FLOAD(a0, b0, 0, 0)
+  for (int kt = 0; kt < KT; kt += 2) {
+    NOISE_STAGE(kt, 0, s0, s1)
+    NOISE_STAGE(kt + 1, 1, s1, s0)
   }
+#undef NOISE_STAGE
+#undef NOISE_MFMA8
+#undef NOISE_FLOAD
+#undef NOISE_SSTORE
+#undef NOISE_GLOAD
 }
 
-NOISE_DEV void zero_acc(floatx16 (&acc)[4][4]) {
+NOISE_DEV void zero_acc(floatx16 (&acc)[4][2]) {
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
+    for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
+}
+
+// Sum over the 32 lanes of each half-wave of 16 per-lane values; lane q of a half ends with the
+// total of value (q >> 1) & 15 (lanes q and q ^ 1 hold the same total).
+NOISE_DEV float halfwave_transpose_sum16(float (&v)[16], int lane) {
+  const int q = lane & 31;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool up = q & 16;
+    const float send = up ? v[i] : v[i + 8];
+    const float keep = up ? v[i + 8] : v[i];
+    v[i] = keep + __shfl_xor(send, 16, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool up = q & 8;
+    const float send = up ? v[i] : v[i + 4];
+    const float keep = up ? v[i + 4] : v[i];
+    v[i] = keep + __shfl_xor(send, 8, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const bool up = q & 4;
+    const float send = up ? v[i] : v[i + 2];
+    const float keep = up ? v[i + 2] : v[i];
+    v[i] = keep + __shfl_xor(send, 4, 64);
+  }
+  {
+    const bool up = q & 2;
+    const float send = up ? v[0] : v[1];
+    const float keep = up ? v[1] : v[0];
+    v[0] = keep + __shfl_xor(send, 2, 64);
+  }
+  return v[0] + __shfl_xor(v[0], 1, 64);
 }
 
 }  // namespace noise

@@ -13,7 +13,7 @@ Per layer the engine runs (one launch each, all on the current stream):
   attention     y = bf16(softmax_window(q k^T / 8) v); u_o = y.b_o per head
   lowrank_gemm  x += y Wo^T + s u_o a_o^T
   mix_norm      h = bf16(norm x); u_fc = h.b_fc
-  lowrank_gemm  hid = bf16(relu(h Wfc^T + s u a^T)^2); u_mp = hid.b_mp per 128 columns
+  lowrank_gemm  hid = bf16(relu(h Wfc^T + s u a^T)^2); u_mp = hid.b_mp per 64 columns
   lowrank_gemm  x += hid Wmp^T + s u_mp a_mp^T
 then mix_norm (final norm + u_head), head_ce (fp32-accurate head, soft-cap, CE) and member_mean.
 """
@@ -97,7 +97,7 @@ class Workspace:
         self.y = torch.empty(rows, d, **bf)
         self.uproj = torch.empty(rows, cfg.n_head, **f32)
         self.hid = torch.empty(rows, f, **bf)
-        self.umlp = torch.empty(rows, f // 128, **f32)
+        self.umlp = torch.empty(rows, f // 64, **f32)
         self.ce = torch.empty(rows, **f32)
 
 

