@@ -132,17 +132,19 @@ typedef struct {
   int64_t ldqkv;
   uint16_t* y;          /* out [M, 512] bf16 */
   int members, T, heads, window;
-  float scale;          /* 1/sqrt(64) */
+  float scale;          /* 1/sqrt(64); must lie in (0, 0.25] */
   const float* b_proj;  /* c_proj b [noise rows, 512] or NULL: u_proj[r*8 + h] = y_h . b_h */
   int64_t ld_b_proj;
   int member_shift;
   float* u_proj;        /* [M, heads] */
   float* moments;       /* NULL or [members, heads, 2, 64]: mean over t of y and y^2 */
-  float* scratch;       /* moments partials: [members*heads*ceil(T/128), 2, 64] floats */
+  float* scratch;       /* moments partials: [members*heads*ceil(T/256), 2, 64] floats */
 } noise_attention_t;
 
 /* Softmax(q k^T * scale) v over keys s - window .. s (utils/model.py:17-31; eggroll.py:91),
- * plus the per-(member, head) first and second moments of the output over tokens. */
+ * plus the per-(member, head) first and second moments of the output over tokens. The softmax is
+ * shifted by the constant 64 * scale rather than a running maximum: exact (up to bf16 rounding of
+ * the probabilities) for scores -80 < q.k * scale < 96, which unit-rms and N(0, 1) rows satisfy. */
 int noise_window_attention(const noise_attention_t* args, void* stream);
 
 /* ---- RMSNorm'd hidden -> perturbed fp32 head -> soft-cap -> cross-entropy --------------- */

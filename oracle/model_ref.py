@@ -24,7 +24,7 @@ Precision policies:
   'build' -- float64 arithmetic with bfloat16 rounding exactly where the HIP path rounds:
              GEMM inputs (normalised activations, attention inputs and output, relu^2 hidden)
              and the bf16 weight copies of every block matrix, plus the attention probabilities
-             (bf16 per 64-key block under a running max, `window_attention_blocked`); the head
+             (bf16 under a constant softmax shift, `window_attention_shifted`); the head
              weight stays fp32, the residual stream, norms, rank-1 terms, soft-cap and
              log-sum-exp stay full precision;
   'build32' -- the same cast points in float32 arithmetic. |build - build32| measures how far the
@@ -128,31 +128,23 @@ def window_attention(q, k, v, window):
     return (torch.softmax(scores, -1) @ vh).transpose(-3, -2)
 
 
-def window_attention_blocked(q, k, v, window, block=64):
-    """The same attention with the build's probability rounding: keys are visited in 64-aligned
-    blocks; within block b the probabilities exp(s - m_b) (m_b = running max of the scores after
-    block b) are rounded to bf16 before they weight v, then rescaled to the final max; the
-    normaliser sums the unrounded probabilities. Scores are in log2 units (scale * log2 e)."""
+def window_attention_shifted(q, k, v, window, round_p=True):
+    """The same attention with the build's probability rounding: the exponent (in log2 units,
+    scale * log2 e) is shifted by the constant 64 * scale * log2 e -- the largest score unit-rms
+    q and k reach -- instead of by the row maximum; the probabilities exp2(s - shift) are rounded
+    to bf16 before they weight v, and the normaliser sums them unrounded. With the rounding
+    removed (`round_p=False`) this is exactly softmax (shift invariance)."""
     t = q.shape[-3]
     i = torch.arange(t)[:, None]
     j = torch.arange(t)[None, :]
     allowed = (i >= j) & (i - j <= window)
     qh, kh, vh = (z.transpose(-3, -2) for z in (q, k, v))  # [..., H, T, D]
-    s = (qh @ kh.transpose(-1, -2)) * (1.0 / math.sqrt(q.shape[-1]) * math.log2(math.e))
-    s = s.masked_fill(~allowed, float('-inf'))
-    nb = (t + block - 1) // block
-    pad = nb * block - t
-    if pad:
-        s = torch.cat([s, s.new_full(s.shape[:-1] + (pad,), float('-inf'))], -1)
-        vh = torch.cat([vh, vh.new_zeros(vh.shape[:-2] + (pad, vh.shape[-1]))], -2)
-    sb = s.unflatten(-1, (nb, block))                        # [..., H, T, nb, block]
-    run = torch.cummax(sb.amax(-1), -1).values               # running max after each block
-    muse = torch.where(torch.isinf(run), torch.zeros_like(run), run)
-    m_final = muse[..., -1:]
-    p = torch.exp2(sb - muse.unsqueeze(-1))
-    pr = p.to(torch.bfloat16).to(p.dtype) * torch.exp2(muse - m_final).unsqueeze(-1)
-    denom = torch.exp2(sb - m_final.unsqueeze(-1)).sum((-1, -2))
-    out = (pr.flatten(-2) @ vh) / denom.unsqueeze(-1)
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    sl2 = scale * math.log2(math.e)
+    p = torch.exp2((qh @ kh.transpose(-1, -2)) * sl2 - 64.0 * sl2)
+    p = p.masked_fill(~allowed, 0.0)
+    pr = p.to(torch.bfloat16).to(p.dtype) if round_p else p
+    out = (pr @ vh) / p.sum(-1, keepdim=True)
     return out.transpose(-3, -2)
 
 
@@ -239,7 +231,7 @@ def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTC
         q = rb(rms_norm(rotary(q, cos, sin)))
         k = rb(rms_norm(rotary(k, cos, sin)))
         v = rb(v)
-        attend = window_attention_blocked if policy in ('build', 'build32') else window_attention
+        attend = window_attention_shifted if policy in ('build', 'build32') else window_attention
         y = rb(attend(q, k, v, window_sizes(cfg)[i]).reshape(m, length, -1))
         x = x + linear(pre + 'attn.c_proj.weight', y)
         h2 = rb(rms_norm(x))

@@ -178,19 +178,27 @@ def test_rope_norm_ve(device):
     _close_bf16(got[:, 1024:], v)
 
 
-@pytest.mark.parametrize('T,window,members', [(96, 16, 2), (128, 64, 3), (256, 1024, 2), (300, 100, 2), (2048, 1024, 1)])
-def test_window_attention(device, T, window, members):
+@pytest.mark.parametrize('T,window,members,unit', [
+    (96, 16, 2, True), (128, 64, 3, True), (256, 1024, 2, True), (300, 100, 2, True),
+    (2048, 1024, 1, True), (2048, 2048, 1, True), (520, 0, 1, True), (700, 300, 2, False),
+    (2048, 1024, 1, False)])
+def test_window_attention(device, T, window, members, unit):
+    """Against exact softmax attention (bf16 output tolerance) and against the build's rounding
+    model (constant shift, bf16 probabilities); unit-rms q, k as the model feeds them, or raw
+    N(0, 1) rows as in the attention-only workload."""
     g = _gen(T + window)
     M = members * T
-    q = R.rms_norm(torch.randn(M, 8, 64, generator=g)).reshape(M, 512)
-    k = R.rms_norm(torch.randn(M, 8, 64, generator=g)).reshape(M, 512)
+    q = torch.randn(M, 8, 64, generator=g)
+    k = torch.randn(M, 8, 64, generator=g)
+    if unit:
+        q, k = R.rms_norm(q), R.rms_norm(k)
     v = torch.randn(M, 512, generator=g)
-    qkv = _bf(torch.cat([q, k, v], 1))
+    qkv = _bf(torch.cat([q.reshape(M, 512), k.reshape(M, 512), v], 1))
     bp = torch.randn(members, 512, generator=g)
     y = torch.empty(M, 512, dtype=torch.bfloat16, device=device)
     uproj = torch.empty(M, 8, device=device)
     mom = torch.empty(members, 8, 2, 64, device=device)
-    scratch = torch.empty(members * 8 * ((T + 127) // 128) * 128, device=device)
+    scratch = torch.empty(members * 8 * ((T + 255) // 256) * 128, device=device)
     nk.window_attention(qkv.to(device), y, members, T, window, bp.to(device), 0, uproj, mom, scratch)
     qd, kd, vd = (qkv[:, i * 512:(i + 1) * 512].double().view(members, T, 8, 64) for i in range(3))
     ref = R.window_attention(qd, kd, vd, window).reshape(M, 512)
@@ -198,6 +206,8 @@ def test_window_attention(device, T, window, members):
     err = (got - ref).abs()
     assert float(err.max()) < 2e-2 * max(1.0, float(ref.abs().max())), float(err.max())
     assert float(err.mean()) < 2e-3
+    model = R.window_attention_shifted(qd, kd, vd, window).reshape(M, 512)
+    assert float((got - model).abs().max()) < 2 ** -7 * max(1.0, float(model.abs().max()))
     p = torch.arange(M) // T
     torch.testing.assert_close(uproj.cpu().double(), (got * bp[p].double()).view(M, 8, 64).sum(-1), rtol=1e-5, atol=1e-4)
     gy = got.view(members, T, 8, 64)

@@ -144,6 +144,25 @@ def test_window_attention_matches_sdpa():
         torch.testing.assert_close(R.window_attention(q, k, v, w), ref)
 
 
+def test_shifted_attention_is_softmax():
+    """The build's constant softmax shift: exact softmax without the bf16 probability rounding
+    (the shift cancels in the normaliser), bf16-close with it; unit-rms and N(0,1) rows."""
+    g = torch.Generator().manual_seed(3)
+    for unit in (True, False):
+        q, k, v = (torch.randn(2, 130, 3, 64, generator=g, dtype=torch.float64) for _ in range(3))
+        if unit:
+            q, k = R.rms_norm(q), R.rms_norm(k)
+        for w in (0, 7, 64, 200):
+            ref = R.window_attention(q, k, v, w)
+            torch.testing.assert_close(R.window_attention_shifted(q, k, v, w, round_p=False), ref,
+                                       rtol=1e-12, atol=1e-12)
+            err = (R.window_attention_shifted(q, k, v, w) - ref).abs().max()
+            assert float(err) < 2 ** -7 * float(v.abs().max()), float(err)
+            if w == 0:  # one visible key: out = v * bf16(p) / p, within bf16 unit roundoff 2^-8 of v
+                rel = (R.window_attention_shifted(q, k, v, w) - v).abs() / v.abs()
+                assert float(rel.max()) <= 2 ** -8, float(rel.max())
+
+
 def test_norm_and_ce_match_library():
     g = torch.Generator().manual_seed(2)
     x = torch.randn(4, 512, generator=g) * 5
