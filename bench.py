@@ -1,6 +1,7 @@
 """Benchmark: perturbed member-tokens/s of one MI355X on the full EGGROLL population step.
 
     python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
+    python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the MLP pair
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -18,12 +19,16 @@ workload on this host.
 import argparse
 import json
 import os
+import re
 import sys
 import time
+from pathlib import Path
 
 import torch
 
 PEAK_BF16 = 2.5e15  # dense bf16 MFMA, MI355X
+ROOT = Path(__file__).resolve().parent
+TRAFFIC_FILE = ROOT / 'profiles' / 'lowrank_gemm_mlp_pair_traffic.md'
 
 
 def mlp_flops(rows, d=512, f=2048):
@@ -40,6 +45,50 @@ def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 
         per_tok += 2 * d * 3 * d + 2 * d * d + 4 * d * f + 4 * 64 * 8 * keys
     per_tok += 2 * d * V
     return members * T * per_tok
+
+
+def mlp_traffic():
+    """HBM bytes per fused-MLP launch pair measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (scaled by the same counters on a copy of known size), as recorded in the profile summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    m = re.search(r'^traffic_bytes_per_launch_pair:\s*([0-9]+)', TRAFFIC_FILE.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def probe_mlp(rows=512 * 2048, d=512, f=2048, reps=3):
+    """Counter-collection workload: `reps` copies of a 1 GiB fp32 buffer (1 GiB read + 1 GiB
+    written per dispatch), then `reps` fused-MLP launch pairs at the bench shape (512 members x
+    2048 tokens, pair-shared noise rows), with the same kernels and epilogues as the step."""
+    import noise_amd  # noqa: F401  (loads the library)
+    from noise_amd import _lib
+    from noise_amd import kernels as K
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    src = torch.randn(1 << 28, device=dev, generator=g)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    del src, dst
+    members, T = rows // 2048, 2048
+    nrows = members // 2
+    h = torch.randn(rows, d, device=dev, generator=g).bfloat16()
+    w_fc = (torch.randn(f, d, device=dev, generator=g) / d ** 0.5).bfloat16()
+    w_pr = (torch.randn(d, f, device=dev, generator=g) / f ** 0.5).bfloat16()
+    sign = torch.tensor([1e-3, -1e-3], device=dev).repeat(members // 2)
+    a_fc, b_pr = torch.randn(nrows, f, device=dev, generator=g), torch.randn(nrows, f, device=dev, generator=g)
+    a_pr = torch.randn(nrows, d, device=dev, generator=g)
+    u1 = torch.randn(rows, device=dev, generator=g)
+    hid = torch.empty(rows, f, device=dev, dtype=torch.bfloat16)
+    umlp = torch.empty(rows, f // 64, device=dev)
+    x = torch.randn(rows, d, device=dev, generator=g)
+    for _ in range(reps):
+        r1 = K.rank1(sign, T, [a_fc], [u1], 1, 1, 1)
+        K.lowrank_gemm(h, w_fc, r1, _lib.EPI_RELU2_BF16, hid, b_pr, umlp)
+        r1 = K.rank1(sign, T, [a_pr], [umlp], umlp.shape[1], umlp.shape[1], 1)
+        K.lowrank_gemm(hid, w_pr, r1, _lib.EPI_ADD_F32, x)
+    torch.cuda.synchronize()
+    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x MLP pair over {rows} rows', flush=True)
 
 
 def cpu_baseline(seconds_budget=20.0):
@@ -75,11 +124,16 @@ def main():
     ap.add_argument('--tokens', type=int, default=2048)
     ap.add_argument('--chunk', type=int, default=256, help='pairs per batched forward')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    ap.add_argument('--probe-mlp', action='store_true', help='run the counter-collection workload only')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
               'Run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
+
+    if args.probe_mlp:
+        probe_mlp()
+        return
 
     import noise_amd
     from noise_amd.synthetic import sequence
@@ -131,7 +185,7 @@ def main():
                    'members': members, 'pairs': pairs, 'seq_len': T, 'sigma': 1e-3, 'model': '37.7M (8x512, V=4096)',
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
-                     'frac': achieved * 1e12 / PEAK_BF16, 'traffic': None,
+                     'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(),
                      'kernel': 'fused relu^2 MLP: lowrank_gemm<RELU2> (c_fc) + lowrank_gemm<ADD_F32,K=2048> (c_proj)',
                      'flops_per_launch': flops, 'rows_per_launch': rows,
                      'launch_ms': {'c_fc': fc_ms, 'c_proj': mp_ms}},

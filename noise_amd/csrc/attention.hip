@@ -22,8 +22,8 @@
 // normalised and N(0, 1) rows alike. Probabilities are rounded to bf16 for the P V product; the
 // normaliser sums them unrounded.
 //
-// Pipeline: K and V of key block b + 2 are loaded into registers while block b is computed, and
-// stored into the other of two LDS buffers after it: one barrier per 64-key block. Only blocks
+// Pipeline: K and V of key block b + 1 are in flight into registers while block b is computed,
+// and are stored into the other of two LDS buffers after it: one barrier per 64-key block. Only blocks
 // that cross the causal diagonal, the window edge or the end of the sequence evaluate the mask.
 // Workgroups are numbered so that all query blocks of one (member, head) run on one XCD (the
 // hardware deals consecutive workgroup ids round-robin over the 8 XCDs), longest first: that
