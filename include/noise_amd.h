@@ -40,7 +40,7 @@ typedef struct {
   const float* sign;    /* [members] +-sigma; NULL = unperturbed (no rank-1 term) */
   int rows_per_member;  /* T: row r belongs to member r / T */
   int member_shift;     /* noise row of member p = p >> member_shift */
-  int seg_cols;         /* output columns per segment (a multiple of 256) */
+  int seg_cols;         /* output columns per segment (a multiple of 128) */
   int nseg;             /* 1..3 segments side by side (e.g. q | k | v) */
   int u_parts;          /* u of a row = sum of u_parts consecutive floats */
   int64_t lda;          /* row stride of every a[s] (floats) */
@@ -59,7 +59,7 @@ typedef struct {
 /* x W^T + sign (x . b) a^T for A [M, K] bf16 and W [N, K] bf16 (the bf16 weight copy).
  * Replaces `lowrank` (train/val/eggroll.py:56-58) together with the ops fused around it:
  * the residual adds of eggroll.py:92-93 (NOISE_EPI_ADD_F32) and the relu^2 of eggroll.py:93
- * (NOISE_EPI_RELU2_BF16). Requires N % 256 == 0 and K % 64 == 0. */
+ * (NOISE_EPI_RELU2_BF16). Requires N % 128 == 0 and K % 64 == 0. */
 int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
                        int M, int N, int K, const noise_rank1_t* r1, int mode,
                        void* C, int64_t ldc, const float* b_next, int64_t ld_bnext,

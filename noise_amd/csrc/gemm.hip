@@ -5,20 +5,22 @@
 // epilogue. The dot products u = A . b arrive precomputed per row (written by the producer of A),
 // so the rank-1 term costs one FMA per output element.
 //
-// Tiling for gfx950: a 256x256 output tile per workgroup of 8 waves (2 x 4, two per SIMD), each
-// wave owning a 128x64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32
-// accumulators per lane); the K loop is mma_tile_256 (two-stage-ahead global prefetch,
-// double-buffered LDS and fragments). The epilogue runs in four rounds of 32 rows per wave: the
-// rank-1 term and the mode's transform are applied to one accumulator block, the block is staged
-// through LDS as fp32 and written out with 16-byte coalesced accesses (a wave moves 1 KB of
-// contiguous output per instruction). Workgroups are renumbered so that each XCD walks a
-// contiguous run of tiles (neighbouring N tiles share the A rows in that XCD's L2).
+// Tiling for gfx950: a 256 x BN output tile per workgroup of 2 x (BN / 64) waves, each wave
+// owning a 128x64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators
+// per lane); the K loop is mma_tile<BN> (two-stage-ahead global prefetch, double-buffered LDS and
+// fragments). BN = 128 (4 waves, two workgroups per CU: one's barriers and epilogue overlap the
+// other's MFMAs) serves the relu^2 up-projection, whose 4 GiB bf16 epilogue dominates; BN = 256
+// (8 waves, one workgroup per CU, half the L2 -> LDS traffic per FLOP) is measured faster for the
+// fp32-output and long-K shapes.
+// The epilogue runs in four rounds of 32 rows per wave: the rank-1 term and the mode's transform
+// are applied to one accumulator block, the block is staged through LDS as fp32 and written out
+// with 16-byte coalesced accesses. Workgroups are renumbered so that each XCD walks a contiguous
+// run of tiles (neighbouring N tiles share the A rows in that XCD's L2).
 #include "mma_tile.h"
 
 namespace {
 
-constexpr int BM = noise::TILE, BN = noise::TILE, BK = 2 * noise::TBK;
-constexpr int NT = noise::TILE_THREADS;
+constexpr int BM = noise::TILE_M, BK = 2 * noise::TBK;
 constexpr int SLD = 72;  // epilogue staging row stride (floats): the two half-waves of a store
                          // are 4 rows apart = 288 floats = 32 banks apart
 
@@ -39,14 +41,17 @@ struct GemmArgs {
 
 // LONGK marks the K >= 1024 instantiation (the MLP down-projection, K = 2048) so that it is a
 // kernel of its own in profiles; the code is the same.
-template <int MODE, bool LONGK>
-__global__ void __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2, 2)))
+template <int MODE, int BN, bool LONGK>
+__global__ void __attribute__((amdgpu_flat_work_group_size(2 * BN, 2 * BN), amdgpu_waves_per_eu(2, 2)))
 lowrank_gemm_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
+  using Cfg = noise::TileCfg<BN>;
+  constexpr int NT = Cfg::THREADS, WN = BN / 64;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS];
   __shared__ float su_s[BM];
+  static_assert(Cfg::SMEM_ELEMS * 2 >= Cfg::WAVES * 32 * SLD * 4, "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / WN, wn = wave % WN;
   const int ntn = g.N / BN;
   const int ntiles = gridDim.x;
   int bid = blockIdx.x;
@@ -71,7 +76,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
 
   floatx16 acc[4][2];
   noise::zero_acc(acc);
-  noise::mma_tile_256(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
+  noise::mma_tile<BN>(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
                       smem, acc);
 
   // ---- epilogue ----
@@ -94,7 +99,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
     }
   }
 
-  float* stage = reinterpret_cast<float*>(&smem[0][0][0][0]);  // [8 waves][32 rows][SLD] fp32
+  float* stage = reinterpret_cast<float*>(smem);  // [waves][32 rows][SLD] fp32
   float* wstage = stage + wave * 32 * SLD;
   constexpr bool OUT_BF16 = MODE == NOISE_EPI_BF16 || MODE == NOISE_EPI_RELU2_BF16;
 
@@ -133,16 +138,16 @@ lowrank_gemm_kernel(const GemmArgs g) {
       if ((lane & 1) == 0 && row < g.M) g.u_next[(int64_t)row * g.ld_unext + (n0 + wn * 64) / 64] = tot;
     }
     __syncthreads();
-    // (2) copy-out: this round covers rows wm*128 + mi*32 .. +32 of both row halves, all 256
+    // (2) copy-out: this round covers rows wm*128 + mi*32 .. +32 of both row halves, all BN
     // columns. Chunk id -> (row half h, row r, column c); wave (h, c / 64) staged it.
     if (OUT_BF16) {
       uint16_t* C16 = reinterpret_cast<uint16_t*>(g.C);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {  // 64 rows x 32 chunks of 8 columns
-        const int id = q * NT + tid, rr = id >> 5, c8 = (id & 31) * 8;
+      for (int q = 0; q < 4; ++q) {  // 64 rows x BN/8 chunks of 8 columns
+        const int id = q * NT + tid, rr = id / (BN / 8), c8 = (id % (BN / 8)) * 8;
         const int h = rr >> 5, r = rr & 31;
         const int row = m0 + h * 128 + mi * 32 + r;
-        const float* src = stage + ((h * 4 + (c8 >> 6)) * 32 + r) * SLD + (c8 & 63);
+        const float* src = stage + ((h * WN + (c8 >> 6)) * 32 + r) * SLD + (c8 & 63);
         const float4 lo = *reinterpret_cast<const float4*>(src);
         const float4 hi = *reinterpret_cast<const float4*>(src + 4);
         if (row < g.M)
@@ -154,18 +159,18 @@ lowrank_gemm_kernel(const GemmArgs g) {
       float4 prev[8];
       if (MODE == NOISE_EPI_ADD_F32) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {  // 64 rows x 64 chunks of 4 columns
-          const int id = q * NT + tid, rr = id >> 6, c4 = (id & 63) * 4;
+        for (int q = 0; q < 8; ++q) {  // 64 rows x BN/4 chunks of 4 columns
+          const int id = q * NT + tid, rr = id / (BN / 4), c4 = (id % (BN / 4)) * 4;
           const int row = m0 + (rr >> 5) * 128 + mi * 32 + (rr & 31);
           prev[q] = *reinterpret_cast<const float4*>(C32 + (int64_t)(row < g.M ? row : g.M - 1) * g.ldc + n0 + c4);
         }
       }
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int id = q * NT + tid, rr = id >> 6, c4 = (id & 63) * 4;
+        const int id = q * NT + tid, rr = id / (BN / 4), c4 = (id % (BN / 4)) * 4;
         const int h = rr >> 5, r = rr & 31;
         const int row = m0 + h * 128 + mi * 32 + r;
-        float4 v = *reinterpret_cast<const float4*>(stage + ((h * 4 + (c4 >> 6)) * 32 + r) * SLD + (c4 & 63));
+        float4 v = *reinterpret_cast<const float4*>(stage + ((h * WN + (c4 >> 6)) * 32 + r) * SLD + (c4 & 63));
         if (MODE == NOISE_EPI_ADD_F32) {
           v.x += prev[q].x; v.y += prev[q].y; v.z += prev[q].z; v.w += prev[q].w;
         }
@@ -184,7 +189,7 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
                                   int64_t ld_unext, void* stream) {
   NOISE_REQUIRE(A && W && C, "lowrank_gemm: null A, W or C");
   NOISE_REQUIRE(M >= 0 && N > 0 && K > 0, "lowrank_gemm: bad sizes M=%d N=%d K=%d", M, N, K);
-  NOISE_REQUIRE(N % BN == 0, "lowrank_gemm: N=%d must be a multiple of %d", N, BN);
+  NOISE_REQUIRE(N % 128 == 0, "lowrank_gemm: N=%d must be a multiple of 128", N);
   NOISE_REQUIRE(K % BK == 0, "lowrank_gemm: K=%d must be a multiple of %d", K, BK);
   NOISE_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0,
                 "lowrank_gemm: lda=%lld ldw=%lld must be >= K and multiples of 8", (long long)lda,
@@ -208,10 +213,10 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
   g.r1 = r1 ? *r1 : none;
   if (g.r1.sign) {
     NOISE_REQUIRE(g.r1.rows_per_member > 0, "lowrank_gemm: rows_per_member must be > 0");
-    NOISE_REQUIRE(g.r1.nseg >= 1 && g.r1.nseg <= 3 && g.r1.seg_cols % BN == 0 &&
+    NOISE_REQUIRE(g.r1.nseg >= 1 && g.r1.nseg <= 3 && g.r1.seg_cols % 128 == 0 &&
                       g.r1.seg_cols * g.r1.nseg == N,
                   "lowrank_gemm: segments (%d x %d) must tile N=%d in multiples of %d", g.r1.nseg,
-                  g.r1.seg_cols, N, BN);
+                  g.r1.seg_cols, N, 128);
     NOISE_REQUIRE(g.r1.u_parts >= 1 && g.r1.ldu >= g.r1.u_parts, "lowrank_gemm: bad u_parts/ldu");
     NOISE_REQUIRE(g.r1.member_shift >= 0 && g.r1.member_shift < 31, "lowrank_gemm: bad member_shift");
     for (int s = 0; s < g.r1.nseg; ++s)
@@ -225,20 +230,29 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
     NOISE_REQUIRE(mode == NOISE_EPI_RELU2_BF16, "lowrank_gemm: b_next/u_next only apply to the relu2 epilogue");
     NOISE_REQUIRE(ld_unext >= N / 64 && ld_bnext >= N, "lowrank_gemm: ld_unext/ld_bnext too small");
   }
-  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / BN);
+  // 256-column tiles unless the relu^2 epilogue (or N, or a segment) asks for 128.
+  const bool wide = mode != NOISE_EPI_RELU2_BF16 && N % 256 == 0 && (!g.r1.sign || g.r1.seg_cols % 256 == 0);
+  const int bn = wide ? 256 : 128;
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / bn);
   NOISE_REQUIRE(tiles < (1ll << 31), "lowrank_gemm: too many tiles");
   hipStream_t st = (hipStream_t)stream;
   const bool longk = K >= 1024;
+  const dim3 grid((unsigned)tiles);
+#define NOISE_GEMM_LAUNCH(MODE_, BN_, LK_) lowrank_gemm_kernel<MODE_, BN_, LK_><<<grid, 2 * (BN_), 0, st>>>(g)
   switch (mode) {
-    case NOISE_EPI_BF16: lowrank_gemm_kernel<NOISE_EPI_BF16, false><<<(int)tiles, NT, 0, st>>>(g); break;
-    case NOISE_EPI_F32: lowrank_gemm_kernel<NOISE_EPI_F32, false><<<(int)tiles, NT, 0, st>>>(g); break;
-    case NOISE_EPI_ADD_F32:
-      if (longk)
-        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, true><<<(int)tiles, NT, 0, st>>>(g);
-      else
-        lowrank_gemm_kernel<NOISE_EPI_ADD_F32, false><<<(int)tiles, NT, 0, st>>>(g);
+    case NOISE_EPI_BF16:
+      if (wide) NOISE_GEMM_LAUNCH(NOISE_EPI_BF16, 256, false); else NOISE_GEMM_LAUNCH(NOISE_EPI_BF16, 128, false);
       break;
-    default: lowrank_gemm_kernel<NOISE_EPI_RELU2_BF16, false><<<(int)tiles, NT, 0, st>>>(g); break;
+    case NOISE_EPI_F32:
+      if (wide) NOISE_GEMM_LAUNCH(NOISE_EPI_F32, 256, false); else NOISE_GEMM_LAUNCH(NOISE_EPI_F32, 128, false);
+      break;
+    case NOISE_EPI_ADD_F32:
+      if (wide && longk) NOISE_GEMM_LAUNCH(NOISE_EPI_ADD_F32, 256, true);
+      else if (wide) NOISE_GEMM_LAUNCH(NOISE_EPI_ADD_F32, 256, false);
+      else NOISE_GEMM_LAUNCH(NOISE_EPI_ADD_F32, 128, false);
+      break;
+    default: NOISE_GEMM_LAUNCH(NOISE_EPI_RELU2_BF16, 128, false); break;
   }
+#undef NOISE_GEMM_LAUNCH
   return noise::check_launch("lowrank_gemm");
 }

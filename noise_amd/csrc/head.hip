@@ -3,7 +3,8 @@
 // Reference semantics (train/val/eggroll.py:94-102; utils/model.py:203-209): for every member
 // row r, z = h_r (W + s a b^T)^T over the whole vocabulary, z' = 15 tanh(z / 15), and
 // ce_r = logsumexp(z') - z'[target]. The reference materialises [32, T, V] fp32 logits per slice;
-// here a workgroup owns 256 rows and sweeps the vocabulary in 256-column tiles, keeping only
+// here a workgroup (4 waves, two per CU) owns 256 rows and sweeps the vocabulary in 128-column
+// tiles of mma_tile<128>, keeping only
 // per-row running sums of exp(z') (the soft-cap bounds z' to [-15, 15], so no running max is
 // needed in fp32) and the target's z'.
 //
@@ -14,21 +15,27 @@
 
 namespace {
 
-__global__ void __attribute__((amdgpu_flat_work_group_size(noise::TILE_THREADS, noise::TILE_THREADS),
-                              amdgpu_waves_per_eu(2, 2)))
+constexpr int HBN = 128;
+using HCfg = noise::TileCfg<HBN>;
+constexpr int HT = HCfg::THREADS;
+
+// ALIGNED: every 256-row tile lies inside one member (T % 256 == 0), so the rank-1 vector a is one
+// row per tile; the general instantiation reads a per row (and is only used for ragged T).
+template <bool ALIGNED>
+__global__ void __attribute__((amdgpu_flat_work_group_size(HT, HT), amdgpu_waves_per_eu(2, 2)))
 head_ce_kernel(const noise_head_t g) {
-  __shared__ __attribute__((aligned(16))) noise::TileSmem smem;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[HCfg::SMEM_ELEMS];
   __shared__ float su_s[256];
   __shared__ int tgt_s[256];
   __shared__ float tz_s[256];
-  __shared__ float sum_s[4][256];
+  __shared__ float sum_s[2][256];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
   const int m0 = blockIdx.x * 256;
   const int T = g.T;
   const bool perturbed = g.sign != nullptr;
-  if (tid < 256) {
+  {
     const int row = m0 + tid;
     float su = 0.f;
     int tg = -1;
@@ -42,48 +49,64 @@ head_ce_kernel(const noise_head_t g) {
     tz_s[tid] = __builtin_nanf("");  // stays NaN for a row whose target is out of range
   }
   const int last_row = (m0 + 256 < g.M ? m0 + 256 : g.M) - 1;
-  const bool uniform = (m0 / T) == (last_row / T);
+  const bool uniform = ALIGNED || (m0 / T) == (last_row / T);
   const int64_t pn0 = (int64_t)(m0 / T) >> g.member_shift;
 
   float rsum[4] = {0.f, 0.f, 0.f, 0.f};
   const uint16_t* A = g.h + (int64_t)m0 * 512;
-  for (int n0 = 0; n0 < g.V; n0 += 256) {
+  for (int n0 = 0; n0 < g.V; n0 += HBN) {
     floatx16 acc[4][2];
     noise::zero_acc(acc);
-    noise::mma_tile_256(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc);
-    noise::mma_tile_256(A, 512, g.M - m0, g.w_lo + (int64_t)n0 * 512, 512, 512, smem, acc);
+    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc);
+    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_lo + (int64_t)n0 * 512, 512, 512, smem, acc);
     const int colbase = n0 + wn * 64 + (lane & 31);
     float a_val[2] = {0.f, 0.f};
     if (perturbed && uniform) {
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni) a_val[ni] = g.a[pn0 * g.lda + colbase + ni * 32];
     }
+// One logit: rank-1 term, soft-cap 15 tanh(z / 15) = 15 - 30 / (exp(2z / 15) + 1) (exact at both
+// saturations, absolute error a few 1e-7 near z = 0), exp(c) = exp2(c log2 e) into the row sum,
+// and the target's capped logit.
+#define NOISE_HEAD_LOGIT(AV)                                                                   \
+  {                                                                                          \
+    const float z = acc[mi][ni][j] + su * (AV);                                              \
+    const float t = __builtin_amdgcn_exp2f(z * (2.0f / 15.0f * 1.4426950408889634f));        \
+    const float c = __builtin_fmaf(-30.0f, __builtin_amdgcn_rcpf(t + 1.0f), 15.0f);          \
+    e += __builtin_amdgcn_exp2f(c * 1.4426950408889634f);                                    \
+    if (colbase + ni * 32 == tg) tz_s[rl] = c;                                               \
+  }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       float es[16];
+      if (uniform) {  // every row of the tile is one member: a is per column
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        const float su = su_s[rl];
-        const int tg = tgt_s[rl];
-        float e = 0.f;
+        for (int j = 0; j < 16; ++j) {
+          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const float su = su_s[rl];
+          const int tg = tgt_s[rl];
+          float e = 0.f;
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          const int col = colbase + ni * 32;
-          float av = a_val[ni];
-          if (perturbed && !uniform) {
-            const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
-            av = g.a[((int64_t)(row / T) >> g.member_shift) * g.lda + col];
-          }
-          const float z = acc[mi][ni][j] + su * av;
-          const float c = 15.0f * tanhf(z * (1.0f / 15.0f));
-          e += expf(c);
-          if (col == tg) tz_s[rl] = c;
+          for (int ni = 0; ni < 2; ++ni) NOISE_HEAD_LOGIT(a_val[ni])
+          es[j] = e;
         }
-        es[j] = e;
+      } else if (!ALIGNED) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const float su = su_s[rl];
+          const int tg = tgt_s[rl];
+          const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
+          const float* arow = perturbed ? g.a + ((int64_t)(row / T) >> g.member_shift) * g.lda : nullptr;
+          float e = 0.f;
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni) NOISE_HEAD_LOGIT(perturbed ? arow[colbase + ni * 32] : 0.f)
+          es[j] = e;
+        }
       }
       rsum[mi] += noise::halfwave_transpose_sum16(es, lane);
     }
+#undef NOISE_HEAD_LOGIT
   }
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
@@ -92,9 +115,9 @@ head_ce_kernel(const noise_head_t g) {
     if ((lane & 1) == 0) sum_s[wn][rl] = rsum[mi];
   }
   __syncthreads();
-  if (tid < 256) {
+  {
     const int row = m0 + tid;
-    if (row < g.M) g.ce[row] = logf((sum_s[0][tid] + sum_s[1][tid]) + (sum_s[2][tid] + sum_s[3][tid])) - tz_s[tid];
+    if (row < g.M) g.ce[row] = logf(sum_s[0][tid] + sum_s[1][tid]) - tz_s[tid];
   }
 }
 
@@ -109,6 +132,9 @@ extern "C" int noise_head_ce(const noise_head_t* args, void* stream) {
   NOISE_REQUIRE(((uintptr_t)g.h % 16) == 0 && ((uintptr_t)g.w_hi % 16) == 0 && ((uintptr_t)g.w_lo % 16) == 0,
                 "head_ce: h and weights must be 16-byte aligned");
   if (g.M == 0) return NOISE_OK;
-  head_ce_kernel<<<(g.M + 255) / 256, noise::TILE_THREADS, 0, (hipStream_t)stream>>>(g);
+  if (g.T % 256 == 0)
+    head_ce_kernel<true><<<(g.M + 255) / 256, HT, 0, (hipStream_t)stream>>>(g);
+  else
+    head_ce_kernel<false><<<(g.M + 255) / 256, HT, 0, (hipStream_t)stream>>>(g);
   return noise::check_launch("head_ce");
 }

@@ -1,9 +1,10 @@
-// 256 x 256 bf16 MFMA tile main loop shared by the perturbed GEMM and the head kernel.
+// 256 x BN bf16 MFMA tile main loop shared by the perturbed GEMM (BN = 128) and the head kernel
+// (BN = 256).
 //
-// acc += A[0:256, 0:K] * B[0:256, 0:K]^T for A, B row-major bf16 with K contiguous. 512 threads
-// = 8 waves (2 x 4), two per SIMD; wave (wm, wn) owns rows wm*128.. and columns wn*64.. as 4 x 2
-// blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane). Block (mi, ni),
-// accumulator j of lane l holds
+// acc += A[0:256, 0:K] * B[0:BN, 0:K]^T for A, B row-major bf16 with K contiguous. The workgroup
+// has 2 x (BN / 64) waves; wave (wm, wn) owns rows wm*128.. and columns wn*64.. as 4 x 2 blocks
+// of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane). Block (mi, ni), accumulator j of
+// lane l holds
 //   row = wm*128 + mi*32 + 8*(j/4) + 4*(l/32) + j%4,   col = wn*64 + ni*32 + l%32.
 //
 // Pipeline (measured on MI355X: under load a stage's global loads take longer than its MFMAs,
@@ -11,11 +12,12 @@
 //   * K advances 32 per stage through two LDS buffers (rows padded to 80 B: the 16-byte
 //     fragment reads of 16 consecutive lanes hit 16 distinct 4-bank groups);
 //   * global loads for stage s+2 are issued at the start of stage s into one of two register
-//     staging sets (16 VGPRs each; the sets alternate by name, never copied: a copy would wait
-//     for the loads in flight) while the other set (stage s+1) drains into LDS at the end of
-//     stage s;
-//   * fragments for k-step 1 are read while the 8 MFMAs of k-step 0 issue; the second wave on
-//     each SIMD fills the MFMA pipe while one waits.
+//     staging sets (the sets alternate by name, never copied: a copy would wait for the loads in
+//     flight) while the other set (stage s+1) drains into LDS at the end of stage s;
+//   * fragments for k-step 1 are read while the 8 MFMAs of k-step 0 issue.
+// With BN = 128 (4 waves, 60 KB of LDS) two workgroups share a CU, so one workgroup's barrier and
+// epilogue overlap the other's MFMAs (measured: +10% over one 8-wave 256 x 256 workgroup in the
+// main loop alone, more with the epilogue).
 // Rows of A at or beyond `a_rows` are read from row a_rows - 1 (their results are discarded).
 // K must be a multiple of 64.
 #pragma once
@@ -23,55 +25,62 @@
 
 namespace noise {
 
-constexpr int TILE = 256, TBK = 32, TLDK = TBK + 8;  // 80-byte LDS rows
-constexpr int TILE_THREADS = 512;
-typedef uint16_t TileSmem[2][2][TILE][TLDK];         // [stage][A|B][row][k], 80 KB
+constexpr int TILE_M = 256, TBK = 32, TLDK = TBK + 8;  // 80-byte LDS rows
 
-NOISE_DEV void mma_tile_256(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
-                            const uint16_t* __restrict__ B, int64_t ldb, int K, TileSmem& smem,
-                            floatx16 (&acc)[4][2]) {
+template <int BN>
+struct TileCfg {
+  static constexpr int WAVES = 2 * (BN / 64);
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int RP = THREADS / 4;             // rows per global-load pass
+  static constexpr int NA = TILE_M / RP, NB = BN / RP;
+  static constexpr int BOFS = TILE_M * TLDK;         // elements from the A to the B half
+  static constexpr int BUF = (TILE_M + BN) * TLDK;   // elements per stage buffer
+  static constexpr int SMEM_ELEMS = 2 * BUF;
+};
+
+template <int BN>
+NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
+                        const uint16_t* __restrict__ B, int64_t ldb, int K, uint16_t* smem,
+                        floatx16 (&acc)[4][2]) {
+  using C = TileCfg<BN>;
+  constexpr int NA = C::NA, NB = C::NB, RP = C::RP, BUF = C::BUF, BOFS = C::BOFS;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / (BN / 64), wn = wave % (BN / 64);
   const int KT = K / TBK;
-  const int lr = tid >> 2, lc = (tid & 3) * 8;  // 128 rows x 4 chunks of 16 B per pass
-  const uint16_t* arow0;
-  const uint16_t* arow1;
-  {
-    int r0 = lr, r1 = 128 + lr;
-    r0 = r0 < a_rows ? r0 : a_rows - 1;
-    r1 = r1 < a_rows ? r1 : a_rows - 1;
-    arow0 = A + (int64_t)r0 * lda + lc;
-    arow1 = A + (int64_t)r1 * lda + lc;
+  const int lr = tid >> 2, lc = (tid & 3) * 8;  // RP rows x 4 chunks of 16 B per pass
+  const uint16_t* arow[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    int r = lr + i * RP;
+    r = r < a_rows ? r : a_rows - 1;
+    arow[i] = A + (int64_t)r * lda + lc;
   }
-  const uint16_t* brow0 = B + (int64_t)lr * ldb + lc;
-  const uint16_t* brow1 = B + (int64_t)(128 + lr) * ldb + lc;
-  const int arow = wm * 128 + (lane & 31), brow = wn * 64 + (lane & 31), kofs = (lane >> 5) * 8;
-  const uint16_t* fa_base = &smem[0][0][arow][kofs];
-  const uint16_t* fb_base = &smem[0][1][brow][kofs];
-  uint16_t* st_base = &smem[0][0][lr][lc];
-  constexpr int BUF = 2 * TILE * TLDK;  // elements between the two stage buffers
-  constexpr int BOFS = TILE * TLDK;     // elements between the A and B halves of a buffer
-  constexpr int HALF = 128 * TLDK;      // elements between row 0 and row 128
+  const uint16_t* brow = B + (int64_t)lr * ldb + lc;
+  const int64_t bstep = (int64_t)RP * ldb;
+  const int far = wm * 128 + (lane & 31), fbr = wn * 64 + (lane & 31), kofs = (lane >> 5) * 8;
+  const uint16_t* fa_base = smem + far * TLDK + kofs;
+  const uint16_t* fb_base = smem + BOFS + fbr * TLDK + kofs;
+  uint16_t* st_base = smem + lr * TLDK + lc;
   bf16x8 a0[4], b0[2], a1[4], b1[2];
-  u32x4 s0[4], s1[4];  // staging sets: [A row lr, A row 128+lr, B row lr, B row 128+lr]
+  u32x4 s0[NA + NB], s1[NA + NB];  // staging sets: NA rows of A, then NB rows of B
 
 // Unconditional (past the end it re-reads the last stage, in bounds): a guarded load would make
 // the wait before the LDS store conservative on the merged path and drain the prefetch.
 #define NOISE_GLOAD(S, KT_)                                                                   \
   {                                                                                         \
     const int k0_ = ((KT_) < KT ? (KT_) : KT - 1) * TBK;                                    \
-    S[0] = *reinterpret_cast<const u32x4*>(arow0 + k0_);                                    \
-    S[1] = *reinterpret_cast<const u32x4*>(arow1 + k0_);                                    \
-    S[2] = *reinterpret_cast<const u32x4*>(brow0 + k0_);                                    \
-    S[3] = *reinterpret_cast<const u32x4*>(brow1 + k0_);                                    \
+    _Pragma("unroll") for (int i = 0; i < NA; ++i)                                          \
+      S[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0_);                                \
+    _Pragma("unroll") for (int i = 0; i < NB; ++i)                                          \
+      S[NA + i] = *reinterpret_cast<const u32x4*>(brow + i * bstep + k0_);                  \
   }
 #define NOISE_SSTORE(S, BUF_)                                                                 \
   {                                                                                         \
     uint16_t* d_ = st_base + (BUF_) * BUF;                                                  \
-    *reinterpret_cast<u32x4*>(d_) = S[0];                                                   \
-    *reinterpret_cast<u32x4*>(d_ + HALF) = S[1];                                            \
-    *reinterpret_cast<u32x4*>(d_ + BOFS) = S[2];                                            \
-    *reinterpret_cast<u32x4*>(d_ + BOFS + HALF) = S[3];                                     \
+    _Pragma("unroll") for (int i = 0; i < NA; ++i)                                          \
+      *reinterpret_cast<u32x4*>(d_ + i * RP * TLDK) = S[i];                                 \
+    _Pragma("unroll") for (int i = 0; i < NB; ++i)                                          \
+      *reinterpret_cast<u32x4*>(d_ + BOFS + i * RP * TLDK) = S[NA + i];                     \
   }
 #define NOISE_FLOAD(FA, FB, BUF_, KOFF)                                                       \
   {                                                                                         \
@@ -103,6 +112,9 @@ NOISE_DEV void mma_tile_256(const uint16_t* __restrict__ A, int64_t lda, int a_r
   NOISE_SSTORE(s0, 0)
   __syncthreads();
   NOISE_FLOAD(a0, b0, 0, 0)
+  // Not unrolled further even for a constant K: full unrolling makes the compiler precompute
+  // every stage's addresses and spill them.
+#pragma unroll 1
   for (int kt = 0; kt < KT; kt += 2) {
     NOISE_STAGE(kt, 0, s0, s1)
     NOISE_STAGE(kt + 1, 1, s1, s0)

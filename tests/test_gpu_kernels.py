@@ -37,6 +37,8 @@ GEMM_CASES = [
     (768, 1536, 512, 100, 3, 1, 1),      # 3 segments, tiles straddling members, pair rows
     (512, 2048, 512, 512, 1, 1, 0),
     (256, 512, 2048, 128, 1, 16, 1),
+    (300, 128, 128, 64, 1, 1, 0),        # one column tile, row tail
+    (300, 384, 128, 64, 3, 2, 1),        # 128-column segments
 ]
 
 
@@ -93,7 +95,7 @@ def test_lowrank_gemm_unperturbed_and_errors(device):
     nk.lowrank_gemm(A, W, None, _lib.EPI_F32, C)
     torch.testing.assert_close(C.cpu().double(), A.cpu().double() @ W.cpu().double().t(), rtol=1e-5, atol=1e-4)
     with pytest.raises(ValueError):
-        nk.lowrank_gemm(A, W[:100], None, _lib.EPI_F32, C)     # N not a multiple of 256
+        nk.lowrank_gemm(A, W[:100], None, _lib.EPI_F32, C)     # N not a multiple of 128
     with pytest.raises(ValueError):
         nk.lowrank_gemm(A[:, :100], W[:, :100], None, _lib.EPI_F32, C)  # K not a multiple of 64
 

@@ -33,11 +33,11 @@ def test_library_exports_every_declared_symbol():
 
 def test_argument_errors_raise_before_launch():
     lib = _lib.load()
-    # N = 100 is not a multiple of 256: rejected on the host with a ValueError.
+    # N = 100 is not a multiple of 128: rejected on the host with a ValueError.
     fake = C.c_void_p(256)
     st = lib.noise_lowrank_gemm(fake, 64, fake, 64, 10, 100, 64, None, 0, fake, 100, None, 0, None, 0, None)
     assert st == _lib.NOISE_EINVAL
-    with pytest.raises(ValueError, match='multiple of 256'):
+    with pytest.raises(ValueError, match='multiple of 128'):
         _lib.check(st)
     st = lib.noise_embed_norm(fake, 500, 4096, 500, fake, 0, 8, 1, None, None, 0, None, 0, 0, fake, None, None)
     assert st == _lib.NOISE_EINVAL
