@@ -126,6 +126,15 @@ typedef struct {
  * v + gate * lowrank_embed(value_embeds) (eggroll.py:85-89). */
 int noise_rope_norm_ve(const noise_rope_t* args, void* stream);
 
+/* The q|k|v projection with noise_rope_norm_ve fused into its epilogue, without the fp32
+ * intermediate: rope->out [M, 1536] bf16 = rope_norm_ve(A W^T + rank-1) for W = [Wq; Wk; Wv]
+ * [1536, K] bf16 and the three rank-1 segments of r1 (512 columns each). Replaces `lowrank`
+ * (train/val/eggroll.py:56-58) for c_q, c_k, c_v together with apply_rotary_emb + norm
+ * (utils/model.py:55-58; eggroll.py:90) and the value-embedding add (eggroll.py:85-89).
+ * rope->qkv is not read; rope->M must equal M; r1->rows_per_member must equal rope->T. */
+int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M, int K,
+                        const noise_rank1_t* r1, const noise_rope_t* rope, void* stream);
+
 /* ---- windowed causal attention ---------------------------------------------------------- */
 typedef struct {
   const uint16_t* qkv;  /* [M, ldqkv] bf16, q at column 0, k at 512, v at 1024 (head h at h*64) */

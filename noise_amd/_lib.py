@@ -57,6 +57,7 @@ SIGNATURES = {
     'noise_embed_norm': [P, I64, INT, INT, P, I64, INT, INT, P, P, I64, P, I64, INT, P, P, P],
     'noise_mix_norm': [C.POINTER(MixNorm), P],
     'noise_rope_norm_ve': [C.POINTER(Rope), P],
+    'noise_qkv_rope_gemm': [P, I64, P, I64, INT, INT, C.POINTER(Rank1), C.POINTER(Rope), P],
     'noise_window_attention': [C.POINTER(Attention), P],
     'noise_head_ce': [C.POINTER(Head), P],
     'noise_member_mean': [P, INT, INT, P, P],

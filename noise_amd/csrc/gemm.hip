@@ -21,6 +21,10 @@
 namespace {
 
 constexpr int BM = noise::TILE_M, BK = 2 * noise::TBK;
+// Epilogue of the fused q|k|v projection (noise_qkv_rope_gemm only): rotary + RMSNorm on the q
+// and k heads, v + gate * value embedding on the v heads, bf16 out.
+constexpr int EPI_QKV_ROPE = 4;
+constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (F.rms_norm default)
 constexpr int SLD = 72;  // epilogue staging row stride (floats): the two half-waves of a store
                          // are 4 rows apart = 288 floats = 32 banks apart
 
@@ -37,6 +41,7 @@ struct GemmArgs {
   int64_t ld_bnext;
   float* u_next;
   int64_t ld_unext;
+  noise_rope_t rope;  // EPI_QKV_ROPE only (rope.qkv unused: the input is this GEMM's accumulator)
 };
 
 // LONGK marks the K >= 1024 instantiation (the MLP down-projection, K = 2048) so that it is a
@@ -48,6 +53,12 @@ lowrank_gemm_kernel(const GemmArgs g) {
   constexpr int NT = Cfg::THREADS, WN = BN / 64;
   __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS];
   __shared__ float su_s[BM];
+  // EPI_QKV_ROPE per-row data: token position, token id (-1 if out of range), sign * a_ve[token],
+  // and the VE gate of the tile's BN / 64 heads.
+  __shared__ int t_s[BM];
+  __shared__ int tok_s[BM];
+  __shared__ float sa_s[BM];
+  __shared__ float gate_s[BM][BN / 64];
   static_assert(Cfg::SMEM_ELEMS * 2 >= Cfg::WAVES * 32 * SLD * 4, "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -72,6 +83,21 @@ lowrank_gemm_kernel(const GemmArgs g) {
       su = g.r1.sign[row / T] * u;
     }
     su_s[tid] = su;
+    if (MODE == EPI_QKV_ROPE) {
+      const int r = row < g.M ? row : g.M - 1;
+      const int p = r / T, t = r - p * T;
+      t_s[tid] = t;
+      if (n0 >= 1024 && g.rope.gate) {
+        const int64_t tok = g.rope.idx[(int64_t)p * g.rope.idx_stride + t];
+        const bool ok = tok >= 0 && tok < g.rope.vocab;
+        tok_s[tid] = ok ? (int)tok : -1;
+        sa_s[tid] = (ok && g.rope.sign)
+                        ? g.rope.sign[p] * g.rope.ve_a[((int64_t)p >> g.rope.member_shift) * g.rope.ld_ve_a + tok]
+                        : 0.f;
+#pragma unroll
+        for (int hh = 0; hh < WN; ++hh) gate_s[tid][hh] = g.rope.gate[(int64_t)r * 8 + (n0 - 1024) / 64 + hh];
+      }
+    }
   }
 
   floatx16 acc[4][2];
@@ -101,12 +127,77 @@ lowrank_gemm_kernel(const GemmArgs g) {
 
   float* stage = reinterpret_cast<float*>(smem);  // [waves][32 rows][SLD] fp32
   float* wstage = stage + wave * 32 * SLD;
-  constexpr bool OUT_BF16 = MODE == NOISE_EPI_BF16 || MODE == NOISE_EPI_RELU2_BF16;
+  constexpr bool OUT_BF16 = MODE == NOISE_EPI_BF16 || MODE == NOISE_EPI_RELU2_BF16 || MODE == EPI_QKV_ROPE;
 
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     // (1) rank-1 term + transform of block row mi, staged as fp32 in this wave's LDS slice.
     float pd[16];
+    if (MODE == EPI_QKV_ROPE) {
+      // Lane holds dims d = lane % 32 (ni = 0) and d + 32 (ni = 1) of one head for 16 rows: the
+      // rotary pairs (x1, x2) of apply_rotary_emb are the lane's two values.
+      float x[2][16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
+        const float su = su_s[rl];
+        const int pn = (row / T) >> shift;
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          float av = a_val[ni];
+          if (!uniform && perturbed) av = aseg[(int64_t)pn * g.r1.lda + (colbase + ni * 32 - seg_base)];
+          x[ni][j] = acc[mi][ni][j] + su * av;
+        }
+      }
+      if (n0 < 1024) {  // q or k: rotate, then RMS-normalise over the head's 64 dims
+        const int d = lane & 31;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const int t = t_s[rl];
+          const float cs = g.rope.cos[(int64_t)t * 32 + d], sn = g.rope.sin[(int64_t)t * 32 + d];
+          const float o1 = x[0][j] * cs + x[1][j] * sn;
+          const float o2 = x[0][j] * -sn + x[1][j] * cs;
+          x[0][j] = o1;
+          x[1][j] = o2;
+          pd[j] = o1 * o1 + o2 * o2;
+        }
+        const float tot = noise::halfwave_transpose_sum16(pd, lane);  // row (lane/2) % 16 of the half
+        const float rr = rsqrtf(tot * (1.0f / 64) + RMS_EPS);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float r = __shfl(rr, (lane & 32) + 2 * j, 64);
+          x[0][j] *= r;
+          x[1][j] *= r;
+        }
+      } else if (g.rope.gate) {  // v + gate * (table[token] + sign a_ve[token] b_ve)
+        const int vh = (n0 - 1024) / 64 + wn;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
+          const int tok = tok_s[rl];
+          const float gt = gate_s[rl][wn], sa = sa_s[rl];
+          const int64_t pn = (int64_t)(row / T) >> g.rope.member_shift;
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni) {
+            const int c = vh * 64 + ni * 32 + (lane & 31);
+            float ve = __builtin_nanf("");
+            if (tok >= 0) {
+              ve = g.rope.ve_table[(int64_t)tok * 512 + c];
+              if (g.rope.sign) ve += sa * g.rope.ve_b[pn * g.rope.ld_ve_b + c];
+            }
+            x[ni][j] += gt * ve;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          wstage[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] = x[ni][j];
+    } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
@@ -130,6 +221,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
         }
         wstage[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] = v;
       }
+    }
     }
     if (want_u) {
       const float tot = noise::halfwave_transpose_sum16(pd, lane);
@@ -181,12 +273,9 @@ lowrank_gemm_kernel(const GemmArgs g) {
   }
 }
 
-}  // namespace
-
-extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
-                                  int M, int N, int K, const noise_rank1_t* r1, int mode, void* C,
-                                  int64_t ldc, const float* b_next, int64_t ld_bnext, float* u_next,
-                                  int64_t ld_unext, void* stream) {
+// Validates the arguments shared by both entry points and fills g (everything but the rope part).
+int prepare_gemm(GemmArgs& g, const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M,
+                 int N, int K, const noise_rank1_t* r1, void* C, int64_t ldc, int T_unperturbed) {
   NOISE_REQUIRE(A && W && C, "lowrank_gemm: null A, W or C");
   NOISE_REQUIRE(M >= 0 && N > 0 && K > 0, "lowrank_gemm: bad sizes M=%d N=%d K=%d", M, N, K);
   NOISE_REQUIRE(N % 128 == 0, "lowrank_gemm: N=%d must be a multiple of 128", N);
@@ -199,14 +288,10 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
                 "lowrank_gemm: C must be 16-byte aligned with ldc a multiple of 8");
   NOISE_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)W % 16) == 0,
                 "lowrank_gemm: A and W must be 16-byte aligned");
-  NOISE_REQUIRE(mode >= NOISE_EPI_BF16 && mode <= NOISE_EPI_RELU2_BF16, "lowrank_gemm: bad mode %d", mode);
-  if (M == 0) return NOISE_OK;
-  GemmArgs g;
+  g = GemmArgs{};
   g.A = A; g.lda = lda; g.W = W; g.ldw = ldw; g.M = M; g.N = N; g.K = K;
-  g.C = C; g.ldc = ldc; g.b_next = b_next; g.ld_bnext = ld_bnext; g.u_next = u_next;
-  g.ld_unext = ld_unext;
+  g.C = C; g.ldc = ldc;
   noise_rank1_t none = {};
-  none.rows_per_member = M;
   none.seg_cols = N;
   none.nseg = 1;
   none.u_parts = 1;
@@ -223,21 +308,36 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
       NOISE_REQUIRE(g.r1.a[s] && g.r1.u[s], "lowrank_gemm: null a/u for segment %d", s);
     NOISE_REQUIRE(g.r1.lda >= g.r1.seg_cols, "lowrank_gemm: r1.lda < seg_cols");
   } else {
-    g.r1.rows_per_member = M;
+    g.r1.rows_per_member = T_unperturbed;
   }
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / 128);
+  NOISE_REQUIRE(tiles < (1ll << 31), "lowrank_gemm: too many tiles");
+  return NOISE_OK;
+}
+
+}  // namespace
+
+extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
+                                  int M, int N, int K, const noise_rank1_t* r1, int mode, void* C,
+                                  int64_t ldc, const float* b_next, int64_t ld_bnext, float* u_next,
+                                  int64_t ld_unext, void* stream) {
+  NOISE_REQUIRE(mode >= NOISE_EPI_BF16 && mode <= NOISE_EPI_RELU2_BF16, "lowrank_gemm: bad mode %d", mode);
+  GemmArgs g;
+  int rc = prepare_gemm(g, A, lda, W, ldw, M, N, K, r1, C, ldc, M > 0 ? M : 1);
+  if (rc) return rc;
   NOISE_REQUIRE(!b_next == !u_next, "lowrank_gemm: b_next and u_next go together");
   if (b_next) {
     NOISE_REQUIRE(mode == NOISE_EPI_RELU2_BF16, "lowrank_gemm: b_next/u_next only apply to the relu2 epilogue");
     NOISE_REQUIRE(ld_unext >= N / 64 && ld_bnext >= N, "lowrank_gemm: ld_unext/ld_bnext too small");
   }
+  g.b_next = b_next; g.ld_bnext = ld_bnext; g.u_next = u_next; g.ld_unext = ld_unext;
+  if (M == 0) return NOISE_OK;
   // 256-column tiles unless the relu^2 epilogue (or N, or a segment) asks for 128.
   const bool wide = mode != NOISE_EPI_RELU2_BF16 && N % 256 == 0 && (!g.r1.sign || g.r1.seg_cols % 256 == 0);
   const int bn = wide ? 256 : 128;
-  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (N / bn);
-  NOISE_REQUIRE(tiles < (1ll << 31), "lowrank_gemm: too many tiles");
+  const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (N / bn)));
   hipStream_t st = (hipStream_t)stream;
   const bool longk = K >= 1024;
-  const dim3 grid((unsigned)tiles);
 #define NOISE_GEMM_LAUNCH(MODE_, BN_, LK_) lowrank_gemm_kernel<MODE_, BN_, LK_><<<grid, 2 * (BN_), 0, st>>>(g)
   switch (mode) {
     case NOISE_EPI_BF16:
@@ -255,4 +355,24 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
   }
 #undef NOISE_GEMM_LAUNCH
   return noise::check_launch("lowrank_gemm");
+}
+
+extern "C" int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M,
+                                   int K, const noise_rank1_t* r1, const noise_rope_t* rope, void* stream) {
+  NOISE_REQUIRE(rope && rope->out && rope->cos && rope->sin, "qkv_rope_gemm: null rope, out or tables");
+  const noise_rope_t& rp = *rope;
+  NOISE_REQUIRE(rp.M == M && rp.T > 0, "qkv_rope_gemm: rope.M=%d must equal M=%d, T=%d > 0", rp.M, M, rp.T);
+  NOISE_REQUIRE(!r1 || !r1->sign || r1->rows_per_member == rp.T,
+                "qkv_rope_gemm: rank-1 rows_per_member must equal rope.T");
+  NOISE_REQUIRE(!rp.gate || (rp.ve_table && rp.idx && rp.vocab > 0 && rp.member_shift >= 0 &&
+                             (!rp.sign || (rp.ve_a && rp.ve_b && rp.ld_ve_a >= rp.vocab && rp.ld_ve_b >= 512))),
+                "qkv_rope_gemm: value embedding needs table, idx, vocab and (perturbed) ve_a/ve_b");
+  GemmArgs g;
+  int rc = prepare_gemm(g, A, lda, W, ldw, M, 1536, K, r1, rp.out, 1536, rp.T);
+  if (rc) return rc;
+  g.rope = rp;
+  if (M == 0) return NOISE_OK;
+  const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (1536 / 128)));
+  lowrank_gemm_kernel<EPI_QKV_ROPE, 128, false><<<grid, 256, 0, (hipStream_t)stream>>>(g);
+  return noise::check_launch("qkv_rope_gemm");
 }

@@ -124,10 +124,8 @@ def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_
     _lib.call('noise_mix_norm', C.byref(g), _stream())
 
 
-def rope_norm_ve(qkv32, out16, T, cos, sin, sign=None, gate=None, ve_table=None, idx=None, ve_nz=None,
-                 idx_stride=0):
-    g = Rope()
-    g.qkv, g.out, g.M, g.T = qkv32.data_ptr(), out16.data_ptr(), qkv32.shape[0], T
+def _rope_args(g, T, cos, sin, sign, gate, ve_table, idx, ve_nz, idx_stride):
+    g.T = T
     g.cos, g.sin = cos.data_ptr(), sin.data_ptr()
     if gate is not None:
         g.gate, g.ve_table, g.idx, g.idx_stride, g.vocab = (gate.data_ptr(), ve_table.data_ptr(),
@@ -137,6 +135,31 @@ def rope_norm_ve(qkv32, out16, T, cos, sin, sign=None, gate=None, ve_table=None,
             g.member_shift = ve_nz.shift
             g.ve_a, g.ve_b = ve_nz.a.data_ptr(), ve_nz.b.data_ptr()
             g.ld_ve_a, g.ld_ve_b = ve_nz.a.stride(0), ve_nz.b.stride(0)
+    return g
+
+
+def qkv_rope_gemm(A, W, r1, out16, T, cos, sin, sign=None, gate=None, ve_table=None, idx=None, ve_nz=None,
+                  idx_stride=0):
+    """out16 [M, 1536] bf16 = rope_norm_ve(A W^T + rank-1) in one launch (W = [Wq; Wk; Wv])."""
+    _on_gpu(A, W, out16, cos, sin, gate, ve_table, idx)
+    M, K = A.shape
+    _need(W.shape[0] == 1536 and W.shape[1] == K, 'qkv_rope_gemm: W must be [1536, K]')
+    _need(out16.dtype == torch.bfloat16 and tuple(out16.shape) == (M, 1536) and out16.is_contiguous(),
+          'qkv_rope_gemm: out must be a contiguous [M, 1536] bf16 tensor')
+    lda = _rows(A, K, torch.bfloat16, 'A')
+    ldw = _rows(W, K, torch.bfloat16, 'W')
+    g = Rope()
+    g.out, g.M = out16.data_ptr(), M
+    _rope_args(g, T, cos, sin, sign, gate, ve_table, idx, ve_nz, idx_stride)
+    _lib.call('noise_qkv_rope_gemm', _ptr(A), lda, _ptr(W), ldw, M, K,
+              C.byref(r1) if r1 is not None else None, C.byref(g), _stream())
+
+
+def rope_norm_ve(qkv32, out16, T, cos, sin, sign=None, gate=None, ve_table=None, idx=None, ve_nz=None,
+                 idx_stride=0):
+    g = Rope()
+    g.qkv, g.out, g.M = qkv32.data_ptr(), out16.data_ptr(), qkv32.shape[0]
+    _rope_args(g, T, cos, sin, sign, gate, ve_table, idx, ve_nz, idx_stride)
     _lib.call('noise_rope_norm_ve', C.byref(g), _stream())
 
 

@@ -8,8 +8,8 @@ the one sequence idx -> targets. `noise` maps a matrix/embedding name to (a [m, 
 
 Per layer the engine runs (one launch each, all on the current stream):
   mix_norm      x = (lr + s er) x + (l0 + s e0) x0; h = bf16(norm x); u_q,k,v = h.b; VE gate
-  lowrank_gemm  [q|k|v] = h Wqkv^T + s u a^T                                  (fp32 out)
-  rope_norm_ve  q, k = bf16(norm(rot(.))); v = bf16(v + gate ve)
+  qkv_rope_gemm [q|k|v] = h Wqkv^T + s u a^T, then in the epilogue
+                q, k = bf16(norm(rot(.))); v = bf16(v + gate ve)
   attention     y = bf16(softmax_window(q k^T / 8) v); u_o = y.b_o per head
   lowrank_gemm  x += y Wo^T + s u_o a_o^T
   mix_norm      h = bf16(norm x); u_fc = h.b_fc
@@ -92,7 +92,6 @@ class Workspace:
         self.u3 = torch.empty(rows, 3, **f32)
         self.u1 = torch.empty(rows, **f32)
         self.gate = torch.empty(rows, cfg.n_kv_head, **f32)
-        self.qkv32 = torch.empty(rows, 3 * d, **f32)
         self.qkv16 = torch.empty(rows, 3 * d, **bf)
         self.y = torch.empty(rows, d, **bf)
         self.uproj = torch.empty(rows, cfg.n_head, **f32)
@@ -141,7 +140,7 @@ class Engine:
         M = members * T
         ws = self.workspace(M)
         x, x0, h, u3, u1 = ws.x[:M], ws.x0[:M], ws.h[:M], ws.u3[:M], ws.u1[:M]
-        gate, qkv32, qkv16, y = ws.gate[:M], ws.qkv32[:M], ws.qkv16[:M], ws.y[:M]
+        gate, qkv16, y = ws.gate[:M], ws.qkv16[:M], ws.y[:M]
         uproj, hid, umlp, ce = ws.uproj[:M], ws.hid[:M], ws.umlp[:M], ws.ce[:M]
         cos, sin = self.rotary(T)
         pert = sign is not None
@@ -164,10 +163,9 @@ class Engine:
                        gate_w=W.gate(i) if ve else None, gate_nz=g(pre + 'attn.ve_gate.weight') if ve else None,
                        gate=gate)
             r1 = K.rank1(sign, T, [q.a, k.a, v.a], [u3[:, 0], u3[:, 1], u3[:, 2]], 1, 3, shift) if pert else None
-            K.lowrank_gemm(h, W.qkv[i], r1, _lib.EPI_F32, qkv32)
-            K.rope_norm_ve(qkv32, qkv16, T, cos, sin, sign, gate if ve else None,
-                           W.table(f'value_embeds.{i}.weight') if ve else None, idx,
-                           g(f'value_embeds.{i}.weight') if ve else None, idx_stride)
+            K.qkv_rope_gemm(h, W.qkv[i], r1, qkv16, T, cos, sin, sign, gate if ve else None,
+                            W.table(f'value_embeds.{i}.weight') if ve else None, idx,
+                            g(f'value_embeds.{i}.weight') if ve else None, idx_stride)
             K.window_attention(qkv16, y, members, T, wins[i], o.b if pert else None, shift,
                                uproj if pert else None)
             r1 = K.rank1(sign, T, [o.a], [uproj], cfg.n_head, cfg.n_head, shift) if pert else None

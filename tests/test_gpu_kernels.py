@@ -180,6 +180,38 @@ def test_rope_norm_ve(device):
     _close_bf16(got[:, 1024:], v)
 
 
+@pytest.mark.parametrize('T,members,shift,ve,pert', [
+    (256, 4, 1, True, True), (100, 5, 0, True, True), (2048, 1, 0, False, True), (64, 8, 1, True, False),
+    (300, 2, 1, False, False)])
+def test_qkv_rope_gemm_matches_unfused(device, T, members, shift, ve, pert):
+    """The fused q|k|v projection equals lowrank_gemm (fp32 out) followed by rope_norm_ve on the
+    same inputs: the same fp32 arithmetic up to the order of the norm's sum of squares."""
+    g = _gen(T * 7 + members)
+    M, K, V = T * members, 512, 4096
+    rows = (members >> shift) + 1
+    A = _bf(torch.randn(M, K, generator=g)).to(device)
+    W = _bf(torch.randn(1536, K, generator=g) / math.sqrt(K)).to(device)
+    sign = (torch.randn(members, generator=g) * 0.3).to(device) if pert else None
+    a = [torch.randn(rows, 512, generator=g).to(device) for _ in range(3)]
+    u = [torch.randn(M, 1, generator=g).to(device) for _ in range(3)]
+    r1 = nk.rank1(sign, T, a, u, 1, 1, shift) if pert else None
+    cos, sin = (x.to(device) for x in R.rotary_tables(T))
+    gate = (torch.rand(M, 8, generator=g) * 2).to(device) if ve else None
+    table = torch.randn(V, 512, generator=g).to(device)
+    idx = torch.randint(0, V, (T,), generator=g).to(device)
+    nz = NoiseRows(a=torch.randn(rows, V, generator=g).to(device), b=torch.randn(rows, 512, generator=g).to(device),
+                   shift=shift)
+    fused = torch.empty(M, 1536, dtype=torch.bfloat16, device=device)
+    nk.qkv_rope_gemm(A, W, r1, fused, T, cos, sin, sign, gate, table if ve else None, idx, nz if ve else None)
+    qkv32 = torch.empty(M, 1536, device=device)
+    nk.lowrank_gemm(A, W, nk.rank1(sign, T, a, u, 1, 1, shift) if pert else None, _lib.EPI_F32, qkv32)
+    ref = torch.empty(M, 1536, dtype=torch.bfloat16, device=device)
+    nk.rope_norm_ve(qkv32, ref, T, cos, sin, sign, gate, table if ve else None, idx, nz if ve else None)
+    got, want = fused.cpu().double(), ref.cpu().double()
+    assert float((got == want).double().mean()) >= 0.99
+    assert float((got - want).abs().max()) <= 2 ** -7 * max(1.0, float(want.abs().max()))
+
+
 @pytest.mark.parametrize('T,window,members,unit', [
     (96, 16, 2, True), (128, 64, 3, True), (256, 1024, 2, True), (300, 100, 2, True),
     (2048, 1024, 1, True), (2048, 2048, 1, True), (520, 0, 1, True), (700, 300, 2, False),
