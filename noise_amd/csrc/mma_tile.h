@@ -99,6 +99,7 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
 // the free set L; the set S holding stage KS + 1 drains into buffer CUR ^ 1 after the MFMAs.
 #define NOISE_STAGE(KS, CUR, L, S)                                                            \
   NOISE_GLOAD(L, (KS) + 2)                                                                  \
+  __builtin_amdgcn_sched_barrier(0);                                                        \
   NOISE_FLOAD(a1, b1, CUR, 16)                                                              \
   NOISE_MFMA8(a0, b0)                                                                       \
   NOISE_MFMA8(a1, b1)                                                                       \
