@@ -51,15 +51,17 @@ __global__ void __attribute__((amdgpu_flat_work_group_size(2 * BN, 2 * BN), amdg
 lowrank_gemm_kernel(const GemmArgs g) {
   using Cfg = noise::TileCfg<BN>;
   constexpr int NT = Cfg::THREADS, WN = BN / 64;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS];
+  // The main loop's stage buffers, reused by the epilogue's fp32 staging (whichever is larger).
+  constexpr int STAGE_ELEMS = Cfg::WAVES * 32 * SLD * 2;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS > STAGE_ELEMS ? Cfg::SMEM_ELEMS : STAGE_ELEMS];
   __shared__ float su_s[BM];
+  __shared__ int pn_s[BM];  // noise row (member >> member_shift) of each tile row
   // EPI_QKV_ROPE per-row data: token position, token id (-1 if out of range), sign * a_ve[token],
   // and the VE gate of the tile's BN / 64 heads.
   __shared__ int t_s[BM];
   __shared__ int tok_s[BM];
   __shared__ float sa_s[BM];
   __shared__ float gate_s[BM][BN / 64];
-  static_assert(Cfg::SMEM_ELEMS * 2 >= Cfg::WAVES * 32 * SLD * 4, "epilogue staging fits the tile buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -83,6 +85,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
       su = g.r1.sign[row / T] * u;
     }
     su_s[tid] = su;
+    pn_s[tid] = ((row < g.M ? row : g.M - 1) / T) >> g.r1.member_shift;
     if (MODE == EPI_QKV_ROPE) {
       const int r = row < g.M ? row : g.M - 1;
       const int p = r / T, t = r - p * T;
@@ -107,56 +110,60 @@ lowrank_gemm_kernel(const GemmArgs g) {
 
   // ---- epilogue ----
   const int last_row = (m0 + BM < g.M ? m0 + BM : g.M) - 1;
-  const bool uniform = (m0 / T) == (last_row / T);
-  const int p0 = m0 / T;
-  const int shift = g.r1.member_shift;
+  const bool uniform = (m0 / T) == (last_row / T);  // one member (one noise row) per tile
   const float* aseg = perturbed ? g.r1.a[seg] : nullptr;
   const int seg_base = perturbed ? seg * g.r1.seg_cols : 0;
   const int colbase = n0 + wn * 64 + (lane & 31);
   const bool want_u = MODE == NOISE_EPI_RELU2_BF16 && g.u_next != nullptr;
 
+  // Uniform tiles: a and b_next are one value per column for the whole tile.
   float a_val[2] = {0.f, 0.f}, bn_val[2] = {0.f, 0.f};
   if (uniform) {
+    const int64_t pn = pn_s[0];
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
       const int col = colbase + ni * 32;
-      if (perturbed) a_val[ni] = aseg[(int64_t)(p0 >> shift) * g.r1.lda + (col - seg_base)];
-      if (want_u) bn_val[ni] = g.b_next[(int64_t)(p0 >> shift) * g.ld_bnext + col];
+      if (perturbed) a_val[ni] = aseg[pn * g.r1.lda + (col - seg_base)];
+      if (want_u) bn_val[ni] = g.b_next[pn * g.ld_bnext + col];
     }
   }
 
   float* stage = reinterpret_cast<float*>(smem);  // [waves][32 rows][SLD] fp32
-  float* wstage = stage + wave * 32 * SLD;
+  float* wstage = stage + wave * 32 * SLD + 4 * (lane >> 5) * SLD + (lane & 31);
   constexpr bool OUT_BF16 = MODE == NOISE_EPI_BF16 || MODE == NOISE_EPI_RELU2_BF16 || MODE == EPI_QKV_ROPE;
+
+// Tile row of accumulator j in block row mi, and its rank-1 value x = acc + sign u a.
+#define NOISE_RL(J) (wm * 128 + mi * 32 + 8 * ((J) >> 2) + 4 * (lane >> 5) + ((J) & 3))
+#define NOISE_RANK1(X)                                                                          \
+  if (uniform) {                                                                              \
+    _Pragma("unroll") for (int j = 0; j < 16; ++j) {                                          \
+      const float su = su_s[NOISE_RL(j)];                                                     \
+      _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) X[ni][j] = acc[mi][ni][j] + su * a_val[ni]; \
+    }                                                                                         \
+  } else {                                                                                    \
+    _Pragma("unroll") for (int j = 0; j < 16; ++j) {                                          \
+      const float su = su_s[NOISE_RL(j)];                                                     \
+      const float* ar = perturbed ? aseg + (int64_t)pn_s[NOISE_RL(j)] * g.r1.lda - seg_base : nullptr; \
+      _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                        \
+        X[ni][j] = acc[mi][ni][j] + (perturbed ? su * ar[colbase + ni * 32] : 0.f);           \
+    }                                                                                         \
+  }
 
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     // (1) rank-1 term + transform of block row mi, staged as fp32 in this wave's LDS slice.
+    float x[2][16];
     float pd[16];
+    NOISE_RANK1(x)
     if (MODE == EPI_QKV_ROPE) {
       // Lane holds dims d = lane % 32 (ni = 0) and d + 32 (ni = 1) of one head for 16 rows: the
       // rotary pairs (x1, x2) of apply_rotary_emb are the lane's two values.
-      float x[2][16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
-        const float su = su_s[rl];
-        const int pn = (row / T) >> shift;
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          float av = a_val[ni];
-          if (!uniform && perturbed) av = aseg[(int64_t)pn * g.r1.lda + (colbase + ni * 32 - seg_base)];
-          x[ni][j] = acc[mi][ni][j] + su * av;
-        }
-      }
       if (n0 < 1024) {  // q or k: rotate, then RMS-normalise over the head's 64 dims
         const int d = lane & 31;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-          const int t = t_s[rl];
-          const float cs = g.rope.cos[(int64_t)t * 32 + d], sn = g.rope.sin[(int64_t)t * 32 + d];
+          const int t = t_s[NOISE_RL(j)];
+          const float cs = g.rope.cos[t * 32 + d], sn = g.rope.sin[t * 32 + d];
           const float o1 = x[0][j] * cs + x[1][j] * sn;
           const float o2 = x[0][j] * -sn + x[1][j] * cs;
           x[0][j] = o1;
@@ -173,56 +180,46 @@ lowrank_gemm_kernel(const GemmArgs g) {
         }
       } else if (g.rope.gate) {  // v + gate * (table[token] + sign a_ve[token] b_ve)
         const int vh = (n0 - 1024) / 64 + wn;
+        const int c0 = vh * 64 + (lane & 31);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-          const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
+          const int rl = NOISE_RL(j);
           const int tok = tok_s[rl];
           const float gt = gate_s[rl][wn], sa = sa_s[rl];
-          const int64_t pn = (int64_t)(row / T) >> g.rope.member_shift;
+          const float* bv = g.rope.sign ? g.rope.ve_b + (int64_t)pn_s[rl] * g.rope.ld_ve_b + c0 : nullptr;
+          const float* tv = g.rope.ve_table + (int64_t)(tok >= 0 ? tok : 0) * 512 + c0;
 #pragma unroll
           for (int ni = 0; ni < 2; ++ni) {
-            const int c = vh * 64 + ni * 32 + (lane & 31);
-            float ve = __builtin_nanf("");
-            if (tok >= 0) {
-              ve = g.rope.ve_table[(int64_t)tok * 512 + c];
-              if (g.rope.sign) ve += sa * g.rope.ve_b[pn * g.rope.ld_ve_b + c];
-            }
+            float ve = tok >= 0 ? tv[ni * 32] : __builtin_nanf("");
+            if (g.rope.sign) ve += sa * bv[ni * 32];
             x[ni][j] += gt * ve;
           }
         }
       }
+    } else if (MODE == NOISE_EPI_RELU2_BF16) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < 16; ++j) {
+        pd[j] = 0.f;
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          wstage[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] = x[ni][j];
-    } else {
+        for (int ni = 0; ni < 2; ++ni) x[ni][j] = bf2f(f2bf(x[ni][j] > 0.f ? x[ni][j] * x[ni][j] : 0.f));
+      }
+      if (want_u) {
+        if (uniform) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      const int row = m0 + rl < g.M ? m0 + rl : g.M - 1;
-      const float su = su_s[rl];
-      const int pn = (row / T) >> shift;
-      pd[j] = 0.f;
+          for (int j = 0; j < 16; ++j) pd[j] = x[0][j] * bn_val[0] + x[1][j] * bn_val[1];
+        } else {
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int col = colbase + ni * 32;
-        float av = a_val[ni];
-        if (!uniform && perturbed) av = aseg[(int64_t)pn * g.r1.lda + (col - seg_base)];
-        float v = acc[mi][ni][j] + su * av;
-        if (MODE == NOISE_EPI_RELU2_BF16) {
-          v = bf2f(f2bf(v > 0.f ? v * v : 0.f));
-          if (want_u) {
-            float bn = bn_val[ni];
-            if (!uniform) bn = g.b_next[(int64_t)pn * g.ld_bnext + col];
-            pd[j] += v * bn;
+          for (int j = 0; j < 16; ++j) {
+            const float* br = g.b_next + (int64_t)pn_s[NOISE_RL(j)] * g.ld_bnext + colbase;
+            pd[j] = x[0][j] * br[0] + x[1][j] * br[32];
           }
         }
-        wstage[(8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] = v;
       }
     }
-    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) wstage[(8 * (j >> 2) + (j & 3)) * SLD + ni * 32] = x[ni][j];
     if (want_u) {
       const float tot = noise::halfwave_transpose_sum16(pd, lane);
       const int jj = (lane & 31) >> 1;
@@ -271,6 +268,8 @@ lowrank_gemm_kernel(const GemmArgs g) {
     }
     if (mi < 3) __syncthreads();  // the copy-out reads are done before the next round writes
   }
+#undef NOISE_RANK1
+#undef NOISE_RL
 }
 
 // Validates the arguments shared by both entry points and fills g (everything but the rope part).

@@ -9,8 +9,11 @@
 //
 // Pipeline (measured on MI355X: under load a stage's global loads take longer than its MFMAs,
 // so loads run two stages ahead):
-//   * K advances 32 per stage through two LDS buffers (rows padded to 80 B: the 16-byte
-//     fragment reads of 16 consecutive lanes hit 16 distinct 4-bank groups);
+//   * K advances 32 per stage through two LDS buffers of 64-byte rows whose four 16-byte chunks
+//     are swizzled, chunk c of row r stored at c ^ ((r >> 2) & 3): both the staging stores (four
+//     lanes per row) and the fragment reads (one row per lane) then touch 16 distinct 16-byte
+//     bank groups per 16 lanes. Measured on MI355X: zero LDS bank-conflict cycles, against 8 per
+//     16-byte store with padded 80-byte rows (which read conflict-free);
 //   * global loads for stage s+2 are issued at the start of stage s into one of two register
 //     staging sets (the sets alternate by name, never copied: a copy would wait for the loads in
 //     flight) while the other set (stage s+1) drains into LDS at the end of stage s;
@@ -25,7 +28,7 @@
 
 namespace noise {
 
-constexpr int TILE_M = 256, TBK = 32, TLDK = TBK + 8;  // 80-byte LDS rows
+constexpr int TILE_M = 256, TBK = 32, TLDK = TBK;  // 64-byte LDS rows, chunk-swizzled
 
 template <int BN>
 struct TileCfg {
@@ -57,10 +60,17 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
   }
   const uint16_t* brow = B + (int64_t)lr * ldb + lc;
   const int64_t bstep = (int64_t)RP * ldb;
-  const int far = wm * 128 + (lane & 31), fbr = wn * 64 + (lane & 31), kofs = (lane >> 5) * 8;
-  const uint16_t* fa_base = smem + far * TLDK + kofs;
-  const uint16_t* fb_base = smem + BOFS + fbr * TLDK + kofs;
-  uint16_t* st_base = smem + lr * TLDK + lc;
+  // Fragment rows are lane % 32 plus multiples of 32, so their swizzle is ((lane % 32) >> 2) & 3;
+  // k-step 0 reads logical chunk lane / 32, k-step 1 chunk 2 + lane / 32 (= that ^ 2).
+  const int sw = ((lane & 31) >> 2) & 3;
+  const int kofs0 = (((lane >> 5)) ^ sw) * 8, kofs1 = kofs0 ^ 16;
+  const int far = wm * 128 + (lane & 31), fbr = wn * 64 + (lane & 31);
+  const uint16_t* fa_base0 = smem + far * TLDK + kofs0;
+  const uint16_t* fb_base0 = smem + BOFS + fbr * TLDK + kofs0;
+  const uint16_t* fa_base1 = smem + far * TLDK + kofs1;
+  const uint16_t* fb_base1 = smem + BOFS + fbr * TLDK + kofs1;
+  // Staging rows lr + i * RP share lr's swizzle (RP is a multiple of 16).
+  uint16_t* st_base = smem + lr * TLDK + ((lc >> 3) ^ ((lr >> 2) & 3)) * 8;
   bf16x8 a0[4], b0[2], a1[4], b1[2];
   u32x4 s0[NA + NB], s1[NA + NB];  // staging sets: NA rows of A, then NB rows of B
 
@@ -82,10 +92,10 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
     _Pragma("unroll") for (int i = 0; i < NB; ++i)                                          \
       *reinterpret_cast<u32x4*>(d_ + BOFS + i * RP * TLDK) = S[NA + i];                     \
   }
-#define NOISE_FLOAD(FA, FB, BUF_, KOFF)                                                       \
+#define NOISE_FLOAD(FA, FB, BUF_, KS_)                                                        \
   {                                                                                         \
-    const uint16_t* pa_ = fa_base + (BUF_) * BUF + (KOFF);                                  \
-    const uint16_t* pb_ = fb_base + (BUF_) * BUF + (KOFF);                                  \
+    const uint16_t* pa_ = ((KS_) ? fa_base1 : fa_base0) + (BUF_) * BUF;                     \
+    const uint16_t* pb_ = ((KS_) ? fb_base1 : fb_base0) + (BUF_) * BUF;                     \
     _Pragma("unroll") for (int i = 0; i < 4; ++i)                                           \
       FA[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pa_ + i * 32 * TLDK)); \
     _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
@@ -100,7 +110,7 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
 #define NOISE_STAGE(KS, CUR, L, S)                                                            \
   NOISE_GLOAD(L, (KS) + 2)                                                                  \
   __builtin_amdgcn_sched_barrier(0);                                                        \
-  NOISE_FLOAD(a1, b1, CUR, 16)                                                              \
+  NOISE_FLOAD(a1, b1, CUR, 1)                                                               \
   NOISE_MFMA8(a0, b0)                                                                       \
   NOISE_MFMA8(a1, b1)                                                                       \
   if ((KS) + 1 < KT) NOISE_SSTORE(S, (CUR) ^ 1)                                             \
