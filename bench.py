@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
     python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the MLP pair
+    python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -91,6 +92,32 @@ def probe_mlp(rows=512 * 2048, d=512, f=2048, reps=3):
     print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x MLP pair over {rows} rows', flush=True)
 
 
+def probe_attention(members=512, T=2048, reps=2):
+    """Counter-collection workload: the window-1024 and window-2048 attention launches of one
+    bench chunk (512 members x 2048 tokens x 8 heads, unit-rms q and k), `reps` times each."""
+    import noise_amd  # noqa: F401  (loads the library)
+    from noise_amd import kernels as K
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    M = members * T
+    qkv = torch.empty(M, 1536, device=dev, dtype=torch.bfloat16)
+    for i in range(3):  # q, k unit-rms per head; v N(0, 1)
+        blk = torch.randn(M, 512, device=dev, generator=g)
+        if i < 2:
+            blk = blk.view(M, 8, 64)
+            blk = (blk * torch.rsqrt(blk.square().mean(-1, keepdim=True))).view(M, 512)
+        qkv[:, i * 512:(i + 1) * 512] = blk.bfloat16()
+        del blk
+    y = torch.empty(M, 512, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(members // 2, 512, device=dev, generator=g)
+    uproj = torch.empty(M, 8, device=dev)
+    for _ in range(reps):
+        for w in (1024, 2048):
+            K.window_attention(qkv, y, members, T, w, b, 1, uproj)
+    torch.cuda.synchronize()
+    print(f'probe-attention: {reps} x windows 1024 and 2048 over {members} members x {T} tokens', flush=True)
+
+
 def cpu_baseline(seconds_budget=20.0):
     from noise_amd.synthetic import antithetic, pair_noise, sequence
     from oracle import model_ref as R
@@ -124,7 +151,8 @@ def main():
     ap.add_argument('--tokens', type=int, default=2048)
     ap.add_argument('--chunk', type=int, default=256, help='pairs per batched forward')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    ap.add_argument('--probe-mlp', action='store_true', help='run the counter-collection workload only')
+    ap.add_argument('--probe-mlp', action='store_true', help='run the MLP counter-collection workload only')
+    ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
@@ -133,6 +161,9 @@ def main():
 
     if args.probe_mlp:
         probe_mlp()
+        return
+    if args.probe_attention:
+        probe_attention()
         return
 
     import noise_amd

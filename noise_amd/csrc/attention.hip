@@ -32,11 +32,18 @@
 
 namespace {
 
-constexpr int BQ = 256, BKEY = 64, LDK = 72, NTH = 256;  // 144-byte LDS rows
+constexpr int BQ = 256, BKEY = 64, LDK = 64, NTH = 256;  // 128-byte LDS rows, chunk-swizzled
 constexpr float LOG2E = 1.4426950408889634f;
 
+// Every LDS tile here has 128-byte rows of eight 16-byte chunks, chunk c of row r stored at
+// c ^ ((r >> 1) & 7): 16 lanes reading one chunk of 16 consecutive rows, or 16 lanes writing two
+// whole rows, touch all 64 banks once (padded rows instead conflict on 16-byte stores).
+NOISE_DEV int swz(int row, int elem) {  // element offset of (row, elem) within a 64-element row
+  return row * LDK + ((((elem >> 3) ^ (row >> 1)) & 7) << 3) + (elem & 7);
+}
+
 struct AttnSmem {
-  uint16_t kv[2][2][BKEY][LDK];  // [buffer][K | V^T][key | dim][dim | permuted key], 36 KB
+  uint16_t kv[2][2][BKEY * LDK];  // [buffer][K | V^T] swizzled [key | dim][dim | permuted key], 32 KB
   float mom[4][2][64];           // per-wave moment partials
 };
 
@@ -61,7 +68,9 @@ void window_attention_kernel(const noise_attention_t g) {
   const int loc = bid >> 3;
   const int qblk = nqb - 1 - loc % nqb;
   const int p = loc / nqb;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // The wave index through readfirstlane: the compiler then knows every per-wave quantity below
+  // (which blocks a wave needs, which are fully inside the window) is uniform, and branches on it.
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, q32 = lane & 31;
   const int q0 = qblk * BQ;
   const int64_t rowbase = (int64_t)p * T;
@@ -125,14 +134,14 @@ void window_attention_kernel(const noise_attention_t g) {
   {                                                                                           \
     _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
       const int c_ = tid + i * NTH;                                                           \
-      *reinterpret_cast<u32x4*>(&sm.kv[BUF][0][c_ >> 3][(c_ & 7) * 8]) = sk[i];               \
+      *reinterpret_cast<u32x4*>(&sm.kv[BUF][0][swz(c_ >> 3, (c_ & 7) * 8)]) = sk[i];          \
     }                                                                                         \
     _Pragma("unroll") for (int c = 0; c < 4; ++c) {                                           \
       const int e_ = c >> 1, sh_ = (c & 1) * 16;                                              \
       u32x2 t_;                                                                               \
       t_[0] = ((sv[0][e_] >> sh_) & 0xffffu) | (((sv[1][e_] >> sh_) & 0xffffu) << 16);        \
       t_[1] = ((sv[2][e_] >> sh_) & 0xffffu) | (((sv[3][e_] >> sh_) & 0xffffu) << 16);        \
-      *reinterpret_cast<u32x2*>(&sm.kv[BUF][1][4 * dg + c][kpos]) = t_;                       \
+      *reinterpret_cast<u32x2*>(&sm.kv[BUF][1][swz(4 * dg + c, kpos)]) = t_;                  \
     }                                                                                         \
   }
 
@@ -160,7 +169,7 @@ void window_attention_kernel(const noise_attention_t g) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 kf = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(&sm.kv[cur][0][kb2 * 32 + q32][ks * 16 + half * 8]));
+              bf16x8, *reinterpret_cast<const u32x4*>(&sm.kv[cur][0][swz(kb2 * 32 + q32, ks * 16 + half * 8)]));
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
             s[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][ks], s[qb], 0, 0, 0);
@@ -203,7 +212,7 @@ void window_attention_kernel(const noise_attention_t g) {
           for (int db = 0; db < 2; ++db) {
             const bf16x8 vf = __builtin_bit_cast(
                 bf16x8,
-                *reinterpret_cast<const u32x4*>(&sm.kv[cur][1][db * 32 + q32][(kb2 * 2 + kk) * 16 + half * 8]));
+                *reinterpret_cast<const u32x4*>(&sm.kv[cur][1][swz(db * 32 + q32, (kb2 * 2 + kk) * 16 + half * 8)]));
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb)
               o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[qb][db], 0, 0, 0);
@@ -221,7 +230,7 @@ void window_attention_kernel(const noise_attention_t g) {
   // ---- epilogue: normalise, stage bf16 y through LDS for whole-row stores, dot with b_proj,
   // moments. The loop's last barrier has released both K/V buffers: wave w stages its 64 x 64
   // tile in buffer (w >> 1), half (w & 1).
-  uint16_t(*ys)[LDK] = sm.kv[w >> 1][w & 1];
+  uint16_t* ys = sm.kv[w >> 1][w & 1];  // swizzled [64 queries][64 dims]
   float mom[64];
 #pragma unroll
   for (int i = 0; i < 64; ++i) mom[i] = 0.f;
@@ -246,7 +255,7 @@ void window_attention_kernel(const noise_attention_t g) {
           y[2 * e] = bf_lo(pk[e]);
           y[2 * e + 1] = bf_hi(pk[e]);
         }
-        *reinterpret_cast<u32x2*>(&ys[qb * 32 + q32][dim]) = pk;
+        *reinterpret_cast<u32x2*>(&ys[swz(qb * 32 + q32, dim)]) = pk;
         if (valid) {
           if (g.b_proj) {
             const float4 bv = *reinterpret_cast<const float4*>(g.b_proj + pn * g.ld_b_proj + h * 64 + dim);
@@ -271,7 +280,7 @@ void window_attention_kernel(const noise_attention_t g) {
     const int c = lane + 64 * i, row = c >> 3, c8 = (c & 7) * 8;
     if (wq0 + row < T)
       *reinterpret_cast<u32x4*>(g.y + (rowbase + wq0 + row) * 512 + h * 64 + c8) =
-          *reinterpret_cast<const u32x4*>(&ys[row][c8]);
+          *reinterpret_cast<const u32x4*>(&ys[swz(row, c8)]);
   }
   if (g.moments) {
     halfwave_transpose_sum(mom, lane);
