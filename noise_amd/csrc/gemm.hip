@@ -7,8 +7,8 @@
 //
 // Tiling for gfx950: a 256 x BN output tile per workgroup of 2 x (BN / 64) waves, each wave
 // owning a 128x64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators
-// per lane); the K loop is mma_tile<BN> (two-stage-ahead global prefetch, double-buffered LDS and
-// fragments). BN = 128 (4 waves, two workgroups per CU: one's barriers and epilogue overlap the
+// per lane); the K loop is mma_tile<BN> (global -> LDS direct loads two stages ahead, three LDS
+// stage buffers). BN = 128 (4 waves, two workgroups per CU: one's barriers and epilogue overlap the
 // other's MFMAs) serves the relu^2 up-projection, whose 4 GiB bf16 epilogue dominates; BN = 256
 // (8 waves, one workgroup per CU, half the L2 -> LDS traffic per FLOP) is measured faster for the
 // fp32-output and long-K shapes.
@@ -53,15 +53,23 @@ lowrank_gemm_kernel(const GemmArgs g) {
   constexpr int NT = Cfg::THREADS, WN = BN / 64;
   // The main loop's stage buffers, reused by the epilogue's fp32 staging (whichever is larger).
   constexpr int STAGE_ELEMS = Cfg::WAVES * 32 * SLD * 2;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS > STAGE_ELEMS ? Cfg::SMEM_ELEMS : STAGE_ELEMS];
-  __shared__ float su_s[BM];
-  __shared__ int pn_s[BM];  // noise row (member >> member_shift) of each tile row
+  // All of the kernel's LDS is one array: the tile's direct global -> LDS loads are synchronised
+  // by explicit waits, and a single LDS object keeps the compiler from adding conservative waits
+  // for them before unrelated LDS reads. Per-row data first (immediate-offset addressing), then
+  // the tile buffers / epilogue staging.
+  constexpr int TILE_BYTES = 2 * (Cfg::SMEM_ELEMS > STAGE_ELEMS ? Cfg::SMEM_ELEMS : STAGE_ELEMS);
+  constexpr int ROW_BYTES = BM * 4;
+  constexpr int ROW_ARRAYS = MODE == EPI_QKV_ROPE ? 5 + BN / 64 : 2;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ROW_ARRAYS * ROW_BYTES + TILE_BYTES];
+  float* su_s = reinterpret_cast<float*>(lds);
+  int* pn_s = reinterpret_cast<int*>(lds + ROW_BYTES);  // noise row of each tile row
   // EPI_QKV_ROPE per-row data: token position, token id (-1 if out of range), sign * a_ve[token],
   // and the VE gate of the tile's BN / 64 heads.
-  __shared__ int t_s[BM];
-  __shared__ int tok_s[BM];
-  __shared__ float sa_s[BM];
-  __shared__ float gate_s[BM][BN / 64];
+  int* t_s = reinterpret_cast<int*>(lds + 2 * ROW_BYTES);
+  int* tok_s = reinterpret_cast<int*>(lds + 3 * ROW_BYTES);
+  float* sa_s = reinterpret_cast<float*>(lds + 4 * ROW_BYTES);
+  float(*gate_s)[BN / 64] = reinterpret_cast<float(*)[BN / 64]>(lds + 5 * ROW_BYTES);
+  uint16_t* smem = reinterpret_cast<uint16_t*>(lds + ROW_ARRAYS * ROW_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;

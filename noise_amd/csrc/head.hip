@@ -24,11 +24,17 @@ constexpr int HT = HCfg::THREADS;
 template <bool ALIGNED>
 __global__ void __attribute__((amdgpu_flat_work_group_size(HT, HT), amdgpu_waves_per_eu(2, 2)))
 head_ce_kernel(const noise_head_t g) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[HCfg::SMEM_ELEMS];
-  __shared__ float su_s[256];
-  __shared__ int tgt_s[256];
-  __shared__ float tz_s[256];
-  __shared__ float sum_s[2][256];
+  // One LDS object (per-row data first, where every access is an immediate offset, then the tile
+  // buffers): the tile's direct global -> LDS loads are synchronised by explicit waits, and a
+  // single object keeps the compiler from adding conservative waits for them before unrelated
+  // LDS reads.
+  constexpr int ROWS_BYTES = 5 * 256 * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ROWS_BYTES + 2 * HCfg::SMEM_ELEMS];
+  float* su_s = reinterpret_cast<float*>(lds);
+  int* tgt_s = reinterpret_cast<int*>(lds + 1024);
+  float* tz_s = reinterpret_cast<float*>(lds + 2048);
+  float(*sum_s)[256] = reinterpret_cast<float(*)[256]>(lds + 3072);
+  uint16_t* smem = reinterpret_cast<uint16_t*>(lds + ROWS_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -57,8 +63,8 @@ head_ce_kernel(const noise_head_t g) {
   for (int n0 = 0; n0 < g.V; n0 += HBN) {
     floatx16 acc[4][2];
     noise::zero_acc(acc);
-    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc);
-    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_lo + (int64_t)n0 * 512, 512, 512, smem, acc);
+    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc,
+                         g.w_lo + (int64_t)n0 * 512);
     const int colbase = n0 + wn * 64 + (lane & 31);
     float a_val[2] = {0.f, 0.f};
     if (perturbed && uniform) {
