@@ -3,8 +3,8 @@
 // Reference semantics (train/val/eggroll.py:94-102; utils/model.py:203-209): for every member
 // row r, z = h_r (W + s a b^T)^T over the whole vocabulary, z' = 15 tanh(z / 15), and
 // ce_r = logsumexp(z') - z'[target]. The reference materialises [32, T, V] fp32 logits per slice;
-// here a workgroup (4 waves, two per CU) owns 256 rows and sweeps the vocabulary in 128-column
-// tiles of mma_tile<128>, keeping only
+// here a workgroup (8 waves) owns 256 rows and sweeps the vocabulary in 256-column tiles of
+// mma_tile<256> (measured 5% faster than two 4-wave workgroups on 128-column tiles), keeping only
 // per-row running sums of exp(z') (the soft-cap bounds z' to [-15, 15], so no running max is
 // needed in fp32) and the target's z'.
 //
@@ -15,7 +15,7 @@
 
 namespace {
 
-constexpr int HBN = 128;
+constexpr int HBN = 256, HWN = HBN / 64;
 using HCfg = noise::TileCfg<HBN>;
 constexpr int HT = HCfg::THREADS;
 
@@ -28,7 +28,7 @@ head_ce_kernel(const noise_head_t g) {
   // buffers): the tile's direct global -> LDS loads are synchronised by explicit waits, and a
   // single object keeps the compiler from adding conservative waits for them before unrelated
   // LDS reads.
-  constexpr int ROWS_BYTES = 5 * 256 * 4;
+  constexpr int ROWS_BYTES = (3 + HWN) * 256 * 4;
   __shared__ __attribute__((aligned(16))) unsigned char lds[ROWS_BYTES + 2 * HCfg::SMEM_ELEMS];
   float* su_s = reinterpret_cast<float*>(lds);
   int* tgt_s = reinterpret_cast<int*>(lds + 1024);
@@ -37,11 +37,11 @@ head_ce_kernel(const noise_head_t g) {
   uint16_t* smem = reinterpret_cast<uint16_t*>(lds + ROWS_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / HWN, wn = wave % HWN;
   const int m0 = blockIdx.x * 256;
   const int T = g.T;
   const bool perturbed = g.sign != nullptr;
-  {
+  if (tid < 256) {
     const int row = m0 + tid;
     float su = 0.f;
     int tg = -1;
@@ -121,9 +121,12 @@ head_ce_kernel(const noise_head_t g) {
     if ((lane & 1) == 0) sum_s[wn][rl] = rsum[mi];
   }
   __syncthreads();
-  {
+  if (tid < 256) {
     const int row = m0 + tid;
-    if (row < g.M) g.ce[row] = logf(sum_s[0][tid] + sum_s[1][tid]) - tz_s[tid];
+    float tot = 0.f;
+#pragma unroll
+    for (int c = 0; c < HWN; ++c) tot += sum_s[c][tid];
+    if (row < g.M) g.ce[row] = logf(tot) - tz_s[tid];
   }
 }
 
