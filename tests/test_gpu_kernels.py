@@ -325,3 +325,79 @@ def test_fitness_gradient_adamw(device):
         opt.step()
         nk.adamw(dp, grad.to(device), dm, dv, 1e-3, 0.5, 0.95, 1e-8, 0.0, step)
     torch.testing.assert_close(dp.cpu(), refp.detach(), rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize('window', [1024, 2048])
+def test_config2_attention_full_size(device, window):
+    """Config 2 at its full shape: q, k, v [256 members, 8 heads, 2048 tokens, 64] ~ N(0, 1) bf16.
+    64 sampled (member, head, query) outputs against exact float64 attention over their visible
+    keys; the moments of 4 sampled (member, head) pairs against the kernel's own output (mean over
+    tokens of y and y^2: an identity independent of size)."""
+    members, T = 256, 2048
+    M = members * T
+    g = torch.Generator(device=device).manual_seed(window)
+    qkv = torch.randn(M, 1536, device=device, generator=g).to(torch.bfloat16)
+    y = torch.empty(M, 512, dtype=torch.bfloat16, device=device)
+    mom = torch.empty(members, 8, 2, 64, device=device)
+    scratch = torch.empty(members * 8 * (T // 256) * 128, device=device)
+    nk.window_attention(qkv, y, members, T, window, moments=mom, scratch=scratch)
+    torch.cuda.synchronize()
+    gc = _gen(window + 1)
+    ps = torch.randint(0, members, (64,), generator=gc)
+    hs = torch.randint(0, 8, (64,), generator=gc)
+    ts = torch.randint(0, T, (64,), generator=gc)
+    ts[:4] = torch.tensor([0, 1, min(window, T - 1), T - 1])
+    for p, h, t in zip(ps.tolist(), hs.tolist(), ts.tolist()):
+        lo = max(0, t - window)
+        rows = qkv[p * T + lo:p * T + t + 1].double().cpu()
+        q = qkv[p * T + t, h * 64:(h + 1) * 64].double().cpu()
+        k = rows[:, 512 + h * 64:512 + (h + 1) * 64]
+        v = rows[:, 1024 + h * 64:1024 + (h + 1) * 64]
+        w = torch.softmax(k @ q / 8.0, 0)
+        ref = w @ v
+        got = y[p * T + t, h * 64:(h + 1) * 64].double().cpu()
+        assert float((got - ref).abs().max()) <= 2e-2 * max(1.0, float(ref.abs().max())), (p, h, t)
+    for p, h in [(0, 0), (17, 3), (128, 7), (255, 5)]:
+        yy = y[p * T:(p + 1) * T, h * 64:(h + 1) * 64].double().cpu()
+        want = torch.stack([yy.mean(0), yy.square().mean(0)])
+        torch.testing.assert_close(mom[p, h].double().cpu(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_config3_head_full_size(device):
+    """Config 3 at its full shape: h [512 members x 2048 tokens, 512] bf16 N(0, 1) normalised,
+    W [4096, 512] fp32 ~ N(0, 1/512) with a rank-1 perturbation (sigma = 1e-3, a, b ~ N(0, 1)),
+    Zipf targets. 256 sampled rows against float64, and the per-member means against the kernel's
+    own per-token losses."""
+    from noise_amd.synthetic import zipf_tokens
+    members, T, V = 512, 2048, 4096
+    M = members * T
+    g = torch.Generator(device=device).manual_seed(3)
+    h = torch.randn(M, 512, device=device, generator=g)
+    h = (h * torch.rsqrt(h.square().mean(1, keepdim=True))).to(torch.bfloat16)
+    gc = _gen(33)
+    W = torch.randn(V, 512, generator=gc) / math.sqrt(512)
+    a = torch.randn(members // 2, V, generator=gc)
+    b = torch.randn(members // 2, 512, generator=gc)
+    sign = torch.tensor([1e-3, -1e-3]).repeat(members // 2)
+    targets = zipf_tokens(T, seed=5)
+    db = b.to(device)
+    u = torch.empty(M, device=device)
+    for p0 in range(0, members, 64):  # u = h . b of each member's noise row, in slices
+        rows = h[p0 * T:(p0 + 64) * T].float().view(64, T, 512)
+        u[p0 * T:(p0 + 64) * T] = torch.einsum('ptd,pd->pt', rows, db[torch.arange(p0, p0 + 64, device=device) // 2]).reshape(-1)
+    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi)
+    nk.cast_bf16(W.to(device), hi, lo)
+    ce = torch.empty(M, device=device)
+    nk.head_ce(h, hi, lo, T, targets.to(device), ce, sign.to(device), NoiseRows(a=a.to(device), shift=1), u)
+    losses = torch.empty(members, device=device)
+    nk.member_mean(ce, members, T, losses)
+    torch.cuda.synchronize()
+    rows = torch.randint(0, M, (256,), generator=gc)
+    hr = h[rows.to(device)].double().cpu()
+    p = rows // T
+    z = hr @ W.double().t() + (sign[p].double() * u[rows.to(device)].double().cpu())[:, None] * a[p // 2].double()
+    ref = R.softcap_ce(z, targets[rows % T])
+    torch.testing.assert_close(ce[rows.to(device)].double().cpu(), ref, rtol=0, atol=5e-5)
+    torch.testing.assert_close(losses.double().cpu(), ce.double().view(members, T).mean(1).cpu(), rtol=1e-6, atol=1e-6)
+    assert float((losses.cpu() - math.log(V)).abs().max()) < 1.0  # near-uniform logits at this scale
