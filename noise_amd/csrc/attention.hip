@@ -7,12 +7,13 @@
 // per-(member, head) first and second moments of y over tokens ("credit moments").
 //
 // gfx950 mapping: one workgroup = 4 waves = 256 queries of one (member, head); each wave owns 64
-// queries as two 32-query MFMA blocks. Scores are formed transposed, S^T = K Q^T with
-// v_mfma_f32_32x32x16_bf16, so a lane holds one query and 16 keys of every 32-key block and the
-// softmax sum needs no cross-lane traffic until the end. The probabilities are reused in-register
-// as the B operand of O^T = V^T P^T (the key order inside an MFMA's K dimension only has to agree
-// between the operands); V is staged transposed in LDS with its keys permuted so that each lane's
-// 8 keys are one 16-byte read.
+// queries as two 32-query MFMA blocks (qb = 0, 1). Scores are formed transposed, S^T = K Q^T with
+// v_mfma_f32_32x32x16_bf16, so a lane holds one query and 16 keys of every 32-key half-block and
+// the softmax sum needs no cross-lane traffic until the end. The probabilities are reused
+// in-register as the B operand of O^T = V^T P^T; the A operand V^T is read from the row-major V
+// tile with ds_read_b64_tr_b16 (the transposing LDS read: lane 4a + b of each 16-lane group
+// receives element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12 of the group),
+// in the key order the score accumulators hold.
 //
 // Softmax shift: the exponent is shifted by the constant 64 * scale (in log2 units), the largest
 // score unit-rms q and k can reach, instead of by a running maximum: probabilities are then final
@@ -22,38 +23,47 @@
 // normalised and N(0, 1) rows alike. Probabilities are rounded to bf16 for the P V product; the
 // normaliser sums them unrounded.
 //
-// Pipeline: K and V of key block b + 1 are in flight into registers while block b is computed,
-// and are stored into the other of two LDS buffers after it: one barrier per 64-key block. Only blocks
-// that cross the causal diagonal, the window edge or the end of the sequence evaluate the mask.
+// Pipeline. Key blocks of 64 stream through a ring of four LDS stages by global -> LDS direct loads
+// (no registers), two blocks ahead, one s_waitcnt + s_barrier per block. Inside a wave the work of
+// 32-key half-block h is split by query block so that matrix and vector work overlap:
+//   X(h): MFMAs  PV of qb 1 for half h - 1, QK of qb 1 for half h;  VALU  softmax of qb 0, half h
+//   Y(h): MFMAs  PV of qb 0 for half h,     QK of qb 0 for half h + 1; VALU softmax of qb 1, half h
+// Each segment is one basic block in which every MFMA is followed by a share of the softmax, the
+// QK accumulation steps alternating with independent PV MFMAs. K and V fragments are read from LDS
+// once, into double-buffered registers, one segment before their first use (V of h and K of h + 1
+// during X(h); K of a block's first half-block right after that block's barrier). Half-blocks that
+// cross the causal diagonal, the window edge or the end of the sequence first set their invisible
+// scores to -inf, per 32-query block; the others are not masked at all.
 // Workgroups are numbered so that all query blocks of one (member, head) run on one XCD (the
 // hardware deals consecutive workgroup ids round-robin over the 8 XCDs), longest first: that
 // head's K and V are then read from HBM once into that XCD's L2.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 
-constexpr int BQ = 256, BKEY = 64, LDK = 64, NTH = 256;  // 128-byte LDS rows, chunk-swizzled
+constexpr int BQ = 256, BKEY = 64, LDK = 64, NTH = 256, NSTAGE = 4;
 constexpr float LOG2E = 1.4426950408889634f;
 
-// Every LDS tile here has 128-byte rows of eight 16-byte chunks, chunk c of row r stored at
-// c ^ ((r >> 1) & 7): 16 lanes reading one chunk of 16 consecutive rows, or 16 lanes writing two
-// whole rows, touch all 64 banks once (padded rows instead conflict on 16-byte stores).
-NOISE_DEV int swz(int row, int elem) {  // element offset of (row, elem) within a 64-element row
+// K tiles and the y staging: 128-byte rows of eight 16-byte chunks, chunk c of row r stored at
+// c ^ ((r >> 1) & 7) (16 lanes reading one chunk of 16 consecutive rows, or writing two whole
+// rows, touch all 64 banks once).
+NOISE_DEV int swz(int row, int elem) {
   return row * LDK + ((((elem >> 3) ^ (row >> 1)) & 7) << 3) + (elem & 7);
 }
+// V tiles: chunk c of row r at c ^ (2 * (r & 3)). A transposing read has each 16-lane group
+// address 4 consecutive rows (keys) x 2 adjacent chunks (8 dims, two 8-byte halves each): the
+// swizzle spreads those 8 chunks over all eight chunk positions.
+NOISE_DEV int swz_v(int row, int chunk) { return row * LDK + ((chunk ^ (2 * (row & 3))) << 3); }
 
 struct AttnSmem {
-  uint16_t kv[2][2][BKEY * LDK];  // [buffer][K | V^T] swizzled [key | dim][dim | permuted key], 32 KB
-  float mom[4][2][64];           // per-wave moment partials
+  uint16_t kv[NSTAGE][2][BKEY * LDK];  // [stage][K | V] row-major [key][dim], swizzled, 64 KB
+  float mom[4][2][64];                 // per-wave moment partials
 };
 
-// LDS column of key k (0..63) in the transposed V tile: within each 32-key half, the keys a lane
-// half `h` needs for k-step `ks` (accumulator rows 8a + 4h + b, a in {2ks', 2ks'+1}, b < 4) are
-// 8 consecutive columns starting at 16 ks' + 8 h.
-NOISE_DEV int vt_pos(int k) {
-  const int kb2 = k >> 5, a = (k >> 3) & 3, hh = (k >> 2) & 1, b = k & 3;
-  return kb2 * 32 + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + b;
-}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void window_attention_kernel(const noise_attention_t g) {
@@ -76,8 +86,8 @@ void window_attention_kernel(const noise_attention_t g) {
   const int64_t rowbase = (int64_t)p * T;
   const int64_t ld = g.ldqkv;
   const uint16_t* Qg = g.qkv + h * 64;
-  const uint16_t* Kg = g.qkv + 512 + h * 64;
-  const uint16_t* Vg = g.qkv + 1024 + h * 64;
+  const uint16_t* Kg = g.qkv + rowbase * ld + 512 + h * 64;
+  const uint16_t* Vg = g.qkv + rowbase * ld + 1024 + h * 64;
 
   const int wq0 = q0 + w * 64;
   const bool wave_live = wq0 < T;
@@ -94,6 +104,11 @@ void window_attention_kernel(const noise_attention_t g) {
           bf16x8, *reinterpret_cast<const u32x4*>(Qg + (rowbase + qi) * ld + ks * 16 + half * 8));
   }
 
+  // Wait for Q here, in the compiler's own accounting: otherwise it guards the first use inside the
+  // loop with a vmcnt that would also wait for the key blocks in flight.
+  __asm__ volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[0][2]), "+v"(qf[0][3]),
+                   "+v"(qf[1][0]), "+v"(qf[1][1]), "+v"(qf[1][2]), "+v"(qf[1][3]));
+
   floatx16 o[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -101,7 +116,9 @@ void window_attention_kernel(const noise_attention_t g) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) o[a][b][j] = 0.f;
-  float lsum[2] = {0.f, 0.f};
+  float lsum[2][2];  // [qb][two partial sums]
+#pragma unroll
+  for (int a = 0; a < 2; ++a) lsum[a][0] = lsum[a][1] = 0.f;
 
   const float sl2 = g.scale * LOG2E;
   const float shift = 64.f * g.scale * LOG2E;
@@ -109,127 +126,274 @@ void window_attention_kernel(const noise_attention_t g) {
   kfirst = kfirst < 0 ? 0 : (kfirst & ~(BKEY - 1));
   const int qlast = q0 + BQ - 1 < T ? q0 + BQ - 1 : T - 1;
   const int nblk = (qlast - kfirst) / BKEY + 1;
+  // This wave's blocks: bf .. bl (none for a wave past the end of the sequence).
+  const int lo_key = wq0 - window;
+  const int bf = !wave_live ? nblk : (lo_key <= kfirst ? 0 : (lo_key - kfirst) >> 6);
+  const int bl = !wave_live ? nblk - 1 : (wq1 - kfirst) >> 6;
 
-  // Staging: K as 2 x 16 B (key c >> 3, dims (c & 7) * 8 for c = tid, tid + 256); V as a 4-key x
-  // 4-dim patch (keys 4 kg.., dims 4 dg..; the 16 lanes sharing kg read one 128-byte row).
-  const int kg = tid >> 4, dg = tid & 15;
-  const int kpos = vt_pos(4 * kg);
-  u32x4 sk[2];
-  u32x2 sv[4];
-#define NOISE_ATT_GLOAD(KB)                                                                     \
+  // ---- global -> LDS direct loads: wave w fetches rows 16w .. 16w + 15 of the K and the V tile,
+  // 8 rows (1 KB) per instruction; lane l lands at row 8i + l / 8, physical chunk l % 8, so it
+  // fetches the logical chunk the swizzle maps there. Rows past the sequence repeat row T - 1.
+  // The loads are issued through inline asm: the compiler then tracks no LDS DMA and adds no
+  // conservative vmcnt waits in front of the transposing LDS reads below; the loop's explicit
+  // s_waitcnt + s_barrier orders every DMA against the reads of its stage.
+  const uint32_t lds_kv = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)&sm.kv[0][0][0];
+  // M0 (the LDS destination of the load, latched at issue) is saved and restored around it.
+#define NOISE_ATT_DMA(SRC, LDS_ADDR)                                                            \
   {                                                                                           \
+    uint32_t m0save_;                                                                         \
+    __asm__ volatile(                                                                         \
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"                                  \
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"                                  \
+        : "=&s"(m0save_)                                                                      \
+        : "v"(SRC), "s"(__builtin_amdgcn_readfirstlane(LDS_ADDR))                            \
+        : "memory");                                                                          \
+  }
+#define NOISE_ATT_LOAD(BLK)                                                                     \
+  {                                                                                           \
+    const int blk_ = (BLK);                                                                   \
+    const int st_ = blk_ % NSTAGE;                                                            \
     _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
-      const int c_ = tid + i * NTH;                                                           \
-      int kj_ = (KB) + (c_ >> 3);                                                             \
-      kj_ = kj_ < T ? kj_ : T - 1;                                                            \
-      sk[i] = *reinterpret_cast<const u32x4*>(Kg + (rowbase + kj_) * ld + (c_ & 7) * 8);      \
-    }                                                                                         \
-    _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                           \
-      int kj_ = (KB) + 4 * kg + r;                                                            \
-      kj_ = kj_ < T ? kj_ : T - 1;                                                            \
-      sv[r] = *reinterpret_cast<const u32x2*>(Vg + (rowbase + kj_) * ld + 4 * dg);            \
+      const int r_ = 16 * w + 8 * i + (lane >> 3), pc_ = lane & 7;                            \
+      int key_ = kfirst + blk_ * BKEY + r_;                                                   \
+      key_ = key_ < T ? key_ : T - 1;                                                         \
+      const int64_t ro_ = (int64_t)key_ * ld;                                                 \
+      const uint32_t dst_ = lds_kv + 2u * (uint32_t)((st_ * 2 * BKEY + 16 * w + 8 * i) * LDK);  \
+      NOISE_ATT_DMA(Kg + ro_ + ((pc_ ^ ((r_ >> 1) & 7)) * 8), dst_);                          \
+      NOISE_ATT_DMA(Vg + ro_ + ((pc_ ^ (2 * (r_ & 3))) * 8), dst_ + 2u * BKEY * LDK);         \
     }                                                                                         \
   }
-#define NOISE_ATT_SSTORE(BUF)                                                                   \
-  {                                                                                           \
-    _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                           \
-      const int c_ = tid + i * NTH;                                                           \
-      *reinterpret_cast<u32x4*>(&sm.kv[BUF][0][swz(c_ >> 3, (c_ & 7) * 8)]) = sk[i];          \
-    }                                                                                         \
-    _Pragma("unroll") for (int c = 0; c < 4; ++c) {                                           \
-      const int e_ = c >> 1, sh_ = (c & 1) * 16;                                              \
-      u32x2 t_;                                                                               \
-      t_[0] = ((sv[0][e_] >> sh_) & 0xffffu) | (((sv[1][e_] >> sh_) & 0xffffu) << 16);        \
-      t_[1] = ((sv[2][e_] >> sh_) & 0xffffu) | (((sv[3][e_] >> sh_) & 0xffffu) << 16);        \
-      *reinterpret_cast<u32x2*>(&sm.kv[BUF][1][swz(4 * dg + c, kpos)]) = t_;                  \
-    }                                                                                         \
+
+  // ---- fragment addresses (elements within one stage's K or V tile)
+  // K (A operand of S^T = K Q^T): lane's key row q32 (+32 per half-block), dims 16 ks + 8 half.
+  int kfo[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) kfo[ks] = swz(q32, ks * 16 + half * 8);
+  // V^T (A operand of O^T = V^T P^T) by transposing reads: in 16-lane group g = lane / 16, source
+  // lane s = a + 4e addresses key kbase + e, dims 32 db + 16 (g & 1) + 4a .. + 3, where kbase =
+  // 32 kb2 + 16 kk + 4 (g >> 1) (+ 8 for the second read); lane 16g + 4a' + b' then holds dim
+  // 32 db + lane % 32 for keys kbase .. kbase + 3 -- the keys its P accumulators hold
+  // (16 kk + 4 half + {0..3} and + {8..11}).
+  int vfo[2];
+  {
+    const int s16 = lane & 15, a = s16 & 3, e = s16 >> 2, gq = lane >> 4;
+    const int key = 4 * (gq >> 1) + e;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+      vfo[db] = swz_v(key, 4 * db + 2 * (gq & 1) + (a >> 1)) + 4 * (a & 1);
   }
 
-  NOISE_ATT_GLOAD(kfirst)
-  NOISE_ATT_SSTORE(0)
-  __syncthreads();
-  if (nblk > 1) NOISE_ATT_GLOAD(kfirst + BKEY)
+  floatx16 s[2];      // S^T of the current half-block, per query block
+  bf16x8 pf[2][2];    // P (bf16) [qb][kk]: keys 16 kk .. 16 kk + 15 of the half-block
+  // Fragment registers, double-buffered by half-block parity: K fragments [parity][ks], V^T
+  // fragments [parity][kk][db]. Each is read from LDS once, one segment before its first use
+  // (except K of a block's first half-block, read right after the block's barrier).
+  bf16x8 kf[2][4];
+  bf16x8 vf[2][2][2];
 
-  for (int b = 0; b < nblk; ++b) {
-    const int cur = b & 1;
-    const int kb = kfirst + b * BKEY;
-    // Wave-uniform: does any (query, key) pair of this wave and block fall in the window, and
-    // do all of them?
-    const bool need = wave_live && kb <= wq1 && kb + BKEY - 1 >= wq0 - window;
-    if (need) {
-      const bool full = kb + BKEY - 1 <= wq0 && wq0 + 63 - kb <= window && kb + BKEY <= T;
-      // One 32-key half at a time: scores, probabilities, then their P V product.
+  // Half-block hh (= 2 b + kb2) lives in stage b % NSTAGE.
+#define NOISE_KBASE(HH) (&sm.kv[((HH) >> 1) % NSTAGE][0][((HH) & 1) * 32 * LDK])
+#define NOISE_VBASE(HH) (&sm.kv[((HH) >> 1) % NSTAGE][1][((HH) & 1) * 32 * LDK])
+  auto read_k = [&](int hh, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* kb_ = NOISE_KBASE(hh);
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
-        floatx16 s[2];  // [query block]
+    for (int ks = 0; ks < 4; ++ks)
+      kf[BUF][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(kb_ + kfo[ks]));
+  };
+  auto read_v = [&](int hh, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint16_t* vb_ = NOISE_VBASE(hh);
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) s[c][j] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 kf = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(&sm.kv[cur][0][swz(kb2 * 32 + q32, ks * 16 + half * 8)]));
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-            s[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][ks], s[qb], 0, 0, 0);
-        }
-        if (full) {
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][j], sl2, -shift));
-              s[qb][j] = pv;
-              lsum[qb] += pv;
-            }
-        } else {
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            // key kb + kb2*32 + 8(j/4) + 4 half + j%4 is visible iff 0 <= qi - key <= window
-            const int base = wq0 + qb * 32 + q32 - kb - kb2 * 32 - 4 * half;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int d = base - (8 * (j >> 2) + (j & 3));
-              const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][j], sl2, -shift));
-              const float pm = (unsigned)d <= (unsigned)window ? pv : 0.f;
-              s[qb][j] = pm;
-              lsum[qb] += pm;
-            }
-          }
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          bf16x8 pf[2];
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            u32x4 pk;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pk[e] = pack_bf2(s[qb][8 * kk + 2 * e], s[qb][8 * kk + 2 * e + 1]);
-            pf[qb] = __builtin_bit_cast(bf16x8, pk);
-          }
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            const bf16x8 vf = __builtin_bit_cast(
-                bf16x8,
-                *reinterpret_cast<const u32x4*>(&sm.kv[cur][1][swz(db * 32 + q32, (kb2 * 2 + kk) * 16 + half * 8)]));
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
-              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[qb][db], 0, 0, 0);
-          }
-        }
+      for (int db = 0; db < 2; ++db) {
+        const uint16_t* a0 = vb_ + vfo[db] + 16 * kk * LDK;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0 + 8 * LDK));
+        u32x4 u;
+        u[0] = __builtin_bit_cast(u32x2, lo)[0];
+        u[1] = __builtin_bit_cast(u32x2, lo)[1];
+        u[2] = __builtin_bit_cast(u32x2, hi)[0];
+        u[3] = __builtin_bit_cast(u32x2, hi)[1];
+        vf[BUF][kk][db] = __builtin_bit_cast(bf16x8, u);
       }
+  };
+  // One segment's MFMAs: the PV of query block QP (V^T buffer VB) and the QK of query block QK
+  // (K buffer KB), issued alternately so that each step of the 4-deep QK accumulation has an
+  // independent PV MFMA between it and the next.
+  auto mfma_pair = [&](auto qpc, auto vbc, auto qkc, auto kbc, auto withpv) {
+    constexpr int QP = decltype(qpc)::value, VB = decltype(vbc)::value;
+    constexpr int QK = decltype(qkc)::value, KB = decltype(kbc)::value;
+    constexpr bool PV = decltype(withpv)::value;
+    floatx16 acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[KB][0], qf[QK][0], (floatx16){}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (PV)
+        o[QP][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[VB][i >> 1][i & 1], pf[QP][i >> 1],
+                                                               o[QP][i & 1], 0, 0, 0);
+      if (i < 3) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[KB][i + 1], qf[QK][i + 1], acc, 0, 0, 0);
     }
-    if (b + 1 < nblk) NOISE_ATT_SSTORE(cur ^ 1)
-    __syncthreads();
-    if (b + 2 < nblk) NOISE_ATT_GLOAD(kb + 2 * BKEY)
+    s[QK] = acc;
+  };
+  auto pv = [&](auto qbc, auto bufc) {
+    constexpr int QB = decltype(qbc)::value, BUF = decltype(bufc)::value;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+        o[QB][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[BUF][kk][db], pf[QB][kk], o[QB][db], 0, 0, 0);
+  };
+  // Scores of query block QB over half-block hh that fall outside the window (or the sequence) set
+  // to -inf, so that the softmax below gives them exact zeros: key khalf + 8 (j / 4) + 4 half +
+  // j % 4 is visible to query qa + q32 iff 0 <= query - key <= window.
+  auto mask_scores = [&](auto qbc, int hh) {
+    constexpr int QB = decltype(qbc)::value;
+    const int base = wq0 + QB * 32 + q32 - (kfirst + hh * 32) - 4 * half;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int d = base - (8 * (j >> 2) + (j & 3));
+      s[QB][j] = (unsigned)d <= (unsigned)window ? s[QB][j] : -__builtin_inff();
+    }
+  };
+  // Softmax of query block QB: probabilities into pf[QB] (bf16), their sums into lsum[QB].
+  auto softmax = [&](auto qbc) {
+    constexpr int QB = decltype(qbc)::value;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4 pk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 8 * kk + 2 * i;
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[QB][j], sl2, -shift));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[QB][j + 1], sl2, -shift));
+        lsum[QB][0] += e0;
+        lsum[QB][1] += e1;
+        pk[i] = pack_bf2(e0, e1);
+      }
+      pf[QB][kk] = __builtin_bit_cast(bf16x8, pk);
+    }
+  };
+  // Are all (query, key) pairs of query block qb and half-block hh visible?
+  auto is_full = [&](int qb, int hh) {
+    const int khalf = kfirst + hh * 32, qa = wq0 + qb * 32;
+    return khalf + 31 <= qa && qa + 31 - khalf <= window && khalf + 32 <= T;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  // Segment boundary: neither instructions nor LDS reads move across it.
+  auto fence = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ volatile("" ::: "memory");
+  };
+  // Register pins: an empty asm that "modifies" the values, so that the compiler neither moves a
+  // segment's MFMAs above its mask branch nor sinks its softmax into the next segment.
+#define NOISE_PIN_K(B) \
+  __asm__ volatile("" : "+v"(kf[B][0]), "+v"(kf[B][1]), "+v"(kf[B][2]), "+v"(kf[B][3]))
+#define NOISE_PIN_V(B) \
+  __asm__ volatile("" : "+v"(vf[B][0][0]), "+v"(vf[B][0][1]), "+v"(vf[B][1][0]), "+v"(vf[B][1][1]))
+#define NOISE_PIN_P(QB) \
+  __asm__ volatile("" : "+v"(pf[QB][0]), "+v"(pf[QB][1]), "+v"(lsum[QB][0]), "+v"(lsum[QB][1]))
+  // Instruction order inside a segment: each MFMA followed by a share of the softmax VALU work
+  // (sched_group_barrier masks: 0x008 MFMA, 0x002 VALU, 0x100 LDS read).
+  auto interleave = [&](auto nreads) {
+    if (decltype(nreads)::value > 0) __builtin_amdgcn_sched_group_barrier(0x100, decltype(nreads)::value, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+  };
+  // X(hh): PV of qb 1 for hh - 1, QK of qb 1 for hh, softmax of qb 0 for hh, in one basic block
+  // (the mask, where needed, is applied to the scores first); prefetches V of hh and, for the
+  // first half of a block, K of hh + 1. The pins keep the MFMAs below the mask branch.
+  auto seg_x = [&](int hh, auto par) {
+    constexpr int P = decltype(par)::value;
+    fence();
+    if (!is_full(0, hh)) mask_scores(I0{}, hh);
+    fence();
+    NOISE_PIN_K(P);
+    NOISE_PIN_V(P ^ 1);
+    NOISE_PIN_P(1);
+    read_v(hh, par);
+    if (P == 0) read_k(hh + 1, I1{});
+    mfma_pair(I1{}, std::integral_constant<int, P ^ 1>{}, I1{}, par, std::true_type{});
+    softmax(I0{});
+    interleave(std::integral_constant<int, P == 0 ? 12 : 8>{});
+    NOISE_PIN_P(0);
+  };
+  // Y(hh): PV of qb 0 for hh, QK of qb 0 for hh + 1, softmax of qb 1 for hh. K of hh + 1 was
+  // prefetched unless hh + 1 opens a block (then it is read here, after that block's barrier).
+  auto seg_y = [&](int hh, auto par) {
+    constexpr int P = decltype(par)::value;
+    fence();
+    if (!is_full(1, hh)) mask_scores(I1{}, hh);
+    fence();
+    NOISE_PIN_P(0);
+    NOISE_PIN_V(P);
+    if (P == 1) read_k(hh + 1, I0{});
+    else NOISE_PIN_K(1);
+    mfma_pair(I0{}, par, I0{}, std::integral_constant<int, P ^ 1>{}, std::true_type{});
+    softmax(I1{});
+    interleave(std::integral_constant<int, P == 1 ? 4 : 0>{});
+    NOISE_PIN_P(1);
+  };
+  // The wave's last half-block hh (odd): PV of qb 0, softmax and PV of qb 1, all from registers.
+  auto drain = [&](int hh) {
+    fence();
+    if (!is_full(1, hh)) mask_scores(I1{}, hh);
+    fence();
+    NOISE_PIN_P(0);
+    NOISE_PIN_V(1);
+    pv(I0{}, I1{});
+    softmax(I1{});
+    pv(I1{}, I1{});
+  };
+
+  // Pipeline state before a wave's first block: nothing to add (P and V^T zero) and the scores of
+  // the half-block before it at -inf, so that the first Y contributes exact zeros.
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) pf[qb][kk] = __builtin_bit_cast(bf16x8, (u32x4){0u, 0u, 0u, 0u});
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s[1][j] = -__builtin_inff();
+#pragma unroll
+  for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) vf[b2][kk][db] = pf[0][0];
+
+  NOISE_ATT_LOAD(0)
+  if (nblk > 1) NOISE_ATT_LOAD(1)
+  for (int b = 0; b < nblk; ++b) {
+    // Block b has landed for this wave (the 4 loads of block b + 1 may still fly), then for every
+    // wave; every wave is past the reads of block b - 2, whose stage takes block b + 2.
+    if (b + 1 < nblk) __asm__ volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    else __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (b + 2 < nblk) NOISE_ATT_LOAD(b + 2)
+    if (b >= bf && b <= bl) {
+      seg_y(2 * b - 1, I1{});
+      seg_x(2 * b, I0{});
+      seg_y(2 * b, I0{});
+      seg_x(2 * b + 1, I1{});
+    }
   }
-#undef NOISE_ATT_SSTORE
-#undef NOISE_ATT_GLOAD
+  if (bf <= bl) drain(2 * bl + 1);
+#undef NOISE_PIN_P
+#undef NOISE_PIN_K
+#undef NOISE_PIN_V
+#undef NOISE_VBASE
+#undef NOISE_KBASE
+#undef NOISE_ATT_LOAD
+#undef NOISE_ATT_DMA
+  // Every direct load has landed and every wave is done with the stages.
+  __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // ---- epilogue: normalise, stage bf16 y through LDS for whole-row stores, dot with b_proj,
-  // moments. The loop's last barrier has released both K/V buffers: wave w stages its 64 x 64
-  // tile in buffer (w >> 1), half (w & 1).
+  // moments. Wave w stages its 64 x 64 tile in stage (w >> 1), half (w & 1).
   uint16_t* ys = sm.kv[w >> 1][w & 1];  // swizzled [64 queries][64 dims]
   float mom[64];
 #pragma unroll
@@ -238,7 +402,8 @@ void window_attention_kernel(const noise_attention_t g) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qi = wq0 + qb * 32 + q32;
-    const float lt = lsum[qb] + __shfl_xor(lsum[qb], 32, 64);
+    float lt = lsum[qb][0] + lsum[qb][1];
+    lt += __shfl_xor(lt, 32, 64);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const bool valid = qi < T;
     float dot = 0.f;

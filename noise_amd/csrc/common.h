@@ -17,8 +17,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Round-to-nearest-even float -> bfloat16 bits (v_cvt_pk_bf16_f32 on gfx950).
 NOISE_DEV uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 NOISE_DEV float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+// Two floats -> packed bf16 pair (lo in bits 0-15), one v_cvt_pk_bf16_f32 with both operands; the
+// element-wise form costs two conversions plus a shift and an or.
 NOISE_DEV uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){lo, hi}, bf16x2));
 }
 NOISE_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 NOISE_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
