@@ -131,7 +131,8 @@ int noise_rope_norm_ve(const noise_rope_t* args, void* stream);
  * [1536, K] bf16 and the three rank-1 segments of r1 (512 columns each). Replaces `lowrank`
  * (train/val/eggroll.py:56-58) for c_q, c_k, c_v together with apply_rotary_emb + norm
  * (utils/model.py:55-58; eggroll.py:90) and the value-embedding add (eggroll.py:85-89).
- * rope->qkv is not read; rope->M must equal M; r1->rows_per_member must equal rope->T. */
+ * rope->qkv is not read; rope->M must equal M; r1->rows_per_member must equal rope->T; with a
+ * value embedding, ve_table and ve_b are 16-byte aligned and ld_ve_b is a multiple of 4. */
 int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M, int K,
                         const noise_rank1_t* r1, const noise_rope_t* rope, void* stream);
 

@@ -186,24 +186,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
           x[0][j] *= r;
           x[1][j] *= r;
         }
-      } else if (g.rope.gate) {  // v + gate * (table[token] + sign a_ve[token] b_ve)
-        const int vh = (n0 - 1024) / 64 + wn;
-        const int c0 = vh * 64 + (lane & 31);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int rl = NOISE_RL(j);
-          const int tok = tok_s[rl];
-          const float gt = gate_s[rl][wn], sa = sa_s[rl];
-          const float* bv = g.rope.sign ? g.rope.ve_b + (int64_t)pn_s[rl] * g.rope.ld_ve_b + c0 : nullptr;
-          const float* tv = g.rope.ve_table + (int64_t)(tok >= 0 ? tok : 0) * 512 + c0;
-#pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
-            float ve = tok >= 0 ? tv[ni * 32] : __builtin_nanf("");
-            if (g.rope.sign) ve += sa * bv[ni * 32];
-            x[ni][j] += gt * ve;
-          }
-        }
-      }
+      }  // v + gate * value embedding: added in the copy-out below, from full table-row chunks
     } else if (MODE == NOISE_EPI_RELU2_BF16) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -245,8 +228,32 @@ lowrank_gemm_kernel(const GemmArgs g) {
         const int h = rr >> 5, r = rr & 31;
         const int row = m0 + h * 128 + mi * 32 + r;
         const float* src = stage + ((h * WN + (c8 >> 6)) * 32 + r) * SLD + (c8 & 63);
-        const float4 lo = *reinterpret_cast<const float4*>(src);
-        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+        float4 lo = *reinterpret_cast<const float4*>(src);
+        float4 hi = *reinterpret_cast<const float4*>(src + 4);
+        if (MODE == EPI_QKV_ROPE && n0 >= 1024 && g.rope.gate) {
+          // v + gate * (table[token] + sign a_ve[token] b_ve) on 8 consecutive columns of the row.
+          const int tl = h * 128 + mi * 32 + r, vc = n0 - 1024 + c8;
+          const int tok = tok_s[tl];
+          const float gt = gate_s[tl][c8 >> 6], sa = sa_s[tl];
+          float ve[8];
+          if (tok >= 0) {
+            const float* tv = g.rope.ve_table + (int64_t)tok * 512 + vc;
+            const float4 t0 = *reinterpret_cast<const float4*>(tv), t1 = *reinterpret_cast<const float4*>(tv + 4);
+            ve[0] = t0.x; ve[1] = t0.y; ve[2] = t0.z; ve[3] = t0.w;
+            ve[4] = t1.x; ve[5] = t1.y; ve[6] = t1.z; ve[7] = t1.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ve[e] = __builtin_nanf("");
+          }
+          if (g.rope.sign) {
+            const float* bv = g.rope.ve_b + (int64_t)pn_s[tl] * g.rope.ld_ve_b + vc;
+            const float4 b0 = *reinterpret_cast<const float4*>(bv), b1 = *reinterpret_cast<const float4*>(bv + 4);
+            ve[0] += sa * b0.x; ve[1] += sa * b0.y; ve[2] += sa * b0.z; ve[3] += sa * b0.w;
+            ve[4] += sa * b1.x; ve[5] += sa * b1.y; ve[6] += sa * b1.z; ve[7] += sa * b1.w;
+          }
+          lo.x += gt * ve[0]; lo.y += gt * ve[1]; lo.z += gt * ve[2]; lo.w += gt * ve[3];
+          hi.x += gt * ve[4]; hi.y += gt * ve[5]; hi.z += gt * ve[6]; hi.w += gt * ve[7];
+        }
         if (row < g.M)
           *reinterpret_cast<uint4*>(C16 + (int64_t)row * g.ldc + n0 + c8) =
               make_uint4(pack_bf2(lo.x, lo.y), pack_bf2(lo.z, lo.w), pack_bf2(hi.x, hi.y), pack_bf2(hi.z, hi.w));
@@ -374,6 +381,9 @@ extern "C" int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_
   NOISE_REQUIRE(!rp.gate || (rp.ve_table && rp.idx && rp.vocab > 0 && rp.member_shift >= 0 &&
                              (!rp.sign || (rp.ve_a && rp.ve_b && rp.ld_ve_a >= rp.vocab && rp.ld_ve_b >= 512))),
                 "qkv_rope_gemm: value embedding needs table, idx, vocab and (perturbed) ve_a/ve_b");
+  NOISE_REQUIRE(!rp.gate || (((uintptr_t)rp.ve_table % 16) == 0 &&
+                             (!rp.sign || (((uintptr_t)rp.ve_b % 16) == 0 && rp.ld_ve_b % 4 == 0))),
+                "qkv_rope_gemm: ve_table and ve_b must be 16-byte aligned, ld_ve_b a multiple of 4");
   GemmArgs g;
   int rc = prepare_gemm(g, A, lda, W, ldw, M, 1536, K, r1, rp.out, 1536, rp.T);
   if (rc) return rc;

@@ -107,36 +107,33 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(const noise_mixnorm_t g) 
     if (lane == 0) g.u[(int64_t)row * g.ldu + j] = d;
   }
   if (g.gate_w) {
-    // Channels 0..31 live in lanes 0..3; each of those lanes forms 8 partial gate logits and
-    // its partial dot with b, then the four lanes are summed.
-    float part[9];
+    // Channels 0..31 live in lanes 0..3 (8 each). Lane l < 32 forms the partial logit of gate
+    // l / 4 over channel block l % 4; lanes 32..63 form the same block's partial dot with the
+    // gate's noise vector b (replicated eight times). Both are summed over the 4 lanes of a group.
+    const int blk = lane & 3;
+    float hb[8];
 #pragma unroll
-    for (int q = 0; q < 9; ++q) part[q] = 0.f;
-    if (lane < 4) {
+    for (int k = 0; k < 8; ++k) hb[k] = __shfl(h[k], blk, 64);
+    const bool noise_lane = lane >= 32;
+    float wv[8];
+    if (!noise_lane) {
+      load8(g.gate_w + (lane >> 2) * 32 + blk * 8, wv);
+    } else if (g.sign) {
+      load8(g.gate_b + pn * g.ld_gate_b + blk * 8, wv);
+    } else {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float wv[8];
-        load8(g.gate_w + q * 32 + c, wv);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) part[q] += h[k] * wv[k];
-      }
-      if (g.sign) {
-        float bv[8];
-        load8(g.gate_b + pn * g.ld_gate_b + c, bv);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) part[8] += h[k] * bv[k];
-      }
+      for (int k = 0; k < 8; ++k) wv[k] = 0.f;
     }
+    float part = 0.f;
 #pragma unroll
-    for (int q = 0; q < 9; ++q) part[q] = group_sum(part[q], 4);
-    if (lane == 0) {
-      const float su = s * part[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float z = part[q];
-        if (g.sign) z += su * g.gate_a[pn * g.ld_gate_a + q];
-        g.gate[(int64_t)row * 8 + q] = 2.0f / (1.0f + expf(-z));
-      }
+    for (int k = 0; k < 8; ++k) part += hb[k] * wv[k];
+    part = group_sum(part, 4);
+    const float nd = __shfl(part, 32, 64);  // h[:32] . b_gate
+    if (!noise_lane && blk == 0) {
+      const int q = lane >> 2;
+      float z = part;
+      if (g.sign) z += s * nd * g.gate_a[pn * g.ld_gate_a + q];
+      g.gate[(int64_t)row * 8 + q] = 2.0f / (1.0f + expf(-z));
     }
   }
 }
