@@ -116,9 +116,11 @@ void window_attention_kernel(const noise_attention_t g) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) o[a][b][j] = 0.f;
-  float lsum[2][2];  // [qb][two partial sums]
+  float lsum[2][4];  // [qb][four partial sums]
 #pragma unroll
-  for (int a = 0; a < 2; ++a) lsum[a][0] = lsum[a][1] = 0.f;
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lsum[a][j] = 0.f;
 
   const float sl2 = g.scale * LOG2E;
   const float shift = 64.f * g.scale * LOG2E;
@@ -256,21 +258,23 @@ void window_attention_kernel(const noise_attention_t g) {
       s[QB][j] = (unsigned)d <= (unsigned)window ? s[QB][j] : -__builtin_inff();
     }
   };
-  // Softmax of query block QB: probabilities into pf[QB] (bf16), their sums into lsum[QB].
+  // Softmax of query block QB: probabilities into pf[QB] (bf16), their sums into lsum[QB]. All
+  // exponent arguments first, then the exponentials, then their uses: each v_exp_f32 result is
+  // consumed several instructions after it issues.
   auto softmax = [&](auto qbc) {
     constexpr int QB = decltype(qbc)::value;
+    float e[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) e[j] = __builtin_fmaf(s[QB][j], sl2, -shift);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) e[j] = __builtin_amdgcn_exp2f(e[j]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lsum[QB][j & 3] += e[j];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       u32x4 pk;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = 8 * kk + 2 * i;
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[QB][j], sl2, -shift));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[QB][j + 1], sl2, -shift));
-        lsum[QB][0] += e0;
-        lsum[QB][1] += e1;
-        pk[i] = pack_bf2(e0, e1);
-      }
+      for (int i = 0; i < 4; ++i) pk[i] = pack_bf2(e[8 * kk + 2 * i], e[8 * kk + 2 * i + 1]);
       pf[QB][kk] = __builtin_bit_cast(bf16x8, pk);
     }
   };
@@ -292,8 +296,9 @@ void window_attention_kernel(const noise_attention_t g) {
   __asm__ volatile("" : "+v"(kf[B][0]), "+v"(kf[B][1]), "+v"(kf[B][2]), "+v"(kf[B][3]))
 #define NOISE_PIN_V(B) \
   __asm__ volatile("" : "+v"(vf[B][0][0]), "+v"(vf[B][0][1]), "+v"(vf[B][1][0]), "+v"(vf[B][1][1]))
-#define NOISE_PIN_P(QB) \
-  __asm__ volatile("" : "+v"(pf[QB][0]), "+v"(pf[QB][1]), "+v"(lsum[QB][0]), "+v"(lsum[QB][1]))
+#define NOISE_PIN_P(QB)                                                                      \
+  __asm__ volatile("" : "+v"(pf[QB][0]), "+v"(pf[QB][1]), "+v"(lsum[QB][0]), "+v"(lsum[QB][1]), \
+                   "+v"(lsum[QB][2]), "+v"(lsum[QB][3]))
   // Instruction order inside a segment: each MFMA followed by a share of the softmax VALU work
   // (sched_group_barrier masks: 0x008 MFMA, 0x002 VALU, 0x100 LDS read).
   auto interleave = [&](auto nreads) {
@@ -402,7 +407,7 @@ void window_attention_kernel(const noise_attention_t g) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qi = wq0 + qb * 32 + q32;
-    float lt = lsum[qb][0] + lsum[qb][1];
+    float lt = (lsum[qb][0] + lsum[qb][1]) + (lsum[qb][2] + lsum[qb][3]);
     lt += __shfl_xor(lt, 32, 64);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const bool valid = qi < T;
