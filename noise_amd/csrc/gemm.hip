@@ -49,7 +49,10 @@ struct GemmArgs {
 template <int MODE, int BN, bool LONGK>
 __global__ void __attribute__((amdgpu_flat_work_group_size(2 * BN, 2 * BN), amdgpu_waves_per_eu(2, 2)))
 lowrank_gemm_kernel(const GemmArgs g) {
-  using Cfg = noise::TileCfg<BN>;
+  // 256-column tiles run 64-deep stages (two stage buffers of 64 KB), 128-column tiles 32-deep
+  // stages (three of 24 KB, so that two workgroups fit in a CU).
+  constexpr int NSTG = BN == 256 ? 2 : 3, KDEPTH = BN == 256 ? 64 : 32;
+  using Cfg = noise::TileCfg<BN, NSTG, KDEPTH>;
   constexpr int NT = Cfg::THREADS, WN = BN / 64;
   // The main loop's stage buffers, reused by the epilogue's fp32 staging (whichever is larger).
   constexpr int STAGE_ELEMS = Cfg::WAVES * 32 * SLD * 2;
@@ -113,7 +116,7 @@ lowrank_gemm_kernel(const GemmArgs g) {
 
   floatx16 acc[4][2];
   noise::zero_acc(acc);
-  noise::mma_tile<BN>(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
+  noise::mma_tile<BN, NSTG, KDEPTH>(g.A + (int64_t)m0 * g.lda, g.lda, g.M - m0, g.W + (int64_t)n0 * g.ldw, g.ldw, g.K,
                       smem, acc);
 
   // ---- epilogue ----

@@ -16,7 +16,8 @@
 namespace {
 
 constexpr int HBN = 256, HWN = HBN / 64;
-using HCfg = noise::TileCfg<HBN>;
+constexpr int HNS = 2, HKB = 64;  // two 64-deep stages
+using HCfg = noise::TileCfg<HBN, HNS, HKB>;
 constexpr int HT = HCfg::THREADS;
 
 // ALIGNED: every 256-row tile lies inside one member (T % 256 == 0), so the rank-1 vector a is one
@@ -63,7 +64,7 @@ head_ce_kernel(const noise_head_t g) {
   for (int n0 = 0; n0 < g.V; n0 += HBN) {
     floatx16 acc[4][2];
     noise::zero_acc(acc);
-    noise::mma_tile<HBN>(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc,
+    noise::mma_tile<HBN, HNS, HKB>(A, 512, g.M - m0, g.w_hi + (int64_t)n0 * 512, 512, 512, smem, acc,
                          g.w_lo + (int64_t)n0 * 512);
     const int colbase = n0 + wn * 64 + (lane & 31);
     float a_val[2] = {0.f, 0.f};

@@ -7,18 +7,18 @@
 //   row = wm*128 + mi*32 + 8*(j/4) + 4*(l/32) + j%4,   col = wn*64 + ni*32 + l%32.
 //
 // Pipeline:
-//   * K advances 32 per stage through NS LDS stage buffers of 64-byte rows whose four 16-byte
-//     chunks are swizzled, chunk c of row r stored at c ^ ((r >> 2) & 3), so that the fragment
-//     reads (one row per lane, 16 lanes per bank cycle) touch 16 distinct 16-byte bank groups;
+//   * K advances KB (32 or 64) per stage through NS LDS stage buffers of 64- or 128-byte rows
+//     whose 16-byte chunks are swizzled (see tile_swizzle), so that the fragment reads (one row
+//     per lane, 16 lanes per bank cycle) touch 16 distinct 16-byte bank groups;
 //   * global -> LDS direct loads (global_load_lds_dwordx4: each lane's 16 bytes land at the
 //     wave's LDS base + 16 * lane, no registers involved) fetch stage s + NS - 1 while stage s
-//     computes; lane l of a load covers row l / 4 of a 16-row slab at physical chunk l % 4 and
-//     therefore fetches logical chunk (l % 4) ^ ((row >> 2) & 3) from global memory;
+//     computes; lane l of a load covers row l / LPR of a slab at physical chunk l % LPR and
+//     therefore fetches the logical chunk the swizzle maps there;
 //   * one s_waitcnt vmcnt + s_barrier per stage (inline asm with a memory clobber: the compiler's
 //     own fence would wait for every load in flight, including the later stages).
 // Measured on MI355X against the register-staged two-buffer loop it replaces: +12-15% in the
-// main loop (the GEMM there is bound by L2 -> CU load throughput; more bytes in flight per CU
-// and no VGPR staging or ds_write instructions).
+// main loop. With 256-column tiles two 64-deep stages beat three 32-deep ones by 4-8% (whole
+// 128-byte lines per row); 128-column tiles keep three 32-deep stages (two workgroups per CU).
 // With B2 (a second [BN, K] operand) the loop continues over K again with B2 in place of B, so
 // acc += A B^T + A B2^T in one pipeline (the head's hi + lo weight halves).
 // Rows of A at or beyond `a_rows` are read from row a_rows - 1 (their results are discarded).
@@ -29,57 +29,72 @@
 
 namespace noise {
 
-constexpr int TILE_M = 256, TBK = 32, TLDK = TBK;  // 64-byte LDS rows, chunk-swizzled
+constexpr int TILE_M = 256, TBK = 32, TLDK = TBK;  // default stage depth: 64-byte LDS rows
 
-template <int BN, int NS = 3>
+// KB: K depth per stage, 32 (64-byte LDS rows, chunk c of row r at c ^ ((r >> 2) & 3)) or 64
+// (128-byte rows, c ^ ((r >> 1) & 7)). Both swizzles keep the fragment reads conflict-free; 64
+// fetches whole 128-byte lines per row, which the direct loads move at about twice the rate of
+// 64-byte row pieces (measured on MI355X from L2: 55 vs 31 B/clk per CU).
+template <int BN, int NS = 3, int KB = TBK>
 struct TileCfg {
   static constexpr int WAVES = 2 * (BN / 64);
   static constexpr int THREADS = 64 * WAVES;
+  static constexpr int RPI = 512 / KB;                                 // rows per 1-KB load
   static constexpr int ROWS_A = TILE_M / WAVES, ROWS_B = BN / WAVES;  // rows per wave per stage
-  static constexpr int NIA = ROWS_A / 16, NIB = ROWS_B / 16;           // 1-KB loads per wave
-  static constexpr int BOFS = TILE_M * TLDK;         // elements from the A to the B half
-  static constexpr int BUF = (TILE_M + BN) * TLDK;   // elements per stage buffer
+  static constexpr int NIA = ROWS_A / RPI, NIB = ROWS_B / RPI;         // 1-KB loads per wave
+  static constexpr int BOFS = TILE_M * KB;          // elements from the A to the B half
+  static constexpr int BUF = (TILE_M + BN) * KB;    // elements per stage buffer
   static constexpr int SMEM_ELEMS = NS * BUF;
+  static_assert(KB == 32 || KB == 64, "stage depth");
+  static_assert(NIA * RPI == ROWS_A && NIB * RPI == ROWS_B, "rows per wave");
 };
 
-template <int BN, int NS = 3>
+template <int KB>
+NOISE_DEV int tile_swizzle(int row) {
+  return KB == 32 ? ((row >> 2) & 3) : ((row >> 1) & 7);
+}
+
+template <int BN, int NS = 3, int KB = TBK>
 NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
                         const uint16_t* __restrict__ B, int64_t ldb, int K, uint16_t* smem,
                         floatx16 (&acc)[4][2], const uint16_t* __restrict__ B2 = nullptr) {
-  using C = TileCfg<BN, NS>;
-  constexpr int NIA = C::NIA, NIB = C::NIB, BUF = C::BUF, BOFS = C::BOFS;
+  using C = TileCfg<BN, NS, KB>;
+  constexpr int NIA = C::NIA, NIB = C::NIB, BUF = C::BUF, BOFS = C::BOFS, RPI = C::RPI;
+  constexpr int LPR = 64 / RPI;                 // lanes per row in a load
   constexpr int WAIT = (NS - 2) * (NIA + NIB);  // loads of the younger stages left in flight
   static_assert(NS >= 2 && WAIT < 64, "stage count");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / (BN / 64), wn = wave % (BN / 64);
-  const int KT = K / TBK, KTT = B2 ? 2 * KT : KT;
-  // Direct-load sources: this wave's slabs of A (rows wave * ROWS_A + 16 i ..) and B.
+  const int KT = K / KB, KTT = B2 ? 2 * KT : KT;
+  // Direct-load sources: this wave's slabs of A (rows wave * ROWS_A + RPI i ..) and B. Lane l of
+  // a load lands at row l / LPR, physical chunk l % LPR, so it fetches the logical chunk the
+  // swizzle puts there.
   const uint16_t* ga[NIA];
   int64_t gb[NIB];  // element offsets into B (and B2)
 #pragma unroll
   for (int i = 0; i < NIA; ++i) {
-    const int row = wave * C::ROWS_A + i * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = wave * C::ROWS_A + i * RPI + lane / LPR;
+    const int c = (lane % LPR) ^ tile_swizzle<KB>(row);
     ga[i] = A + (int64_t)(row < a_rows ? row : a_rows - 1) * lda + c * 8;
   }
 #pragma unroll
   for (int i = 0; i < NIB; ++i) {
-    const int row = wave * C::ROWS_B + i * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = wave * C::ROWS_B + i * RPI + lane / LPR;
+    const int c = (lane % LPR) ^ tile_swizzle<KB>(row);
     gb[i] = (int64_t)row * ldb + c * 8;
   }
-  uint16_t* la = smem + wave * C::ROWS_A * TLDK;
-  uint16_t* lb = smem + BOFS + wave * C::ROWS_B * TLDK;
-  // Fragment rows are lane % 32 plus multiples of 32, so their swizzle is ((lane % 32) >> 2) & 3;
-  // k-step 0 reads logical chunk lane / 32, k-step 1 chunk 2 + lane / 32 (= that ^ 2).
-  const int sw = ((lane & 31) >> 2) & 3;
-  const int kofs0 = ((lane >> 5) ^ sw) * 8, kofs1 = kofs0 ^ 16;
+  uint16_t* la = smem + wave * C::ROWS_A * KB;
+  uint16_t* lb = smem + BOFS + wave * C::ROWS_B * KB;
+  // Fragment rows are lane % 32 plus multiples of 32, so their swizzle is that of lane % 32;
+  // k-step ks reads logical chunk 2 ks + lane / 32.
+  const int sw = tile_swizzle<KB>(lane & 31);
   const int far = wm * 128 + (lane & 31), fbr = wn * 64 + (lane & 31);
-  const uint16_t* fa0 = smem + far * TLDK + kofs0;
-  const uint16_t* fb0 = smem + BOFS + fbr * TLDK + kofs0;
-  const uint16_t* fa1 = smem + far * TLDK + kofs1;
-  const uint16_t* fb1 = smem + BOFS + fbr * TLDK + kofs1;
+  int kofs[KB / 16];
+#pragma unroll
+  for (int ks = 0; ks < KB / 16; ++ks) kofs[ks] = ((2 * ks + (lane >> 5)) ^ sw) * 8;
+  const uint16_t* fa = smem + far * KB;
+  const uint16_t* fb = smem + BOFS + fbr * KB;
   bf16x8 a0[4], b0[2], a1[4], b1[2];
 
 // Stage KT_ (clamped to the last one: the surplus loads keep the wait counts exact) into buffer BUF_.
@@ -87,23 +102,23 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
   {                                                                                         \
     const int kk_ = (KT_) < KTT ? (KT_) : KTT - 1;                                          \
     const bool second_ = kk_ >= KT;                                                         \
-    const int k0_ = (second_ ? kk_ - KT : kk_) * TBK;                                       \
+    const int k0_ = (second_ ? kk_ - KT : kk_) * KB;                                        \
     const uint16_t* bsrc_ = second_ ? B2 : B;                                               \
     _Pragma("unroll") for (int i = 0; i < NIA; ++i)                                         \
       __builtin_amdgcn_global_load_lds((const void*)(ga[i] + k0_),                          \
-                                       (void*)(la + (BUF_) * BUF + i * 16 * TLDK), 16, 0, 0); \
+                                       (void*)(la + (BUF_) * BUF + i * RPI * KB), 16, 0, 0); \
     _Pragma("unroll") for (int i = 0; i < NIB; ++i)                                         \
       __builtin_amdgcn_global_load_lds((const void*)(bsrc_ + gb[i] + k0_),                  \
-                                       (void*)(lb + (BUF_) * BUF + i * 16 * TLDK), 16, 0, 0); \
+                                       (void*)(lb + (BUF_) * BUF + i * RPI * KB), 16, 0, 0); \
   }
 #define NOISE_FLOAD(FA, FB, BUF_, KS_)                                                        \
   {                                                                                         \
-    const uint16_t* pa_ = ((KS_) ? fa1 : fa0) + (BUF_) * BUF;                               \
-    const uint16_t* pb_ = ((KS_) ? fb1 : fb0) + (BUF_) * BUF;                               \
+    const uint16_t* pa_ = fa + kofs[KS_] + (BUF_) * BUF;                                    \
+    const uint16_t* pb_ = fb + kofs[KS_] + (BUF_) * BUF;                                    \
     _Pragma("unroll") for (int i = 0; i < 4; ++i)                                           \
-      FA[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pa_ + i * 32 * TLDK)); \
+      FA[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pa_ + i * 32 * KB)); \
     _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
-      FB[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pb_ + i * 32 * TLDK)); \
+      FB[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pb_ + i * 32 * KB)); \
   }
 #define NOISE_MFMA8(FA, FB)                                                                   \
   _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                          \
@@ -122,10 +137,13 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
     // so its buffer takes stage kt + NS - 1.
     __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT) : "memory");
     NOISE_DLOAD(kt + NS - 1, (kt + NS - 1) % NS)
-    NOISE_FLOAD(a0, b0, cur, 0)
-    NOISE_FLOAD(a1, b1, cur, 1)
-    NOISE_MFMA8(a0, b0)
-    NOISE_MFMA8(a1, b1)
+#pragma unroll
+    for (int kp = 0; kp < KB / 32; ++kp) {
+      NOISE_FLOAD(a0, b0, cur, 2 * kp)
+      NOISE_FLOAD(a1, b1, cur, 2 * kp + 1)
+      NOISE_MFMA8(a0, b0)
+      NOISE_MFMA8(a1, b1)
+    }
   }
   // Drain the surplus loads before the caller reuses smem.
   __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
