@@ -257,9 +257,13 @@ lowrank_gemm_kernel(const GemmArgs g) {
           lo.x += gt * ve[0]; lo.y += gt * ve[1]; lo.z += gt * ve[2]; lo.w += gt * ve[3];
           hi.x += gt * ve[4]; hi.y += gt * ve[5]; hi.z += gt * ve[6]; hi.w += gt * ve[7];
         }
+        // Non-temporal: the output streams past L2 instead of evicting the tile operands there
+        // (measured 2-4% faster on the relu^2 and bf16 outputs; the fp32 residual stream, which
+        // the next kernel reads straight back, is better kept on the normal path).
         if (row < g.M)
-          *reinterpret_cast<uint4*>(C16 + (int64_t)row * g.ldc + n0 + c8) =
-              make_uint4(pack_bf2(lo.x, lo.y), pack_bf2(lo.z, lo.w), pack_bf2(hi.x, hi.y), pack_bf2(hi.z, hi.w));
+          __builtin_nontemporal_store(
+              u32x4{pack_bf2(lo.x, lo.y), pack_bf2(lo.z, lo.w), pack_bf2(hi.x, hi.y), pack_bf2(hi.z, hi.w)},
+              reinterpret_cast<u32x4*>(C16 + (int64_t)row * g.ldc + n0 + c8));
       }
     } else {
       float* C32 = reinterpret_cast<float*>(g.C);
