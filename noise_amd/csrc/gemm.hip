@@ -7,11 +7,11 @@
 //
 // Tiling for gfx950: a 256 x BN output tile per workgroup of 2 x (BN / 64) waves, each wave
 // owning a 128x64 sub-tile as 4 x 2 blocks of v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators
-// per lane); the K loop is mma_tile<BN> (global -> LDS direct loads two stages ahead, three LDS
-// stage buffers). BN = 128 (4 waves, two workgroups per CU: one's barriers and epilogue overlap the
-// other's MFMAs) serves the relu^2 up-projection, whose 4 GiB bf16 epilogue dominates; BN = 256
-// (8 waves, one workgroup per CU, half the L2 -> LDS traffic per FLOP) is measured faster for the
-// fp32-output and long-K shapes.
+// per lane); the K loop is mma_tile. BN = 256 (8 waves, one workgroup per CU, two 64-deep stages
+// of whole 128-byte rows) serves every shape in the step; BN = 128 (4 waves, three 32-deep stages,
+// two workgroups per CU) remains for N or rank-1 segments that are not multiples of 256. Measured
+// on MI355X: 256-column tiles with 64-deep stages beat 128-column ones by 4-6% on the relu^2 and
+// q|k|v projections and by 3-8% on the fp32-output shapes.
 // The epilogue runs in four rounds of 32 rows per wave: the rank-1 term and the mode's transform
 // are applied to one accumulator block, the block is staged through LDS as fp32 and written out
 // with 16-byte coalesced accesses. Workgroups are renumbered so that each XCD walks a contiguous
@@ -353,8 +353,8 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
   }
   g.b_next = b_next; g.ld_bnext = ld_bnext; g.u_next = u_next; g.ld_unext = ld_unext;
   if (M == 0) return NOISE_OK;
-  // 256-column tiles unless the relu^2 epilogue (or N, or a segment) asks for 128.
-  const bool wide = mode != NOISE_EPI_RELU2_BF16 && N % 256 == 0 && (!g.r1.sign || g.r1.seg_cols % 256 == 0);
+  // 256-column tiles unless N or a rank-1 segment asks for 128.
+  const bool wide = N % 256 == 0 && (!g.r1.sign || g.r1.seg_cols % 256 == 0);
   const int bn = wide ? 256 : 128;
   const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (N / bn)));
   hipStream_t st = (hipStream_t)stream;
@@ -372,7 +372,9 @@ extern "C" int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t
       else if (wide) NOISE_GEMM_LAUNCH(NOISE_EPI_ADD_F32, 256, false);
       else NOISE_GEMM_LAUNCH(NOISE_EPI_ADD_F32, 128, false);
       break;
-    default: NOISE_GEMM_LAUNCH(NOISE_EPI_RELU2_BF16, 128, false); break;
+    default:
+      if (wide) NOISE_GEMM_LAUNCH(NOISE_EPI_RELU2_BF16, 256, false); else NOISE_GEMM_LAUNCH(NOISE_EPI_RELU2_BF16, 128, false);
+      break;
   }
 #undef NOISE_GEMM_LAUNCH
   return noise::check_launch("lowrank_gemm");
@@ -396,7 +398,7 @@ extern "C" int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_
   if (rc) return rc;
   g.rope = rp;
   if (M == 0) return NOISE_OK;
-  const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (1536 / 128)));
-  lowrank_gemm_kernel<EPI_QKV_ROPE, 128, false><<<grid, 256, 0, (hipStream_t)stream>>>(g);
+  const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (1536 / 256)));
+  lowrank_gemm_kernel<EPI_QKV_ROPE, 256, false><<<grid, 512, 0, (hipStream_t)stream>>>(g);
   return noise::check_launch("qkv_rope_gemm");
 }
