@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
     python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the MLP pair
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
+    python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -118,6 +119,68 @@ def probe_attention(members=512, T=2048, reps=2):
     print(f'probe-attention: {reps} x windows 1024 and 2048 over {members} members x {T} tokens', flush=True)
 
 
+# cycle_derivatives: per (token, direction, vocabulary entry) 4 full-rate VALU instructions (2
+# cycles per wave64 instruction) and 3 quarter-rate transcendentals (8 cycles) -> 32 SIMD cycles
+# per 64 elements; 1024 SIMDs at 2.4 GHz.
+PEAK_PROBE_ELEMS = 1024 * 2.4e9 * 64 / (4 * 2 + 3 * 8)
+
+
+def bench_probe_cycle(steps, warmup, no_cpu, n=2048, P=512, V=4096):
+    """The readout probe of the current records on one GPU: cycle_derivatives over one 2048-token
+    sequence along a full cycle of 512 directions, V = 4096 (train/speedrun/run.py:250-265)."""
+    from noise_amd import probes
+    from noise_amd.synthetic import probe_inputs
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    d = {k: v.to(dev) for k, v in probe_inputs(n, 512, V, sigma=0.005, seed=0).items()}
+    args = (d['base'], d['C'], d['y'], d['steps'], d['sq'], d['dots'], d['dir_sq'])
+    for _ in range(warmup):
+        probes.cycle_derivatives(*args)
+    stream = torch.cuda.current_stream()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in events:
+        a.record(stream)
+        out = probes.cycle_derivatives(*args)
+        b.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    launch_ms = sum(a.elapsed_time(b) for a, b in events) / steps
+    elems = n * P * V
+    achieved = elems / (launch_ms / 1e3)
+    line = {
+        'metric': 'readout probe evaluations/sec on 1 GPU (cycle_derivatives: token x direction, soft-capped LSE over V)',
+        'value': n * P * steps / elapsed, 'unit': 'probes/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
+        'ms_per_step': elapsed / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'f32', 'data': 'synthetic (N(0,4) streams, N(0,9/512) head, sign-flipped Hadamard cycle, Zipf targets)',
+        'config': {'workload': 'readout probe: 2048 tokens x 512 directions x V=4096', 'tokens': n, 'directions': P,
+                   'vocab': V, 'width': 512, 'sigma': 0.005},
+        'roofline': {'bound': 'valu', 'achieved': achieved / 1e9, 'peak': PEAK_PROBE_ELEMS / 1e9, 'unit': 'Gelem/s',
+                     'frac': achieved / PEAK_PROBE_ELEMS, 'traffic': None,
+                     'kernel': 'probe_kernel<4,4> + clean_sum_kernel (one cycle_derivatives call)',
+                     'elements_per_launch': elems, 'launch_ms': launch_ms},
+        'finite': bool(torch.isfinite(out).all()),
+    }
+    if not no_cpu:
+        line['cpu_baseline'] = cpu_baseline_probe(n, P, V)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_probe(n, P, V, tokens=768):
+    import numpy as np
+    from noise_amd.synthetic import probe_inputs
+    from oracle import probes_ref as R
+    d = probe_inputs(tokens, 512, V, probes=P, sigma=0.005, seed=0)
+    args = [d[k].numpy() for k in ('base', 'C', 'y', 'steps', 'sq', 'dots', 'dir_sq')]
+    R.cycle_derivatives(*[a[:1] if a.shape[0] == tokens else a for a in args], dtype=np.float32)
+    t0 = time.perf_counter()
+    R.cycle_derivatives(*args, dtype=np.float32, chunk=1)
+    dt = time.perf_counter() - t0
+    return {'value': tokens * P / dt, 'unit': 'probes/s', 'cores': 1, 'kind': 'port',
+            'sample': f'oracle cycle_derivatives in numpy float32 on CPU, {tokens} tokens x {P} directions x V={V}'}
+
+
 def cpu_baseline(seconds_budget=20.0):
     from noise_amd.synthetic import antithetic, pair_noise, sequence
     from oracle import model_ref as R
@@ -153,6 +216,7 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--probe-mlp', action='store_true', help='run the MLP counter-collection workload only')
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
+    ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
@@ -164,6 +228,9 @@ def main():
         return
     if args.probe_attention:
         probe_attention()
+        return
+    if args.probe_cycle:
+        bench_probe_cycle(max(args.steps, 5), args.warmup, args.no_cpu)
         return
 
     import noise_amd

@@ -203,6 +203,48 @@ int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_
 /* bf16 copy of an fp32 buffer (hi), and optionally the residual bf16(x - hi) (lo). */
 int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, void* stream);
 
+/* ---- Soft-capped log-sum-exp probes of the readout head ----------------------------------
+ * cap(v) = 15 tanh(v / 15). A target y < 0 masks its token (output 0); a target >= V makes the
+ * token's outputs NaN (the reference's gather would fault). */
+
+/* out[i, v] = (CE(cap(raw_i + sigma e_v), y_i) - CE(cap(raw_i - sigma e_v), y_i)) / (2 sigma),
+ * in the closed form log1p(w_v expm1(cap(raw_v +- sigma) - cap(raw_v))) with the target
+ * correction (train/val/run.py:100-111; train/speedrun/run.py:57-68). raw is fp32 or, with
+ * raw_is_bf16, bf16 bit patterns; rows of V elements at stride ld_raw; out fp32 [n, ld_out]. */
+int noise_coordinate_differences(const void* raw, int raw_is_bf16, int64_t ld_raw, const int64_t* y,
+                                 int n, int V, float sigma, float* out, int64_t ld_out, void* stream);
+
+typedef struct {
+  const float* base;      /* [n, V] W x of the clean streams, row stride ld_base */
+  int64_t ld_base;
+  const float* C;         /* [P, V] row j = W D_j, row stride ld_C */
+  int64_t ld_C;
+  const int64_t* rows;    /* row_derivatives: [n, K] indices into C's rows (stride ld_rows) */
+  int64_t ld_rows;
+  const int64_t* y;       /* [n] targets */
+  const float* steps;     /* [n] step of each token's moves */
+  const float* sq;        /* [n] |x|^2 */
+  const float* dots;      /* [n, P] (cycle) or [n, K] (rows): x . D, row stride ld_dots */
+  int64_t ld_dots;
+  const float* dir_sq;    /* [P] (cycle) or [n, K] with row stride ld_dir_sq (rows): |D|^2 */
+  int64_t ld_dir_sq;
+  int n, P, K, V;
+  int width;              /* the stream width the RMS norm divides |x|^2 by */
+  float* clean_sum;       /* workspace [n]: sum_v exp(cap(z0_v) - 15) of each clean token */
+  float* out;             /* [n, P] (cycle) or [n, K] (rows), row stride ld_out */
+  int64_t ld_out;
+} noise_probe_t;
+
+/* Forward differences of each token's readout loss along every direction of a cycle:
+ * inv = rsqrt((sq + 2 s dots_j + s^2 dir_sq_j) / width + eps), z = (base + s C_j) inv,
+ * out[i, j] = (LSE(cap(z)) - cap(z_y) - clean_i) / s_i (train/val/run.py:154-167;
+ * train/speedrun/run.py:90-103). Two launches on `stream`: the clean sums, then the probes. */
+int noise_cycle_derivatives(const noise_probe_t* args, void* stream);
+
+/* The same along each token's own rows of C: direction k of token i is C[rows[i, k]]
+ * (train/val/run.py:170-183). A row index outside [0, P) makes that output NaN. */
+int noise_row_derivatives(const noise_probe_t* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

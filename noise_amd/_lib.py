@@ -50,6 +50,13 @@ class Head(C.Structure):
                 ('targets_stride', I64), ('ce', P)]
 
 
+class Probe(C.Structure):
+    _fields_ = [('base', P), ('ld_base', I64), ('C', P), ('ld_C', I64), ('rows', P), ('ld_rows', I64),
+                ('y', P), ('steps', P), ('sq', P), ('dots', P), ('ld_dots', I64), ('dir_sq', P),
+                ('ld_dir_sq', I64), ('n', INT), ('P', INT), ('K', INT), ('V', INT), ('width', INT),
+                ('clean_sum', P), ('out', P), ('ld_out', I64)]
+
+
 # name -> (restype, argtypes); every function returns an int status.
 SIGNATURES = {
     'noise_abi_version': [],
@@ -65,6 +72,9 @@ SIGNATURES = {
     'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
     'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],
     'noise_cast_bf16': [P, I64, P, P, P],
+    'noise_coordinate_differences': [P, INT, I64, P, INT, INT, F32, P, I64, P],
+    'noise_cycle_derivatives': [C.POINTER(Probe), P],
+    'noise_row_derivatives': [C.POINTER(Probe), P],
 }
 
 _lib = None

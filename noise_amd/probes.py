@@ -1,0 +1,123 @@
+"""Soft-capped log-sum-exp probes of the readout head, on the HIP kernels of libnoise_amd.
+
+Drop-in twins of three functions of the reference trainer, with the same arguments, shapes and
+float32 results (device tensors in, device tensors out, asynchronous on the current stream):
+
+* `coordinate_differences(raw, y, sigma)`  -- train/val/run.py:100-111 (speedrun/run.py:57-68)
+* `cycle_derivatives(base, C, y, steps, sq, dots, dir_sq)`       -- train/val/run.py:154-167
+* `row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq)`   -- train/val/run.py:170-183
+
+The reference reads the stream width from a module constant (WIDTH = 512); here it is the keyword
+`width`. A target y < 0 masks its token (zeros, as the reference's `* (y >= 0)`); a target >= V
+gives NaN for the token instead of the reference's device-side gather fault.
+"""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import Probe
+
+WIDTH = 512
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _f32_rows(t, name, cols=None):
+    _need(t.is_cuda, f'{name}: libnoise_amd kernels take device tensors')
+    _need(t.dtype == torch.float32, f'{name}: expected float32, got {t.dtype}')
+    _need(t.dim() == 2, f'{name}: expected a 2-D tensor, got shape {tuple(t.shape)}')
+    if cols is not None:
+        _need(t.shape[1] == cols, f'{name}: expected {cols} columns, got {t.shape[1]}')
+    return t if t.stride(1) == 1 else t.contiguous()
+
+
+def _vec(t, n, name):
+    _need(t.is_cuda and t.dtype == torch.float32, f'{name}: expected a float32 device tensor')
+    _need(t.numel() == n, f'{name}: expected {n} values, got shape {tuple(t.shape)}')
+    return t.reshape(n).contiguous()
+
+
+def _targets(y, n):
+    _need(y.is_cuda and not y.is_floating_point(), 'y: expected an integer device tensor')
+    _need(y.numel() == n, f'y: expected {n} targets, got shape {tuple(y.shape)}')
+    return y.reshape(n).to(torch.int64).contiguous()
+
+
+def coordinate_differences(raw, y, sigma):
+    """raw [..., V] logits (float32 or bfloat16), y [...] targets -> float32 [..., V]:
+    d CE / d raw_v by central differences of step sigma, in closed form."""
+    _need(raw.is_cuda, 'raw: libnoise_amd kernels take device tensors')
+    _need(raw.dtype in (torch.float32, torch.bfloat16), f'raw: expected float32 or bfloat16, got {raw.dtype}')
+    _need(tuple(y.shape) == tuple(raw.shape[:-1]), f'y {tuple(y.shape)} does not match raw {tuple(raw.shape)}')
+    V = raw.shape[-1]
+    lead = raw.shape[:-1]
+    flat = raw.reshape(-1, V) if raw.dim() != 2 else raw
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    n = flat.shape[0]
+    yy = _targets(y, n)
+    out = torch.empty(n, V, dtype=torch.float32, device=raw.device)
+    if n:
+        _lib.call('noise_coordinate_differences', flat.data_ptr(), int(flat.dtype == torch.bfloat16),
+                  flat.stride(0), yy.data_ptr(), n, V, float(sigma), out.data_ptr(), out.stride(0), _stream())
+    return out.view(*lead, V)
+
+
+def _probe(base, C_, y, steps, sq, dots, dir_sq, width, rows=None):
+    base = _f32_rows(base, 'base')
+    n, V = base.shape
+    C_ = _f32_rows(C_, 'C', V)
+    P = C_.shape[0]
+    K = P if rows is None else rows.shape[1]
+    dots = _f32_rows(dots, 'dots', K)
+    _need(dots.shape[0] == n, f'dots: expected {n} rows, got {dots.shape[0]}')
+    a = Probe()
+    a.base, a.ld_base = base.data_ptr(), base.stride(0)
+    a.C, a.ld_C = C_.data_ptr(), C_.stride(0)
+    yy = _targets(y, n)
+    st = _vec(steps, n, 'steps')
+    sqv = _vec(sq, n, 'sq')
+    a.y, a.steps, a.sq = yy.data_ptr(), st.data_ptr(), sqv.data_ptr()
+    a.dots, a.ld_dots = dots.data_ptr(), dots.stride(0)
+    keep = [base, C_, yy, st, sqv, dots]
+    if rows is None:
+        dsq = _vec(dir_sq, P, 'dir_sq')
+        a.dir_sq, a.ld_dir_sq = dsq.data_ptr(), 0
+        keep.append(dsq)
+    else:
+        _need(rows.is_cuda and not rows.is_floating_point() and rows.dim() == 2 and rows.shape[0] == n,
+              f'rows: expected an integer device tensor [{n}, K], got {tuple(rows.shape)}')
+        rr = rows.to(torch.int64).contiguous()
+        dsq = _f32_rows(dir_sq, 'dir_sq', K)
+        _need(dsq.shape[0] == n, f'dir_sq: expected {n} rows, got {dsq.shape[0]}')
+        a.rows, a.ld_rows = rr.data_ptr(), rr.stride(0)
+        a.dir_sq, a.ld_dir_sq = dsq.data_ptr(), dsq.stride(0)
+        keep += [rr, dsq]
+    a.n, a.P, a.K, a.V, a.width = n, P, K, V, int(width)
+    clean = torch.empty(n, dtype=torch.float32, device=base.device)
+    out = torch.empty(n, K, dtype=torch.float32, device=base.device)
+    a.clean_sum, a.out, a.ld_out = clean.data_ptr(), out.data_ptr(), out.stride(0)
+    if n:
+        _lib.call('noise_row_derivatives' if rows is not None else 'noise_cycle_derivatives', C.byref(a), _stream())
+    # `keep` holds the converted inputs until the launches are queued; torch's allocator reuses their
+    # memory only for later work on this same stream, which runs after these kernels.
+    return out
+
+
+def cycle_derivatives(base, C, y, steps, sq, dots, dir_sq, width=WIDTH):
+    """base [n, V] = W x; C [P, V] (row j = W D_j); y [n]; steps, sq [n, 1] or [n]; dots [n, P];
+    dir_sq [P] -> float32 [n, P]: (loss(x + s D_j) - loss(x)) / s for every token and direction."""
+    return _probe(base, C, y, steps, sq, dots, dir_sq, width)
+
+
+def row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq, width=WIDTH):
+    """rows [n, K] indices into C's rows; dots, dir_sq [n, K] -> float32 [n, K]."""
+    return _probe(base, C, y, steps, sq, dots, dir_sq, width, rows=rows)

@@ -49,3 +49,46 @@ def antithetic(noise, sigma):
     pairs = (first[0] if isinstance(first, tuple) else first).shape[0]
     sign = torch.tensor([sigma, -sigma], dtype=torch.float32).repeat(pairs)
     return member, sign
+
+
+def hadamard(d, dtype=torch.float32):
+    """The Sylvester Hadamard matrix of order d (a power of two), entries +-1."""
+    if d & (d - 1):
+        raise ValueError(f'Orthogonal draws need a power-of-two width, not {d}.')
+    H = torch.ones(1, 1, dtype=dtype)
+    while H.shape[0] < d:
+        H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
+    return H
+
+
+def probe_inputs(n, width=512, vocab=4096, probes=None, sigma=0.005, seed=0, logit_scale=3.0,
+                 x_rms=2.0, dirs='hadamard', masked=0.0, dtype=torch.float32):
+    """Inputs of the readout probe (train/speedrun/run.py:250-263) for n tokens, CPU tensors.
+
+    x [n, width] streams (N(0, x_rms^2)), weight [vocab, width] head (N(0, logit_scale^2 / width),
+    so normalised logits are about N(0, logit_scale^2)), stream_dirs D [width, P]: a full cycle of
+    sign-flipped Hadamard rows (dirs='hadamard', P = width) or Gaussian columns (dirs='gaussian').
+    Derived exactly as the reference's caller does: base = x W^T, C = (W D)^T, steps = sigma *
+    rms(x) clamped at 1e-6, sq = |x|^2, dots = x D, dir_sq = |D_j|^2. Targets are Zipf draws, a
+    fraction `masked` of them set to -1. Products are formed in float64 and rounded to `dtype`.
+    """
+    g = torch.Generator().manual_seed(seed)
+    f64 = torch.float64
+    x = torch.randn(n, width, generator=g, dtype=f64) * x_rms
+    weight = torch.randn(vocab, width, generator=g, dtype=f64) * (logit_scale / width ** 0.5)
+    if dirs == 'hadamard':
+        signs = torch.randint(0, 2, (width,), generator=g).to(f64) * 2 - 1
+        D = (hadamard(width, f64) * signs).T
+        if probes is not None:
+            D = D[:, :probes]
+    else:
+        D = torch.randn(width, probes or width, generator=g, dtype=f64)
+    y = zipf_tokens(n, vocab, seed=seed + 1)
+    if masked:
+        y[torch.rand(n, generator=g) < masked] = -1
+    x, weight, D = x.to(dtype).to(f64), weight.to(dtype).to(f64), D.to(dtype).to(f64)
+    out = dict(x=x, weight=weight, D=D, y=y,
+               base=x @ weight.T, C=(weight @ D).T.contiguous(),
+               steps=sigma * x.square().mean(-1).sqrt().clamp(min=1e-6),
+               sq=x.square().sum(-1), dots=x @ D, dir_sq=D.square().sum(0))
+    return {k: (v if k == 'y' else v.to(dtype)) for k, v in out.items()}

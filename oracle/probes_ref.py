@@ -1,0 +1,98 @@
+"""CPU oracle of the soft-capped log-sum-exp probe functions -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/ and bench.py's `cpu_baseline` leg may import this module, and only as the checker.
+The shipped path (noise_amd/probes.py over libnoise_amd) never calls it.
+
+Restatements in numpy float64 (float32 when asked) of three functions of the reference trainer:
+
+* `coordinate_differences` -- train/val/run.py:100-111 (train/speedrun/run.py:57-68): central
+  differences of each token's soft-capped cross-entropy along each of its own logits, in the
+  closed form log1p(w_v expm1(cap(raw_v +- sigma) - cap(raw_v))) with the target correction;
+* `cycle_derivatives`      -- train/val/run.py:154-167 (train/speedrun/run.py:90-103): forward
+  differences of each token's readout loss along every direction of a cycle, the moved stream's
+  RMS norm evaluated exactly from |x|^2, x.D_j and |D_j|^2;
+* `row_derivatives`        -- train/val/run.py:170-183: the same along per-token rows of the
+  direction set.
+
+cap(v) = 15 tanh(v / 15); norm(x) = x rsqrt(|x|^2 / width + eps), eps = float32 machine epsilon.
+
+Pinning (tests/test_oracle.py): each function against a brute-force evaluation that never uses
+its closed form -- the moved streams / logits are built explicitly and pushed through
+torch.nn.functional.cross_entropy in float64 (one forward per probe), and row_derivatives
+against cycle_derivatives gathered at the rows.
+"""
+import numpy as np
+
+CAP = 15.0
+EPS32 = float(np.finfo(np.float32).eps)
+
+
+def cap(v):
+    return CAP * np.tanh(v / CAP)
+
+
+def _logsumexp(z, axis=-1):
+    m = np.max(z, axis=axis, keepdims=True)
+    return (m + np.log(np.sum(np.exp(z - m), axis=axis, keepdims=True))).squeeze(axis)
+
+
+def coordinate_differences(raw, y, sigma, dtype=np.float64):
+    """raw (n, V) logits before the cap, y (n,) targets (negative: masked), sigma the logit step.
+    Returns (n, V): d loss / d raw_v by central differences (train/val/run.py:100-111)."""
+    raw = np.asarray(raw, dtype)
+    y = np.asarray(y)
+    s = dtype(sigma)
+    z, up, down = cap(raw), cap(raw + s), cap(raw - s)
+    weight = np.exp(z - _logsumexp(z)[:, None])
+    change = np.log1p(weight * np.expm1(up - z)) - np.log1p(weight * np.expm1(down - z))
+    rows = np.arange(raw.shape[0])
+    t = np.clip(y, 0, None)
+    change[rows, t] -= (up - down)[rows, t]
+    return change / (2 * s) * (y >= 0)[:, None]
+
+
+def _head_terms(base, y, sq, width, dtype):
+    t = np.clip(np.asarray(y), 0, None)
+    base_y = base[np.arange(base.shape[0]), t]
+    inv0 = 1.0 / np.sqrt(sq / dtype(width) + dtype(EPS32))
+    clean = _logsumexp(cap(base * inv0[:, None])) - cap(base_y * inv0)
+    return t, base_y, clean
+
+
+def cycle_derivatives(base, C, y, steps, sq, dots, dir_sq, width=512, dtype=np.float64, chunk=32):
+    """base (n, V) = W x of the clean streams; C (P, V) row j = W D_j; y (n,); steps (n,) step per
+    token; sq (n,) |x|^2; dots (n, P) x . D_j; dir_sq (P,) |D_j|^2. Returns (n, P)
+    (train/val/run.py:154-167)."""
+    base, C = np.asarray(base, dtype), np.asarray(C, dtype)
+    steps, sq = np.asarray(steps, dtype).reshape(-1), np.asarray(sq, dtype).reshape(-1)
+    dots, dir_sq = np.asarray(dots, dtype), np.asarray(dir_sq, dtype).reshape(-1)
+    y = np.asarray(y)
+    t, base_y, clean = _head_terms(base, y, sq, width, dtype)
+    out = np.empty((base.shape[0], C.shape[0]), dtype)
+    for i0 in range(0, base.shape[0], chunk):
+        sl = slice(i0, i0 + chunk)
+        s = steps[sl, None]
+        inv = 1.0 / np.sqrt((sq[sl, None] + 2 * s * dots[sl] + s * s * dir_sq[None]) / dtype(width) + dtype(EPS32))
+        z = (base[sl, None, :] + s[..., None] * C[None]) * inv[..., None]
+        dirs_y = C[:, t[sl]].T                                       # (m, P)
+        moved = _logsumexp(cap(z)) - cap((base_y[sl, None] + s * dirs_y) * inv)
+        out[sl] = (moved - clean[sl, None]) / s * (y[sl] >= 0)[:, None]
+    return out
+
+
+def row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq, width=512, dtype=np.float64):
+    """rows (n, K) indices into C's rows; dots, dir_sq (n, K). Returns (n, K)
+    (train/val/run.py:170-183)."""
+    base, C = np.asarray(base, dtype), np.asarray(C, dtype)
+    rows = np.asarray(rows)
+    steps, sq = np.asarray(steps, dtype).reshape(-1), np.asarray(sq, dtype).reshape(-1)
+    dots, dir_sq = np.asarray(dots, dtype), np.asarray(dir_sq, dtype)
+    y = np.asarray(y)
+    t, base_y, clean = _head_terms(base, y, sq, width, dtype)
+    dirs = C[rows]                                                   # (n, K, V)
+    dirs_y = dirs[np.arange(base.shape[0]), :, t]                    # (n, K)
+    s = steps[:, None]
+    inv = 1.0 / np.sqrt((sq[:, None] + 2 * s * dots + s * s * dir_sq) / dtype(width) + dtype(EPS32))
+    z = (base[:, None, :] + s[..., None] * dirs) * inv[..., None]
+    moved = _logsumexp(cap(z)) - cap((base_y[:, None] + s * dirs_y) * inv)
+    return (moved - clean[:, None]) / s * (y >= 0)[:, None]

@@ -1,0 +1,150 @@
+"""Parity of the probe kernels (libnoise_amd through noise_amd.probes) with the float64 oracle
+(oracle/probes_ref.py), on the same seeded inputs.
+
+Tolerances. The probes are differences of two soft-capped log-sum-exps over the vocabulary,
+divided by the step: in float32 the reference's own formula (train/val/run.py:154-167) is off from
+the exact value by up to ~4e-6 in (moved - clean) on these inputs (the oracle evaluated in
+float32 shows it), i.e. ~4e-6 / step on a derivative. The kernels are held to
+|gpu - exact| <= 8e-6 / step + 1e-5 |exact| per element and a mean error below 1.5e-6 / step.
+coordinate_differences forms cap(raw +- sigma) - cap(raw) without cancellation and is held to
+2e-6 + 1e-4 |exact|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from noise_amd.synthetic import probe_inputs
+from oracle import probes_ref as P
+
+pytestmark = pytest.mark.gpu
+
+ATOL_STEP, RTOL, MEAN_STEP = 8e-6, 1e-5, 1.5e-6
+
+
+def _probes():
+    from noise_amd import probes
+    return probes
+
+
+def _cuda(d, device):
+    return {k: v.to(device) for k, v in d.items()}
+
+
+def _check_probe(got, want, steps, mask_rows=(), nan_rows=()):
+    got = got.cpu().double().numpy()
+    s = steps.cpu().double().numpy().reshape(-1, 1)
+    ok = np.ones(got.shape[0], bool)
+    for i in mask_rows:
+        assert np.all(got[i] == 0), i
+        ok[i] = False
+    for i in nan_rows:
+        assert np.all(np.isnan(got[i])), i
+        ok[i] = False
+    err = np.abs(got[ok] - want[ok])
+    bound = ATOL_STEP / s[ok] + RTOL * np.abs(want[ok])
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert np.all(err <= bound), (worst, got[ok][worst], want[ok][worst], err[worst], bound[worst])
+    assert float((err * s[ok]).mean()) <= MEAN_STEP
+
+
+@pytest.mark.parametrize('n,P_,V,dirs', [(37, 72, 4096, 'hadamard'), (5, 3, 4096, 'gaussian'),
+                                        (64, 512, 4096, 'hadamard')])
+def test_cycle_derivatives_matches_oracle(device, n, P_, V, dirs):
+    d = probe_inputs(n, 512, V, probes=P_, sigma=0.005, dirs=dirs, seed=n + P_, masked=0.1)
+    y = d['y'].clone()
+    y[1] = -1
+    nan_row = n - 1
+    y[nan_row] = V                      # out of range: NaN row instead of a device fault
+    g = _cuda(d, device)
+    got = _probes().cycle_derivatives(g['base'], g['C'], y.to(device), g['steps'].view(-1, 1),
+                                      g['sq'].view(-1, 1), g['dots'], g['dir_sq'])
+    torch.cuda.synchronize()
+    yy = y.clone()
+    yy[nan_row] = 0
+    want = P.cycle_derivatives(d['base'], d['C'], yy, d['steps'], d['sq'], d['dots'], d['dir_sq'])
+    masked = [i for i in range(n) if y[i] < 0]
+    _check_probe(got, want, d['steps'], masked, [nan_row])
+
+
+def test_cycle_derivatives_full_cycle_sampled(device):
+    """The bench shape (one 2048-token sequence, a full cycle of 512, V = 4096), checked on a
+    sample of 12 tokens spread over the sequence."""
+    d = probe_inputs(2048, 512, 4096, sigma=0.005, seed=11)
+    g = _cuda(d, device)
+    got = _probes().cycle_derivatives(g['base'], g['C'], g['y'], g['steps'], g['sq'], g['dots'], g['dir_sq'])
+    torch.cuda.synchronize()
+    rows = np.linspace(0, 2047, 12).astype(int)
+    want = P.cycle_derivatives(d['base'][rows], d['C'], d['y'][rows], d['steps'][rows], d['sq'][rows],
+                               d['dots'][rows], d['dir_sq'])
+    assert torch.isfinite(got).all()
+    _check_probe(got[rows], want, d['steps'][rows])
+
+
+def test_cycle_derivatives_unaligned_rows(device):
+    """V = 1001 and rows at odd strides: the scalar-load path with a partial last chunk."""
+    n, P_, V = 9, 10, 1001
+    d = probe_inputs(n, 512, V, probes=P_, sigma=0.01, dirs='gaussian', seed=4)
+    base = torch.empty(n, V + 3, device=device)[:, 1:V + 1]
+    base.copy_(d['base'])
+    C = torch.empty(P_, V + 1, device=device)[:, :V]
+    C.copy_(d['C'])
+    g = _cuda(d, device)
+    got = _probes().cycle_derivatives(base, C, g['y'], g['steps'], g['sq'], g['dots'], g['dir_sq'])
+    torch.cuda.synchronize()
+    want = P.cycle_derivatives(d['base'], d['C'], d['y'], d['steps'], d['sq'], d['dots'], d['dir_sq'])
+    _check_probe(got, want, d['steps'])
+
+
+def test_row_derivatives_matches_oracle(device):
+    n, P_, K, V = 33, 64, 21, 4096
+    d = probe_inputs(n, 512, V, probes=P_, sigma=0.005, dirs='gaussian', seed=8)
+    gen = torch.Generator().manual_seed(2)
+    rows = torch.stack([torch.randperm(P_, generator=gen)[:K] for _ in range(n)])
+    dots = d['dots'].gather(1, rows)
+    dir_sq = d['dir_sq'][rows].contiguous()
+    bad = rows.clone()
+    bad[3, 5] = P_                          # an invalid row index: NaN in that slot only
+    g = _cuda(d, device)
+    got = _probes().row_derivatives(g['base'], g['C'], bad.to(device), g['y'], g['steps'], g['sq'],
+                                    dots.to(device), dir_sq.to(device))
+    torch.cuda.synchronize()
+    want = P.row_derivatives(d['base'], d['C'], rows, d['y'], d['steps'], d['sq'], dots, dir_sq)
+    got = got.cpu().double()
+    assert torch.isnan(got[3, 5])
+    got[3, 5] = float(want[3, 5])
+    _check_probe(got, want, d['steps'])
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_coordinate_differences_matches_oracle(device, dtype):
+    gen = torch.Generator().manual_seed(5)
+    n, V, sigma = 23, 4096, 0.1
+    raw = (torch.randn(n, V, generator=gen) * 8).to(dtype)
+    raw[0, :6] = torch.tensor([80., -80., 30., 0., 15., -15.]).to(dtype)
+    y = torch.randint(0, V, (n,), generator=gen)
+    y[2] = -1
+    y[4] = V
+    got = _probes().coordinate_differences(raw.to(device), y.to(device), sigma)
+    torch.cuda.synchronize()
+    yy = y.clone()
+    yy[4] = 0
+    want = P.coordinate_differences(raw.double().numpy(), yy.numpy(), sigma)
+    got = got.cpu().double().numpy()
+    assert np.all(got[2] == 0)
+    assert np.all(np.isnan(got[4]))
+    keep = [i for i in range(n) if i not in (2, 4)]
+    np.testing.assert_allclose(got[keep], want[keep], rtol=1e-4, atol=2e-6)
+
+
+def test_coordinate_differences_reference_layout(device):
+    """The reference's call: raw [b, t, V] bf16 (a slice of a padded head output), y [b, t]."""
+    gen = torch.Generator().manual_seed(6)
+    b, t, V = 2, 7, 4096
+    padded = (torch.randn(b, t, V + 128, generator=gen) * 6).to(torch.bfloat16)
+    raw = padded.to(device)[..., :V]
+    y = torch.randint(-1, V, (b, t), generator=gen)
+    got = _probes().coordinate_differences(raw, y.to(device), 0.1)
+    torch.cuda.synchronize()
+    assert got.shape == (b, t, V) and got.dtype == torch.float32
+    want = P.coordinate_differences(padded[..., :V].double().reshape(-1, V).numpy(), y.reshape(-1).numpy(), 0.1)
+    np.testing.assert_allclose(got.reshape(-1, V).cpu().double().numpy(), want, rtol=1e-4, atol=2e-6)

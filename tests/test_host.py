@@ -47,6 +47,21 @@ def test_argument_errors_raise_before_launch():
     assert st == _lib.NOISE_EINVAL
     with pytest.raises(FloatingPointError):
         _lib.check(_lib.NOISE_ENONFINITE)
+    # Probe entry points: a non-positive sigma, short row strides and a NULL C are rejected; an
+    # empty batch is a no-op.
+    y = C.c_void_p(512)
+    assert lib.noise_coordinate_differences(fake, 0, 64, y, 4, 64, 0.0, fake, 64, None) == _lib.NOISE_EINVAL
+    assert lib.noise_coordinate_differences(fake, 0, 32, y, 4, 64, 0.1, fake, 64, None) == _lib.NOISE_EINVAL
+    assert lib.noise_coordinate_differences(fake, 0, 64, y, 0, 64, 0.1, fake, 64, None) == _lib.NOISE_OK
+    a = _lib.Probe(base=256, ld_base=32, C=256, ld_C=64, y=512, steps=256, sq=256, dots=256, ld_dots=8,
+                   dir_sq=256, n=4, P=8, K=0, V=64, width=512, clean_sum=256, out=256, ld_out=8)
+    assert lib.noise_cycle_derivatives(C.byref(a), None) == _lib.NOISE_EINVAL      # ld_base < V
+    a.n = 0
+    assert lib.noise_cycle_derivatives(C.byref(a), None) == _lib.NOISE_OK
+    a.n, a.ld_base, a.K = 4, 64, 3
+    assert lib.noise_row_derivatives(C.byref(a), None) == _lib.NOISE_EINVAL        # rows is NULL
+    with pytest.raises(ValueError, match='rows'):
+        _lib.check(_lib.NOISE_EINVAL)
 
 
 def test_state_dict_strict_round_trip():
