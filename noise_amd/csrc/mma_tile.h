@@ -16,6 +16,9 @@
 //     therefore fetches the logical chunk the swizzle maps there;
 //   * one s_waitcnt vmcnt + s_barrier per stage (inline asm with a memory clobber: the compiler's
 //     own fence would wait for every load in flight, including the later stages).
+//   * the fragments of k-step ks + 1 are read (inline-asm ds_read_b128, explicit lgkmcnt waits)
+//     while the MFMAs of k-step ks run: left to itself the compiler folded the two fragment sets
+//     into one and waited for every read right before its MFMAs (+3-4% on the step when fixed).
 // Measured on MI355X against the register-staged two-buffer loop it replaces: +12-15% in the
 // main loop. With 256-column tiles two 64-deep stages beat three 32-deep ones by 4-8% (whole
 // 128-byte lines per row); 128-column tiles keep three 32-deep stages (two workgroups per CU).
@@ -93,8 +96,15 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
   int kofs[KB / 16];
 #pragma unroll
   for (int ks = 0; ks < KB / 16; ++ks) kofs[ks] = ((2 * ks + (lane >> 5)) ^ sw) * 8;
-  const uint16_t* fa = smem + far * KB;
-  const uint16_t* fb = smem + BOFS + fbr * KB;
+  // LDS byte addresses of this lane's fragment rows per k-step in stage buffer 0; a buffer adds
+  // BUF * 2 bytes and a 32-row block 32 * KB * 2 (an immediate offset).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)smem;
+  uint32_t fra[KB / 16], frb[KB / 16];
+#pragma unroll
+  for (int ks = 0; ks < KB / 16; ++ks) {
+    fra[ks] = lds0 + (uint32_t)(far * KB + kofs[ks]) * 2;
+    frb[ks] = lds0 + (uint32_t)(BOFS + fbr * KB + kofs[ks]) * 2;
+  }
   bf16x8 a0[4], b0[2], a1[4], b1[2];
 
 // Stage KT_ (clamped to the last one: the surplus loads keep the wait counts exact) into buffer BUF_.
@@ -111,14 +121,24 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
       __builtin_amdgcn_global_load_lds((const void*)(bsrc_ + gb[i] + k0_),                  \
                                        (void*)(lb + (BUF_) * BUF + i * RPI * KB), 16, 0, 0); \
   }
+// Fragment reads of k-step KS_ from stage buffer BUF_, as inline asm: the compiler neither sinks
+// them next to their use nor waits for them on its own (it cannot see that they are in flight),
+// so the loop below waits for exactly the reads each MFMA group needs (NOISE_FWAIT).
 #define NOISE_FLOAD(FA, FB, BUF_, KS_)                                                        \
   {                                                                                         \
-    const uint16_t* pa_ = fa + kofs[KS_] + (BUF_) * BUF;                                    \
-    const uint16_t* pb_ = fb + kofs[KS_] + (BUF_) * BUF;                                    \
+    const uint32_t pa_ = fra[KS_] + (uint32_t)(BUF_) * (BUF * 2);                           \
+    const uint32_t pb_ = frb[KS_] + (uint32_t)(BUF_) * (BUF * 2);                           \
     _Pragma("unroll") for (int i = 0; i < 4; ++i)                                           \
-      FA[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pa_ + i * 32 * KB)); \
+      __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(FA[i]) : "v"(pa_), "n"(i * 64 * KB)); \
     _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
-      FB[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(pb_ + i * 32 * KB)); \
+      __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(FB[i]) : "v"(pb_), "n"(i * 64 * KB)); \
+  }
+// Wait until at most N_ LDS reads are in flight, then tie the fragments to that point so that no
+// MFMA reading them is scheduled before the wait.
+#define NOISE_FWAIT(N_, FA, FB)                                                               \
+  {                                                                                         \
+    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N_));                                    \
+    __asm__ volatile("" : "+v"(FA[0]), "+v"(FA[1]), "+v"(FA[2]), "+v"(FA[3]), "+v"(FB[0]), "+v"(FB[1])); \
   }
 #define NOISE_MFMA8(FA, FB)                                                                   \
   _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                          \
@@ -137,17 +157,29 @@ NOISE_DEV void mma_tile(const uint16_t* __restrict__ A, int64_t lda, int a_rows,
     // so its buffer takes stage kt + NS - 1.
     __asm__ volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WAIT) : "memory");
     NOISE_DLOAD(kt + NS - 1, (kt + NS - 1) % NS)
+    // Fragments of k-step ks + 1 are read while the MFMAs of k-step ks run; the scheduling
+    // barriers keep each MFMA group between the wait for its fragments and the next reads.
+    NOISE_FLOAD(a0, b0, cur, 0)
 #pragma unroll
     for (int kp = 0; kp < KB / 32; ++kp) {
-      NOISE_FLOAD(a0, b0, cur, 2 * kp)
       NOISE_FLOAD(a1, b1, cur, 2 * kp + 1)
+      NOISE_FWAIT(6, a0, b0)
       NOISE_MFMA8(a0, b0)
+      __builtin_amdgcn_sched_barrier(0);
+      if (2 * kp + 2 < KB / 16) {
+        NOISE_FLOAD(a0, b0, cur, 2 * kp + 2)
+        NOISE_FWAIT(6, a1, b1)
+      } else {
+        NOISE_FWAIT(0, a1, b1)
+      }
       NOISE_MFMA8(a1, b1)
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // Drain the surplus loads before the caller reuses smem.
   __asm__ volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #undef NOISE_MFMA8
+#undef NOISE_FWAIT
 #undef NOISE_FLOAD
 #undef NOISE_DLOAD
 }
