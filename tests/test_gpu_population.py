@@ -79,6 +79,20 @@ def test_clean_forward_matches_reference(device, init_params, golden):
     assert abs(float(ce.mean()) - float(t(golden['config0/clean']).mean())) <= 1e-4
 
 
+def test_evaluate_matches_oracle(device, init_params, tmp_path):
+    """noise_amd.evaluate (utils/eval.py:34-53) on a 3-row split file: the mean loss over every
+    prediction equals the oracle's clean forward of the same rows with bf16-rounded embeddings."""
+    from noise_amd import evaluate as E
+    from noise_amd.synthetic import zipf_tokens
+    rows = zipf_tokens(3 * E.SEQ, seed=7).view(3, E.SEQ)
+    torch.save(rows.to(torch.int32), tmp_path / 'val.pt')
+    value = E.evaluate(init_params, tmp_path, batch_size=2, rows=3, expected=None)
+    p = {k: (v.bfloat16().float() if k == 'transformer.wte.weight' or k.startswith('value_embeds.') else v)
+         for k, v in init_params.items()}
+    oracle = R.clean_loss(p, rows[:, :-1], rows[:, 1:], policy='build').double().mean()
+    assert abs(value - float(oracle)) <= 1e-4, (value, float(oracle))
+
+
 def test_chunking_and_member_permutation(device, init_params):
     """Chunk boundaries do not change a member's loss; permuting members permutes losses bit-exactly."""
     idx, targets = sequence(256, seed=21)

@@ -99,3 +99,20 @@ def test_population_loss_rejects_cpu_tensors():
     with pytest.raises(ValueError, match='GPU'):
         noise_amd.population_loss(None, p, {}, torch.zeros(2), torch.zeros(4, dtype=torch.long),
                                   torch.zeros(4, dtype=torch.long))
+
+
+def test_eval_rows_and_hash(tmp_path):
+    """load_rows (utils/prepare_data.py:39-47): shape check, sha256 of the int32 bytes against the
+    pinned digest for a file named in the table, int64 out."""
+    from noise_amd import evaluate as E
+    x = torch.arange(3 * E.SEQ, dtype=torch.int64).view(3, E.SEQ) % 4096
+    assert E.token_hash(x) == __import__('hashlib').sha256(x.to(torch.int32).numpy().tobytes()).hexdigest()
+    torch.save(x.to(torch.int32), tmp_path / 'rows.pt')
+    got = E.load_rows(tmp_path / 'rows.pt', 3)
+    assert got.dtype == torch.int64 and torch.equal(got, x)
+    with pytest.raises(ValueError, match='token tensor'):
+        E.load_rows(tmp_path / 'rows.pt', 4)
+    torch.save(x, tmp_path / 'val.pt')  # the pinned name, wrong tokens
+    with pytest.raises(ValueError, match='hash mismatch'):
+        E.load_rows(tmp_path / 'val.pt', 3)
+    assert torch.equal(E.load_rows(tmp_path / 'val.pt', 3, expected=None), x)
