@@ -245,6 +245,61 @@ int noise_cycle_derivatives(const noise_probe_t* args, void* stream);
  * (train/val/run.py:170-183). A row index outside [0, P) makes that output NaN. */
 int noise_row_derivatives(const noise_probe_t* args, void* stream);
 
+/* ---- Chain moves with every attention held (chain_chunk, train/val/run.py:307-351, own = None)
+ * Rows are (token i, move p) pairs, row = i * P + p, W wide. */
+
+/* dx0 = norm(e_i + move_row) - x0_i, delta = mix * dx0 (run.py:324-326; mix = lam_r[0] + lam_0[0]). */
+int noise_chain_start(const float* e, const float* x0, const float* move, int m, int P, int W,
+                      float mix, float* dx0, float* delta, void* stream);
+
+typedef struct {
+  float* delta;            /* [m * P, W] moves, updated in place */
+  const float* dx0;        /* NULL, or [m * P, W] moves of x0 (site < 0) */
+  int mix;                 /* first delta = lam_r delta + lam_0 dx0 (every block after the first) */
+  float lam_r, lam_0;
+  const float* mid;        /* [m, W] the block's clean mid stream */
+  const int64_t* idx;      /* [m, ld_idx] routed units of each token, in [0, H) (else NaN) */
+  int64_t ld_idx;
+  const float* hs;         /* [m, ld_hs] their clean pre-activations */
+  int64_t ld_hs;
+  const uint16_t* w_fc;    /* [H, W] bf16 c_fc.weight */
+  const uint16_t* w_out_t; /* [H, W] bf16 c_proj.weight transposed */
+  int m, P, W, k, H;       /* W % 256 == 0, W <= 2048, k % 128 == 0 */
+  uint16_t* dz;            /* workspace [m * P, W] bf16 (16-byte aligned, as the next three) */
+  uint16_t* wf;            /* workspace [m, k, W] bf16 */
+  uint16_t* wo;            /* workspace [m, W, k] bf16 */
+  uint16_t* g;             /* workspace [m * P, k] bf16 */
+} noise_chain_block_t;
+
+/* One block of the chain (run.py:327-350): the optional mix, dz = norm_difference(mid, delta) in
+ * bf16, dh = bf16(dz W_fc[idx]^T), g = bf16((relu(h + dh) - relu(h))(relu(h + dh) + relu(h))),
+ * delta += bf16(g W_out_t[idx]). */
+int noise_chain_block(const noise_chain_block_t* args, void* stream);
+
+typedef struct {
+  const float* delta;      /* [m * P, W] */
+  const float* xL;         /* [m, W] clean top stream */
+  const float* base;       /* [m, ld_base] xL W^T */
+  int64_t ld_base;
+  const uint16_t* weight;  /* [V, W] bf16 head weight (the reference's weight_t transposed) */
+  const float* target_w;   /* [m, W] fp32 head rows of the targets */
+  const int64_t* y;        /* [m] targets; < 0 masks the token, >= V gives NaN */
+  const float* scale;      /* [m, ld_scale] step of each move */
+  int64_t ld_scale;
+  int m, P, W, V;          /* V % 256 == 0 */
+  float* out;              /* [m, ld_out] */
+  int64_t ld_out;
+  uint16_t* dbf;           /* workspace [m * P, W] bf16 (16-byte aligned) */
+  float* inv;              /* workspace [m * P] */
+  float* zy;               /* workspace [m * P] */
+  float* clean;            /* workspace [2 m] */
+} noise_chain_head_t;
+
+/* The head of the chain (run.py:341-351): z = (base + bf16(bf16(delta) W^T)) inv, inv from
+ * |xL + delta|, LSE of the capped z over V fused into the head product, the target term in fp32,
+ * out = (moved - clean) / scale. */
+int noise_chain_head(const noise_chain_head_t* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

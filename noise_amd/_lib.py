@@ -57,6 +57,19 @@ class Probe(C.Structure):
                 ('clean_sum', P), ('out', P), ('ld_out', I64)]
 
 
+class ChainBlock(C.Structure):
+    _fields_ = [('delta', P), ('dx0', P), ('mix', INT), ('lam_r', F32), ('lam_0', F32), ('mid', P),
+                ('idx', P), ('ld_idx', I64), ('hs', P), ('ld_hs', I64), ('w_fc', P), ('w_out_t', P),
+                ('m', INT), ('P', INT), ('W', INT), ('k', INT), ('H', INT),
+                ('dz', P), ('wf', P), ('wo', P), ('g', P)]
+
+
+class ChainHead(C.Structure):
+    _fields_ = [('delta', P), ('xL', P), ('base', P), ('ld_base', I64), ('weight', P), ('target_w', P),
+                ('y', P), ('scale', P), ('ld_scale', I64), ('m', INT), ('P', INT), ('W', INT), ('V', INT),
+                ('out', P), ('ld_out', I64), ('dbf', P), ('inv', P), ('zy', P), ('clean', P)]
+
+
 # name -> (restype, argtypes); every function returns an int status.
 SIGNATURES = {
     'noise_abi_version': [],
@@ -75,6 +88,9 @@ SIGNATURES = {
     'noise_coordinate_differences': [P, INT, I64, P, INT, INT, F32, P, I64, P],
     'noise_cycle_derivatives': [C.POINTER(Probe), P],
     'noise_row_derivatives': [C.POINTER(Probe), P],
+    'noise_chain_start': [P, P, P, INT, INT, INT, F32, P, P, P],
+    'noise_chain_block': [C.POINTER(ChainBlock), P],
+    'noise_chain_head': [C.POINTER(ChainHead), P],
 }
 
 _lib = None

@@ -1,0 +1,395 @@
+// Chain moves of the attention-cut estimator with every attention held (train/val/run.py:307-351,
+// own = None): moves of one site's stream carried through the later blocks' routed MLPs to the
+// head, and the forward difference of each token's soft-capped loss.
+//
+// Rows are (token i, move p) pairs, row = i * P + p, each W wide. Per chunk:
+//   start   (site < 0)  dx0 = norm(e_i + move) - x0_i, delta = (lam_r[0] + lam_0[0]) dx0
+//   block b             delta = lam_r[b] delta + lam_0[b] dx0 (after the first block), then
+//                       dz = norm(mid_i + delta) - norm(mid_i) in closed form, rounded to bf16;
+//                       dh = bf16(dz W_fc[idx_i]^T)      (P x k per token: batched MFMA GEMM)
+//                       g = bf16((relu(h + dh) - relu(h)) (relu(h + dh) + relu(h)))
+//                       delta += bf16(g W_out_t[idx_i])  (P x W per token: batched MFMA GEMM)
+//   head                z = (base_i + bf16(bf16(delta) W^T)) inv, LSE over the vocabulary fused into
+//                       the GEMM's epilogue (a workgroup owns 256 rows and sweeps V), minus the
+//                       clean LSE, the target term by tanh differences, divided by the step.
+// The bf16 roundings are the reference's own (bmm / matmul of bf16 tensors return bf16). The
+// gathered weights W_fc[idx_i] (k x W) and W_out_t[idx_i]^T (W x k) are materialised per token,
+// as the reference does, so that both routed products are plain K-contiguous MFMA GEMMs.
+#include "mma_tile.h"
+#include "softcap.h"
+
+namespace {
+
+using noise::CAP_EPS32;
+using noise::CAP_K1;
+
+// One wave per row of W (a multiple of 64, at most 2048) floats: lane l holds entries l + 64 t.
+constexpr int MAXT = 32;
+
+__global__ __launch_bounds__(256) void chain_start_kernel(const float* __restrict__ e,
+                                                          const float* __restrict__ x0,
+                                                          const float* __restrict__ move, int rows, int P,
+                                                          int W, float mix, float* __restrict__ dx0,
+                                                          float* __restrict__ delta) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t i = r / P;
+  const int nt = W / 64;
+  float u[MAXT];
+  float sq = 0.f;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      u[t] = e[i * W + lane + 64 * t] + move[r * W + lane + 64 * t];
+      sq += u[t] * u[t];
+    }
+  const float inv = rsqrtf(wave_sum(sq) / (float)W + CAP_EPS32);
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      const float d = u[t] * inv - x0[i * W + lane + 64 * t];
+      dx0[r * W + lane + 64 * t] = d;
+      delta[r * W + lane + 64 * t] = mix * d;
+    }
+}
+
+// delta = lam_r delta + lam_0 dx0 (when mix), then dz = norm_difference(mid_i, delta) in bf16
+// (train/val/run.py:246-253): delta inv + mid (inv - inv0).
+__global__ __launch_bounds__(256) void chain_pre_kernel(float* __restrict__ delta,
+                                                        const float* __restrict__ dx0,
+                                                        const float* __restrict__ mid, int rows, int P, int W,
+                                                        int mix, float lam_r, float lam_0,
+                                                        uint16_t* __restrict__ dz) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t i = r / P;
+  const int nt = W / 64;
+  float d[MAXT], x[MAXT];
+  float sq = 0.f, dot = 0.f, dsq = 0.f;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      const int64_t o = r * W + lane + 64 * t;
+      float v = delta[o];
+      if (mix) {
+        v = lam_r * v + (dx0 ? lam_0 * dx0[o] : 0.f);
+        delta[o] = v;
+      }
+      d[t] = v;
+      x[t] = mid[i * W + lane + 64 * t];
+      sq += x[t] * x[t];
+      dot += x[t] * v;
+      dsq += v * v;
+    }
+  sq = wave_sum(sq);
+  dot = wave_sum(dot);
+  dsq = wave_sum(dsq);
+  const float inv0 = rsqrtf(sq / (float)W + CAP_EPS32);
+  const float inv = rsqrtf((sq + 2.f * dot + dsq) / (float)W + CAP_EPS32);
+  const float dinv = inv - inv0;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) dz[r * W + lane + 64 * t] = f2bf(d[t] * inv + x[t] * dinv);
+}
+
+// wf[i][kk][:] = w_fc[idx[i][kk]][:]  and  wo[i][n][kk] = w_out_t[idx[i][kk]][n], through LDS in
+// blocks of 64 columns. An index outside [0, H) gathers NaN.
+__global__ __launch_bounds__(256) void chain_gather_kernel(const uint16_t* __restrict__ w_fc,
+                                                           const uint16_t* __restrict__ w_out_t,
+                                                           const int64_t* __restrict__ idx, int64_t ld_idx,
+                                                           int k, int H, int W, uint16_t* __restrict__ wf,
+                                                           uint16_t* __restrict__ wo) {
+  __shared__ uint16_t tile[256][65];
+  const int64_t i = blockIdx.y;
+  const int c0 = blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  const uint16_t NANBF = 0x7fc0;
+  for (int kb = 0; kb < k; kb += 256) {
+    const int kn = min(256, k - kb);
+    // rows kb .. kb + kn of the gathered sets, columns c0 .. c0 + 63
+    for (int e = tid; e < kn * 64; e += 256) {
+      const int kk = e / 64, c = e % 64;
+      const int64_t u = idx[i * ld_idx + kb + kk];
+      const bool ok = u >= 0 && u < H;
+      wf[(i * k + kb + kk) * W + c0 + c] = ok ? w_fc[u * W + c0 + c] : NANBF;
+      tile[kk][c] = ok ? w_out_t[u * W + c0 + c] : NANBF;
+    }
+    __syncthreads();
+    for (int e = tid; e < kn * 64; e += 256) {
+      const int c = e / kn, kk = e % kn;
+      wo[(i * W + c0 + c) * k + kb + kk] = tile[kk][c];
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- routed MLP products
+
+constexpr int MODE_RELUDIFF = 0, MODE_ADDROUND = 1;
+
+struct ChainGemm {
+  const uint16_t* A;   // [m * P, K] rows of the batch at i * P
+  const uint16_t* B;   // per batch [N, K] at i * N * K
+  int P, N, K;
+  const float* hs;     // MODE_RELUDIFF: [m, ld_hs] clean pre-activations
+  int64_t ld_hs;
+  uint16_t* G;         // MODE_RELUDIFF out [m * P, N] bf16
+  float* delta;        // MODE_ADDROUND in/out [m * P, N] fp32
+};
+
+template <int MODE, int BN>
+__global__ void __attribute__((amdgpu_flat_work_group_size(2 * BN, 2 * BN), amdgpu_waves_per_eu(2, 2)))
+chain_gemm_kernel(const ChainGemm g) {
+  constexpr int NSTG = BN == 256 ? 2 : 3, KDEPTH = BN == 256 ? 64 : 32;
+  using Cfg = noise::TileCfg<BN, NSTG, KDEPTH>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[Cfg::SMEM_ELEMS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int WN = BN / 64;
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t i = blockIdx.z;
+  const int p0 = blockIdx.x * 256, n0 = blockIdx.y * BN;
+  floatx16 acc[4][2];
+  noise::zero_acc(acc);
+  noise::mma_tile<BN, NSTG, KDEPTH>(g.A + (i * g.P + p0) * g.K, g.K, g.P - p0,
+                                    g.B + (i * g.N + n0) * g.K, g.K, g.K, smem, acc);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+      float h = 0.f;
+      if (MODE == MODE_RELUDIFF) h = g.hs[i * g.ld_hs + col];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int p = p0 + wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        if (p >= g.P) continue;
+        const float c = bf2f(f2bf(acc[mi][ni][j]));
+        const int64_t o = (i * g.P + p) * g.N + col;
+        if (MODE == MODE_RELUDIFF) {
+          const float up = fmaxf(h + c, 0.f), dn = fmaxf(h, 0.f);
+          g.G[o] = f2bf((up - dn) * (up + dn));
+        } else {
+          g.delta[o] += c;
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------- head
+
+// Per row: inv = rsqrt((|xL|^2 + 2 xL.delta + |delta|^2) / W + eps), zy = (base_y + delta.tw) inv
+// (the reference's target term, in fp32), bf16(delta) for the head product.
+__global__ __launch_bounds__(256) void chain_head_prep_kernel(const float* __restrict__ delta,
+                                                              const float* __restrict__ xL,
+                                                              const float* __restrict__ base, int64_t ld_base,
+                                                              const float* __restrict__ tw,
+                                                              const int64_t* __restrict__ y, int rows, int P,
+                                                              int W, int V, uint16_t* __restrict__ dbf,
+                                                              float* __restrict__ inv_out,
+                                                              float* __restrict__ zy_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t i = r / P;
+  const int nt = W / 64;
+  float sq = 0.f, dot = 0.f, dsq = 0.f, ty = 0.f;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      const float d = delta[r * W + lane + 64 * t], x = xL[i * W + lane + 64 * t];
+      sq += x * x;
+      dot += x * d;
+      dsq += d * d;
+      ty += d * tw[i * W + lane + 64 * t];
+      dbf[r * W + lane + 64 * t] = f2bf(d);
+    }
+  sq = wave_sum(sq);
+  dot = wave_sum(dot);
+  dsq = wave_sum(dsq);
+  ty = wave_sum(ty);
+  if (lane == 0) {
+    const float inv = rsqrtf((sq + 2.f * dot + dsq) / (float)W + CAP_EPS32);
+    const int64_t t = y[i];
+    const int64_t tc = t < 0 ? 0 : (t < V ? t : 0);
+    inv_out[r] = inv;
+    zy_out[r] = (base[i * ld_base + tc] + ty) * inv;
+  }
+}
+
+// One wave per token: the clean sum S0_i = sum_v exp(cap(base_iv inv0_i) - 15) into clean[i] and the
+// clean target logit z0_y = base_iy inv0_i into clean[m + i].
+__global__ __launch_bounds__(256) void chain_clean_kernel(const float* __restrict__ base, int64_t ld_base,
+                                                          const float* __restrict__ xL,
+                                                          const int64_t* __restrict__ y, int m, int W, int V,
+                                                          float* __restrict__ clean) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= m) return;
+  float sq = 0.f;
+  for (int c = lane; c < W; c += 64) sq += xL[(int64_t)i * W + c] * xL[(int64_t)i * W + c];
+  const float inv0 = rsqrtf(wave_sum(sq) / (float)W + CAP_EPS32);
+  const float s = noise::row_capexp_sum<false>(base + (int64_t)i * ld_base, V, inv0, lane);
+  const int64_t t = y[i];
+  const int64_t tc = t < 0 ? 0 : (t < V ? t : 0);
+  if (lane == 0) {
+    clean[i] = s;
+    clean[m + i] = base[(int64_t)i * ld_base + tc] * inv0;
+  }
+}
+
+struct ChainHead {
+  const uint16_t* dbf;   // [m * P, W] bf16 moves
+  const uint16_t* w;     // [V, W] bf16 head weight (weight_t transposed)
+  const float* base;     // [m, ld_base]
+  int64_t ld_base;
+  const float* inv;      // [m * P]
+  const float* zy;       // [m * P]
+  const float* clean;    // [2 m]: clean sums, then clean target logits
+  const float* scale;    // [m, ld_scale]
+  int64_t ld_scale;
+  const int64_t* y;      // [m]
+  int m, P, W, V;
+  float* out;            // [m, ld_out]
+  int64_t ld_out;
+};
+
+constexpr int HBN = 256, HWN = HBN / 64, HNS = 2, HKB = 64;
+using HCfg = noise::TileCfg<HBN, HNS, HKB>;
+
+// A workgroup owns 256 rows and sweeps the vocabulary in 256-column tiles of mma_tile, keeping per
+// row the running sum of exp(cap(z) - 15), z = (base + bf16(acc)) inv.
+__global__ void __attribute__((amdgpu_flat_work_group_size(HCfg::THREADS, HCfg::THREADS), amdgpu_waves_per_eu(2, 2)))
+chain_head_kernel(const ChainHead g) {
+  constexpr int ROWS_BYTES = (2 + HWN) * 256 * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ROWS_BYTES + 2 * HCfg::SMEM_ELEMS];
+  float* ik_s = reinterpret_cast<float*>(lds);
+  int* tok_s = reinterpret_cast<int*>(lds + 1024);
+  float(*sum_s)[256] = reinterpret_cast<float(*)[256]>(lds + 2048);
+  uint16_t* smem = reinterpret_cast<uint16_t*>(lds + ROWS_BYTES);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / HWN, wn = wave % HWN;
+  const int M = g.m * g.P;
+  const int m0 = blockIdx.x * 256;
+  if (tid < 256) {
+    const int row = m0 + tid < M ? m0 + tid : M - 1;
+    ik_s[tid] = g.inv[row] * CAP_K1;
+    tok_s[tid] = row / g.P;
+  }
+  // (the per-row arrays are read after the main loop's first barrier)
+  float rsum[4] = {0.f, 0.f, 0.f, 0.f};
+  const uint16_t* A = g.dbf + (int64_t)m0 * g.W;
+  for (int n0 = 0; n0 < g.V; n0 += HBN) {
+    floatx16 acc[4][2];
+    noise::zero_acc(acc);
+    noise::mma_tile<HBN, HNS, HKB>(A, g.W, M - m0, g.w + (int64_t)n0 * g.W, g.W, g.W, smem, acc);
+    const int colbase = n0 + wn * 64 + (lane & 31);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      float es[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int rl = wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const float ik = ik_s[rl];
+        const float* brow = g.base + (int64_t)tok_s[rl] * g.ld_base + colbase;
+        es[j] = noise::capexp(brow[0] + bf2f(f2bf(acc[mi][0][j])), ik) +
+                noise::capexp(brow[32] + bf2f(f2bf(acc[mi][1][j])), ik);
+      }
+      rsum[mi] += noise::halfwave_transpose_sum16(es, lane);
+    }
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const int jj = (lane & 31) >> 1;
+    const int rl = wm * 128 + mi * 32 + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+    if ((lane & 1) == 0) sum_s[wn][rl] = rsum[mi];
+  }
+  __syncthreads();
+  if (tid < 256 && m0 + tid < M) {
+    const int row = m0 + tid, i = row / g.P, p = row - i * g.P;
+    float S = 0.f;
+#pragma unroll
+    for (int c = 0; c < HWN; ++c) S += sum_s[c][tid];
+    const int64_t t = g.y[i];
+    float* o = g.out + (int64_t)i * g.ld_out + p;
+    if (t < 0) {
+      *o = 0.f;
+    } else if (t >= g.V) {
+      *o = __builtin_nanf("");
+    } else {
+      const float mmc = logf(S / g.clean[i]) - noise::cap_difference(g.zy[row], g.clean[g.m + i]);
+      *o = mmc / g.scale[(int64_t)i * g.ld_scale + p];
+    }
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int noise_chain_start(const float* e, const float* x0, const float* move, int m, int P, int W,
+                                 float mix, float* dx0, float* delta, void* stream) {
+  NOISE_REQUIRE(m >= 0 && P > 0 && W > 0 && W % 64 == 0 && W <= 64 * MAXT,
+                "chain_start: bad sizes (m=%d P=%d W=%d; W a multiple of 64 up to 2048)", m, P, W);
+  if (m == 0) return NOISE_OK;
+  NOISE_REQUIRE(e && x0 && move && dx0 && delta, "chain_start: NULL argument");
+  const int rows = m * P;
+  chain_start_kernel<<<(rows + 3) / 4, 256, 0, (hipStream_t)stream>>>(e, x0, move, rows, P, W, mix, dx0, delta);
+  return noise::check_launch("chain_start");
+}
+
+extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
+  NOISE_REQUIRE(a, "chain_block: args is NULL");
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 64 * MAXT && a->k > 0 &&
+                    a->k % 128 == 0 && a->H > 0,
+                "chain_block: bad sizes (m=%d P=%d W=%d k=%d H=%d; W a multiple of 256 up to 2048, k of 128)",
+                a->m, a->P, a->W, a->k, a->H);
+  if (a->m == 0) return NOISE_OK;
+  NOISE_REQUIRE(a->delta && a->mid && a->idx && a->hs && a->w_fc && a->w_out_t && a->dz && a->wf && a->wo && a->g,
+                "chain_block: NULL argument");
+  NOISE_REQUIRE(a->ld_idx >= a->k && a->ld_hs >= a->k, "chain_block: ld_idx / ld_hs below k");
+  NOISE_REQUIRE(aligned16(a->dz) && aligned16(a->wf) && aligned16(a->wo) && aligned16(a->g),
+                "chain_block: workspace buffers must be 16-byte aligned");
+  NOISE_REQUIRE(a->m <= 65535 && (int64_t)a->m * a->P < (1ll << 31), "chain_block: at most 65535 tokens per call");
+  const hipStream_t st = (hipStream_t)stream;
+  const int rows = a->m * a->P;
+  const int64_t tiles_p = (a->P + 255) / 256;
+  chain_pre_kernel<<<(rows + 3) / 4, 256, 0, st>>>(a->delta, a->dx0, a->mid, rows, a->P, a->W, a->mix,
+                                                    a->lam_r, a->lam_0, a->dz);
+  if (int e = noise::check_launch("chain_block")) return e;
+  chain_gather_kernel<<<dim3(a->W / 64, a->m), 256, 0, st>>>(a->w_fc, a->w_out_t, a->idx, a->ld_idx, a->k,
+                                                              a->H, a->W, a->wf, a->wo);
+  if (int e = noise::check_launch("chain_block")) return e;
+  ChainGemm g1{a->dz, a->wf, a->P, a->k, a->W, a->hs, a->ld_hs, a->g, nullptr};
+  chain_gemm_kernel<MODE_RELUDIFF, 128><<<dim3((unsigned)tiles_p, a->k / 128, a->m), 256, 0, st>>>(g1);
+  if (int e = noise::check_launch("chain_block")) return e;
+  ChainGemm g2{a->g, a->wo, a->P, a->W, a->k, nullptr, 0, nullptr, a->delta};
+  chain_gemm_kernel<MODE_ADDROUND, 256><<<dim3((unsigned)tiles_p, a->W / 256, a->m), 512, 0, st>>>(g2);
+  return noise::check_launch("chain_block");
+}
+
+extern "C" int noise_chain_head(const noise_chain_head_t* a, void* stream) {
+  NOISE_REQUIRE(a, "chain_head: args is NULL");
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 64 == 0 && a->W <= 64 * MAXT && a->V > 0 &&
+                    a->V % 256 == 0,
+                "chain_head: bad sizes (m=%d P=%d W=%d V=%d; V a multiple of 256)", a->m, a->P, a->W, a->V);
+  if (a->m == 0) return NOISE_OK;
+  NOISE_REQUIRE(a->delta && a->xL && a->base && a->weight && a->target_w && a->y && a->scale && a->out &&
+                    a->dbf && a->inv && a->zy && a->clean,
+                "chain_head: NULL argument");
+  NOISE_REQUIRE(a->ld_base >= a->V && a->ld_scale >= a->P && a->ld_out >= a->P, "chain_head: row strides too small");
+  NOISE_REQUIRE(aligned16(a->dbf) && aligned16(a->weight), "chain_head: dbf and weight must be 16-byte aligned");
+  NOISE_REQUIRE((int64_t)a->m * a->P < (1ll << 31), "chain_head: too many rows");
+  const hipStream_t st = (hipStream_t)stream;
+  const int rows = a->m * a->P;
+  chain_head_prep_kernel<<<(rows + 3) / 4, 256, 0, st>>>(a->delta, a->xL, a->base, a->ld_base, a->target_w, a->y,
+                                                         rows, a->P, a->W, a->V, a->dbf, a->inv, a->zy);
+  if (int e = noise::check_launch("chain_head")) return e;
+  chain_clean_kernel<<<(a->m + 3) / 4, 256, 0, st>>>(a->base, a->ld_base, a->xL, a->y, a->m, a->W, a->V, a->clean);
+  if (int e = noise::check_launch("chain_head")) return e;
+  ChainHead h{a->dbf, a->weight, a->base, a->ld_base, a->inv, a->zy, a->clean, a->scale, a->ld_scale,
+              a->y, a->m, a->P, a->W, a->V, a->out, a->ld_out};
+  chain_head_kernel<<<(rows + 255) / 256, HCfg::THREADS, 0, st>>>(h);
+  return noise::check_launch("chain_head");
+}

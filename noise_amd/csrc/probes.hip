@@ -21,32 +21,19 @@
 // the clean sums S0 coming from a first launch over the n clean rows. Workgroup ids run over the
 // direction tiles fastest, so with a multiple of 8 direction tiles each XCD's L2 holds one eighth
 // of C.
-#include <math.h>
-
-#include "common.h"
+#include "softcap.h"
 
 namespace {
 
-constexpr float K1 = 0.19235933878519514f;     // 2 log2(e) / 15
-constexpr float K2INV = -0.023104906018664842f; // 1 / (-30 log2(e))
-constexpr float EPS32 = 1.1920928955078125e-07f;
+using noise::cap;
+using noise::cap_difference;
+using noise::capexp;
+constexpr float K1 = noise::CAP_K1;
+constexpr float EPS32 = noise::CAP_EPS32;
 constexpr int CHUNK = 256;                      // vocabulary entries per wave per step
-
-// exp(cap(u * inv) - 15) with ik = inv * K1.
-NOISE_DEV float capexp(float u, float ik) {
-  const float e = __builtin_amdgcn_exp2f(u * ik);
-  return __builtin_amdgcn_exp2f(__builtin_amdgcn_rcpf(fmaf(e, K2INV, K2INV)));
-}
 
 NOISE_DEV float uniform(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
-}
-
-NOISE_DEV float cap(float z) { return 15.f * tanhf(z / 15.f); }
-
-// cap(z1) - cap(z0), accurate when z1 is close to z0: tanh(a) - tanh(b) = tanh(a - b)(1 - tanh a tanh b).
-NOISE_DEV float cap_difference(float z1, float z0) {
-  return 15.f * tanhf((z1 - z0) / 15.f) * (1.f - tanhf(z1 / 15.f) * tanhf(z0 / 15.f));
 }
 
 NOISE_DEV float block_sum256(float v, float* red) {
@@ -127,18 +114,8 @@ __global__ __launch_bounds__(256) void clean_sum_kernel(noise_probe_t a) {
   const int lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= a.n) return;
-  const float ik = rsqrtf(a.sq[i] / (float)a.width + EPS32) * K1;
-  const float* row = a.base + (int64_t)i * a.ld_base;
-  float acc = 0.f;
-  if constexpr (VEC) {
-    for (int v = lane * 4; v < a.V; v += 256) {
-      const float4 b = *reinterpret_cast<const float4*>(row + v);
-      acc += (capexp(b.x, ik) + capexp(b.y, ik)) + (capexp(b.z, ik) + capexp(b.w, ik));
-    }
-  } else {
-    for (int v = lane; v < a.V; v += 64) acc += capexp(row[v], ik);
-  }
-  acc = wave_sum(acc);
+  const float inv0 = rsqrtf(a.sq[i] / (float)a.width + EPS32);
+  const float acc = noise::row_capexp_sum<VEC>(a.base + (int64_t)i * a.ld_base, a.V, inv0, lane);
   if (lane == 0) a.clean_sum[i] = acc;
 }
 

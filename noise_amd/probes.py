@@ -6,6 +6,9 @@ float32 results (device tensors in, device tensors out, asynchronous on the curr
 * `coordinate_differences(raw, y, sigma)`  -- train/val/run.py:100-111 (speedrun/run.py:57-68)
 * `cycle_derivatives(base, C, y, steps, sq, dots, dir_sq)`       -- train/val/run.py:154-167
 * `row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq)`   -- train/val/run.py:170-183
+* `chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t,
+  weight_t, base, target_logit_w, y, own=None)`                   -- train/val/run.py:307-351,
+  with every attention held (own = None); the own-query variants are not built here
 
 The reference reads the stream width from a module constant (WIDTH = 512); here it is the keyword
 `width`. A target y < 0 masks its token (zeros, as the reference's `* (y >= 0)`); a target >= V
@@ -16,7 +19,7 @@ import ctypes as C
 import torch
 
 from . import _lib
-from ._lib import Probe
+from ._lib import ChainBlock, ChainHead, Probe
 
 WIDTH = 512
 
@@ -121,3 +124,81 @@ def cycle_derivatives(base, C, y, steps, sq, dots, dir_sq, width=WIDTH):
 def row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq, width=WIDTH):
     """rows [n, K] indices into C's rows; dots, dir_sq [n, K] -> float32 [n, K]."""
     return _probe(base, C, y, steps, sq, dots, dir_sq, width, rows=rows)
+
+
+def _dev_f32(t, shape, name):
+    _need(t.is_cuda, f'{name}: libnoise_amd kernels take device tensors')
+    _need(tuple(t.shape) == tuple(shape), f'{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}')
+    return t.float().contiguous()
+
+
+def _dev_bf16(t, shape, name):
+    _need(t.is_cuda, f'{name}: libnoise_amd kernels take device tensors')
+    _need(tuple(t.shape) == tuple(shape), f'{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}')
+    return t.to(torch.bfloat16).contiguous()
+
+
+def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t, base,
+                target_logit_w, y, own=None):
+    """Forward differences of each token's loss along every move of one site, attention held, MLPs
+    restricted to each token's routed units (train/val/run.py:307-351). site: -1 for the raw
+    embedding, else the block whose mid stream moves; move [m, P, W]; scale [m, P]; e, x0, xL
+    [m, W]; mids, idx, hs per block ([m, W], [m, k], [m, k]); w_fc, w_out_t per block [H, W];
+    weight_t [W, V]; base [m, V]; target_logit_w [m, W]; y [m]. Returns float32 [m, P]."""
+    if own is not None:
+        raise NotImplementedError('chain_chunk: only own=None (every attention held) runs on libnoise_amd')
+    m, P, W = move.shape
+    L = len(mids)
+    V = weight_t.shape[1]
+    H, k = w_fc[0].shape[0], idx[0].shape[1]
+    dev = move.device
+    _need(-1 <= site < L, f'site {site} outside [-1, {L})')
+    mv = _dev_f32(move, (m, P, W), 'move').view(m * P, W)
+    sc = _dev_f32(scale, (m, P), 'scale')
+    e, x0, xL = (_dev_f32(t, (m, W), n) for t, n in ((e, 'e'), (x0, 'x0'), (xL, 'xL')))
+    lr = [float(v) for v in torch.as_tensor(lam_r).reshape(-1).tolist()]
+    l0 = [float(v) for v in torch.as_tensor(lam_0).reshape(-1).tolist()]
+    _need(len(lr) >= L and len(l0) >= L, 'lam_r / lam_0: one value per block')
+    weight = _dev_bf16(weight_t, (W, V), 'weight_t').t().contiguous()
+    bs = _dev_f32(base, (m, V), 'base')
+    tw = _dev_f32(target_logit_w, (m, W), 'target_logit_w')
+    yy = _targets(y, m)
+    out = torch.empty(m, P, dtype=torch.float32, device=dev)
+    if m == 0:
+        return out
+    stream = _stream()
+    if site < 0:
+        dx0 = torch.empty(m * P, W, dtype=torch.float32, device=dev)
+        delta = torch.empty_like(dx0)
+        _lib.call('noise_chain_start', e.data_ptr(), x0.data_ptr(), mv.data_ptr(), m, P, W, lr[0] + l0[0],
+                  dx0.data_ptr(), delta.data_ptr(), stream)
+        first = 0
+    else:
+        dx0, delta, first = None, mv.clone(), site
+    dz = torch.empty(m * P, W, dtype=torch.bfloat16, device=dev)
+    wf = torch.empty(m, k, W, dtype=torch.bfloat16, device=dev)
+    wo = torch.empty(m, W, k, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(m * P, k, dtype=torch.bfloat16, device=dev)
+    for b in range(first, L):
+        mid = _dev_f32(mids[b], (m, W), f'mids[{b}]')
+        ib = idx[b].to(device=dev, dtype=torch.int64).contiguous()
+        hb = _dev_f32(hs[b], (m, k), f'hs[{b}]')
+        wfc = _dev_bf16(w_fc[b], (H, W), f'w_fc[{b}]')
+        wot = _dev_bf16(w_out_t[b], (H, W), f'w_out_t[{b}]')
+        _need(tuple(ib.shape) == (m, k), f'idx[{b}]: expected shape {(m, k)}, got {tuple(ib.shape)}')
+        a = ChainBlock(delta=delta.data_ptr(), dx0=dx0.data_ptr() if dx0 is not None else None,
+                       mix=int(b > first), lam_r=lr[b], lam_0=l0[b], mid=mid.data_ptr(), idx=ib.data_ptr(),
+                       ld_idx=k, hs=hb.data_ptr(), ld_hs=k, w_fc=wfc.data_ptr(), w_out_t=wot.data_ptr(),
+                       m=m, P=P, W=W, k=k, H=H, dz=dz.data_ptr(), wf=wf.data_ptr(), wo=wo.data_ptr(),
+                       g=g.data_ptr())
+        _lib.call('noise_chain_block', C.byref(a), stream)
+    dbf = torch.empty(m * P, W, dtype=torch.bfloat16, device=dev)
+    inv = torch.empty(m * P, dtype=torch.float32, device=dev)
+    zy = torch.empty_like(inv)
+    clean = torch.empty(2 * m, dtype=torch.float32, device=dev)
+    h = ChainHead(delta=delta.data_ptr(), xL=xL.data_ptr(), base=bs.data_ptr(), ld_base=V, weight=weight.data_ptr(),
+                  target_w=tw.data_ptr(), y=yy.data_ptr(), scale=sc.data_ptr(), ld_scale=P, m=m, P=P, W=W, V=V,
+                  out=out.data_ptr(), ld_out=P, dbf=dbf.data_ptr(), inv=inv.data_ptr(), zy=zy.data_ptr(),
+                  clean=clean.data_ptr())
+    _lib.call('noise_chain_head', C.byref(h), stream)
+    return out

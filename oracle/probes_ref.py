@@ -96,3 +96,70 @@ def row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq, width=512, dtype=
     z = (base[:, None, :] + s[..., None] * dirs) * inv[..., None]
     moved = _logsumexp(cap(z)) - cap((base_y[:, None] + s * dirs_y) * inv)
     return (moved - clean[:, None]) / s * (y >= 0)[:, None]
+
+
+# ---------------------------------------------------------------- chain_chunk (attention held)
+
+def _bf16(x):
+    """Round float64/32 numpy values to bfloat16 (round to nearest even), returned as float64."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).bfloat16().double().numpy()
+
+
+def _rms(x, width):
+    return x / np.sqrt(np.sum(x * x, -1, keepdims=True) / width + EPS32)
+
+
+def norm_difference(x, delta, width=512):
+    """norm(x + delta) - norm(x) in the closed form of train/val/run.py:246-253: x (m, W),
+    delta (m, P, W)."""
+    sq = np.sum(x * x, -1)[:, None]
+    dots = np.einsum('md,mpd->mp', x, delta)
+    inv0 = 1.0 / np.sqrt(sq / width + EPS32)
+    inv = 1.0 / np.sqrt((sq + 2 * dots + np.sum(delta * delta, -1)) / width + EPS32)
+    return delta * inv[..., None] + x[:, None, :] * (inv - inv0)[..., None]
+
+
+def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t,
+                base, target_logit_w, y, width=512, policy='fp64'):
+    """train/val/run.py:307-351 with own = None (every attention held): forward differences of each
+    token's loss along every move of one site, each later MLP restricted to the token's routed
+    units. policy 'fp64': float64 throughout; 'build': float64 with bfloat16 rounding where the
+    reference casts (dz, both routed products and their inputs, the head product and its input);
+    'build32': the same casts in float32 arithmetic, so |build - build32| shows how far the casts
+    alone let two correct evaluations drift (a product landing on the other side of a bf16
+    rounding boundary). Returns (m, P)."""
+    dt = np.float32 if policy == 'build32' else np.float64
+    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32') else (lambda v: v)
+    f = lambda v: np.asarray(v, dt)
+    move, scale, e, x0, xL, base, tw = map(f, (move, scale, e, x0, xL, base, target_logit_w))
+    lam_r, lam_0 = f(lam_r), f(lam_0)
+    y = np.asarray(y)
+    L = len(mids)
+    if site < 0:
+        dx0 = _rms(e[:, None, :] + move, width) - x0[:, None, :]
+        delta, first = (lam_r[0] + lam_0[0]) * dx0, 0
+    else:
+        dx0, delta, first = None, move, site
+    for b in range(first, L):
+        if b > first:
+            delta = lam_r[b] * delta + (lam_0[b] * dx0 if dx0 is not None else 0)
+        dz = rb(norm_difference(f(mids[b]), delta.astype(dt), width))
+        wf = f(w_fc[b])[np.asarray(idx[b])]                      # (m, k, W)
+        dh = rb(np.einsum('mpd,mkd->mpk', dz, wf))
+        h = f(hs[b])[:, None, :]
+        up, down = np.maximum(h + dh, 0), np.maximum(h, 0)
+        wo = f(w_out_t[b])[np.asarray(idx[b])]                   # (m, k, W)
+        delta = delta + rb(np.einsum('mpk,mkd->mpd', rb((up - down) * (up + down)), wo))
+    sq = np.sum(xL * xL, -1)[:, None]
+    dots = np.einsum('md,mpd->mp', xL, delta)
+    inv = 1.0 / np.sqrt((sq + 2 * dots + np.sum(delta * delta, -1)) / width + EPS32)
+    t = np.clip(y, 0, None)
+    moved_logits = rb(np.einsum('mpd,dv->mpv', rb(delta), f(weight_t)))
+    z = (base[:, None, :] + moved_logits) * inv[..., None]
+    base_y = base[np.arange(base.shape[0]), t]
+    zy = (base_y[:, None] + np.einsum('mpd,md->mp', delta, tw)) * inv
+    moved = _logsumexp(cap(z)) - cap(zy)
+    inv0 = 1.0 / np.sqrt(sq / width + EPS32)
+    clean = _logsumexp(cap(base * inv0)) - cap(base_y * inv0[:, 0])
+    return (moved - clean[:, None]) / scale * (y >= 0)[:, None]

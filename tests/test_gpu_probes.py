@@ -7,7 +7,7 @@ the exact value by up to ~4e-6 in (moved - clean) on these inputs (the oracle ev
 float32 shows it), i.e. ~4e-6 / step on a derivative. The kernels are held to
 |gpu - exact| <= 8e-6 / step + 1e-5 |exact| per element and a mean error below 1.5e-6 / step.
 coordinate_differences forms cap(raw +- sigma) - cap(raw) without cancellation and is held to
-2e-6 + 1e-4 |exact|.
+2e-6 + 1e-4 |exact|. chain_chunk carries the reference's bf16 casts: see its test.
 """
 import numpy as np
 import pytest
@@ -148,3 +148,66 @@ def test_coordinate_differences_reference_layout(device):
     assert got.shape == (b, t, V) and got.dtype == torch.float32
     want = P.coordinate_differences(padded[..., :V].double().reshape(-1, V).numpy(), y.reshape(-1).numpy(), 0.1)
     np.testing.assert_allclose(got.reshape(-1, V).cpu().double().numpy(), want, rtol=1e-4, atol=2e-6)
+
+
+def _chain_case(site, m, P_, L, seed=0, W=512, H=2048, k=128, V=4096):
+    """Chain inputs at the model's widths: bf16 block and head weights, routed units with their
+    clean pre-activations W_fc[idx] norm(mid), moves of the size the Cut estimator takes."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g)
+    nrm = lambda x: x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1.1920929e-07)
+    e = rn(m, W) * 2
+    x0 = nrm(e)
+    mids = [rn(m, W) * 3 for _ in range(L)]
+    w_fc = [(rn(H, W) * 3 ** 0.5 / W ** 0.5).bfloat16() for _ in range(L)]
+    w_out_t = [(rn(H, W) / H ** 0.5).bfloat16() for _ in range(L)]
+    idx = [torch.stack([torch.randperm(H, generator=g)[:k] for _ in range(m)]) for _ in range(L)]
+    hs = [torch.einsum('mkd,md->mk', w_fc[b].float()[idx[b]], nrm(mids[b])) for b in range(L)]
+    xL = rn(m, W) * 4
+    weight = rn(V, W) * 3 / W ** 0.5
+    y = torch.randint(0, V, (m,), generator=g)
+    steps = 0.01 * (e if site < 0 else mids[site]).square().mean(-1, keepdim=True).sqrt()
+    move = steps.unsqueeze(-1) * rn(m, P_, W)
+    scale = steps.expand(-1, P_).contiguous()
+    lam_r, lam_0 = 1 + 0.1 * rn(L), 0.1 + 0.05 * rn(L)
+    return dict(move=move, scale=scale, e=e, x0=x0, mids=mids, xL=xL, idx=idx, hs=hs, lam_r=lam_r, lam_0=lam_0,
+                w_fc=w_fc, w_out_t=w_out_t, weight_t=weight.T.bfloat16().contiguous(), base=xL @ weight.T,
+                target_logit_w=weight[y.clamp(min=0)], y=y)
+
+
+def _to(d, device):
+    return {k: ([v.to(device) for v in x] if isinstance(x, list) else x.to(device)) for k, x in d.items()}
+
+
+def _oracle_chain(site, d, rows, policy):
+    sub = {k: ([v[rows] for v in x] if k in ('mids', 'idx', 'hs') else
+               (x if k in ('lam_r', 'lam_0', 'w_fc', 'w_out_t', 'weight_t') else x[rows]))
+           for k, x in d.items()}
+    sub = {k: ([v.double().numpy() if v.is_floating_point() else v.numpy() for v in x] if isinstance(x, list)
+               else (x.double().numpy() if x.is_floating_point() else x.numpy())) for k, x in sub.items()}
+    return P.chain_chunk(site, **sub, policy=policy)
+
+
+@pytest.mark.parametrize('site,m,P_,L', [(-1, 6, 40, 3), (1, 5, 37, 3), (0, 3, 516, 2)])
+def test_chain_chunk_matches_oracle(device, site, m, P_, L):
+    """chain_chunk against the oracle with the reference's bf16 cast points. A derivative here is
+    (moved - clean) / step with bf16-rounded logit moves, so a product that lands on the other side
+    of a bf16 rounding boundary moves it by ~1e-3 relative: the oracle's own float32 evaluation
+    with the same casts (build32) drifts that far from its float64 one (build). The GPU is held to
+    twice that envelope, max and mean."""
+    d = _chain_case(site, m, P_, L, seed=m + P_)
+    d['y'][1] = -1
+    got = _probes().chain_chunk(site, **_to(d, device)).cpu().double().numpy()
+    torch.cuda.synchronize()
+    rows = np.arange(m)
+    want = _oracle_chain(site, d, rows, 'build')
+    env = np.abs(want - _oracle_chain(site, d, rows, 'build32'))
+    assert np.all(got[1] == 0)
+    ok = rows != 1
+    err = np.abs(got[ok] - want[ok])
+    scale = np.abs(want[ok]).max()
+    print(f'chain site {site}: max |gpu - build| {err.max():.3e} (envelope {env[ok].max():.3e}), '
+          f'mean {err.mean():.3e} (envelope {env[ok].mean():.3e}), max |want| {scale:.3e}')
+    assert np.isfinite(got).all()
+    assert err.max() <= 2 * env[ok].max() + 1e-4 * scale
+    assert err.mean() <= 2 * env[ok].mean() + 1e-5 * scale

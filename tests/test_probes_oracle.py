@@ -90,3 +90,69 @@ def test_cycle_derivatives_small_step_is_gradient():
     got = P.cycle_derivatives(d['base'], d['C'], d['y'], d['steps'], d['sq'], d['dots'], d['dir_sq'],
                               width=width)
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-6)
+
+
+def _chain_inputs(site, m=3, P_=5, W=32, H=64, k=8, V=48, L=3, seed=0):
+    """A tiny attention-held chain: clean streams, routed units and their clean pre-activations
+    (hs = W_fc[idx] norm(mid), as the reference captures them), head and moves."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, dtype=F64)
+    nrm = lambda x: x * torch.rsqrt(x.square().sum(-1, keepdim=True) / W + EPS)
+    e = rn(m, W) * 2
+    x0 = nrm(e)
+    mids = [rn(m, W) * 1.5 for _ in range(L)]
+    w_fc = [rn(H, W) / W ** 0.5 for _ in range(L)]
+    w_out_t = [rn(H, W) / H ** 0.5 for _ in range(L)]
+    idx = [torch.stack([torch.randperm(H, generator=g)[:k] for _ in range(m)]) for _ in range(L)]
+    hs = [torch.einsum('mkd,md->mk', w_fc[b][idx[b]], nrm(mids[b])) for b in range(L)]
+    xL = rn(m, W) * 2
+    weight = rn(V, W) * 3 / W ** 0.5
+    y = torch.randint(0, V, (m,), generator=g)
+    y[1] = -1
+    steps = 0.05 * (e if site < 0 else mids[site]).square().mean(-1).sqrt()
+    move = steps[:, None, None] * rn(m, P_, W)
+    scale = steps[:, None].expand(m, P_).clone()
+    lam_r, lam_0 = 1 + 0.1 * rn(L), 0.1 + 0.05 * rn(L)
+    return dict(move=move, scale=scale, e=e, x0=x0, mids=mids, xL=xL, idx=idx, hs=hs, lam_r=lam_r,
+                lam_0=lam_0, w_fc=w_fc, w_out_t=w_out_t, weight_t=weight.T.contiguous(),
+                base=xL @ weight.T, target_logit_w=weight[y.clamp(min=0)], y=y), nrm, weight
+
+
+@pytest.mark.parametrize('site', [-1, 0, 2])
+def test_chain_chunk_brute_force(site):
+    """chain_chunk (train/val/run.py:307-351, every attention held) against explicit moved streams:
+    norm(x + D) itself, the routed units' relu^2 at the moved pre-activations, the head's CE."""
+    d, nrm, weight = _chain_inputs(site)
+    m, P_, W = d['move'].shape
+    L = len(d['mids'])
+    ce = lambda x, yy: F.cross_entropy(15 * torch.tanh(nrm(x) @ weight.T / 15), yy.clamp(min=0), reduction='none')
+    want = torch.zeros(m, P_, dtype=F64)
+    for i in range(m):
+        if d['y'][i] < 0:
+            continue
+        clean = ce(d['xL'][i:i + 1], d['y'][i:i + 1])
+        for p in range(P_):
+            if site < 0:
+                dx0 = nrm(d['e'][i] + d['move'][i, p]) - d['x0'][i]
+                D, first = (d['lam_r'][0] + d['lam_0'][0]) * dx0, 0
+            else:
+                D, first = d['move'][i, p], site
+            for b in range(first, L):
+                if b > first:
+                    D = d['lam_r'][b] * D + (d['lam_0'][b] * dx0 if site < 0 else 0)
+                rows = d['idx'][b][i]
+                hp = d['w_fc'][b][rows] @ nrm(d['mids'][b][i] + D)
+                h = d['hs'][b][i]
+                D = D + (torch.relu(hp).square() - torch.relu(h).square()) @ d['w_out_t'][b][rows]
+            want[i, p] = (ce(d['xL'][i:i + 1] + D, d['y'][i:i + 1]) - clean)[0] / d['scale'][i, p]
+    got = P.chain_chunk(site, **{k: v for k, v in d.items()}, width=W)
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-11)
+    assert np.all(got[1] == 0)
+
+
+def test_norm_difference_is_difference_of_norms():
+    g = torch.Generator().manual_seed(4)
+    x, dl = torch.randn(4, 16, generator=g, dtype=F64), torch.randn(4, 3, 16, generator=g, dtype=F64) * 0.1
+    nrm = lambda v: v * torch.rsqrt(v.square().sum(-1, keepdim=True) / 16 + EPS)
+    np.testing.assert_allclose(P.norm_difference(x.numpy(), dl.numpy(), 16),
+                               (nrm(x[:, None] + dl) - nrm(x)[:, None]).numpy(), rtol=1e-12, atol=1e-14)
