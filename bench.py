@@ -4,6 +4,7 @@
     python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the MLP pair
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
     python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
+    python bench.py --probe-chain    # chain_chunk (attention held) at the Cut estimator's shape, own JSON line
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -167,6 +168,60 @@ def bench_probe_cycle(steps, warmup, no_cpu, n=2048, P=512, V=4096):
     print(json.dumps(line), flush=True)
 
 
+def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=4096):
+    """chain_chunk with every attention held (train/val/run.py:307-351) for one chunk of the Cut
+    estimator: 256 tokens x a full cycle of 512 moves of the raw embedding (site -1) through 8
+    blocks with 128 routed units each, then the head over V = 4096."""
+    from noise_amd import probes
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g)
+    nrm = lambda x: x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1.1920929e-07)
+    e = rn(m, W) * 2
+    mids = [rn(m, W) * 3 for _ in range(L)]
+    w_fc = [(rn(H, W) * 3 ** 0.5 / W ** 0.5).bfloat16() for _ in range(L)]
+    w_out_t = [(rn(H, W) / H ** 0.5).bfloat16() for _ in range(L)]
+    idx = [torch.argsort(rn(m, H), -1)[:, :k].contiguous() for _ in range(L)]
+    hs = [torch.einsum('mkd,md->mk', w_fc[b].float()[idx[b]], nrm(mids[b])) for b in range(L)]
+    xL = rn(m, W) * 4
+    weight = rn(V, W) * 3 / W ** 0.5
+    y = torch.randint(0, V, (m,), device=dev, generator=g)
+    steps_ = 0.01 * e.square().mean(-1, keepdim=True).sqrt()
+    args = dict(move=steps_.unsqueeze(-1) * rn(m, P, W), scale=steps_.expand(-1, P).contiguous(), e=e, x0=nrm(e),
+                mids=mids, xL=xL, idx=idx, hs=hs, lam_r=torch.ones(L), lam_0=torch.full((L,), 0.1), w_fc=w_fc,
+                w_out_t=w_out_t, weight_t=weight.T.bfloat16().contiguous(), base=xL @ weight.T,
+                target_logit_w=weight[y], y=y)
+    for _ in range(warmup):
+        probes.chain_chunk(-1, **args)
+    stream = torch.cuda.current_stream()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in events:
+        a.record(stream)
+        out = probes.chain_chunk(-1, **args)
+        b.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    call_ms = sum(a.elapsed_time(b) for a, b in events) / steps
+    flops = 2 * m * P * W * k * 2 * L + 2 * m * P * W * V
+    line = {
+        'metric': 'chain_chunk moves/sec on 1 GPU (token x move through 8 routed blocks and the soft-capped head)',
+        'value': m * P * steps / elapsed, 'unit': 'moves/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
+        'ms_per_step': elapsed / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'bf16', 'data': 'synthetic (random streams, bf16 block weights, Gaussian moves)',
+        'config': {'workload': 'chain_chunk site -1, attention held: 256 tokens x 512 moves, 8 blocks, k=128, V=4096',
+                   'tokens': m, 'moves': P, 'blocks': L, 'routed_units': k, 'vocab': V},
+        'roofline': {'bound': 'mfma', 'achieved': flops / (call_ms / 1e3) / 1e12, 'peak': PEAK_BF16 / 1e12,
+                     'unit': 'TFLOP/s', 'frac': flops / (call_ms / 1e3) / PEAK_BF16, 'traffic': None,
+                     'kernel': 'one chain_chunk call (start + 8 blocks + head)', 'flops_per_call': flops,
+                     'call_ms': call_ms},
+        'finite': bool(torch.isfinite(out).all()),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def cpu_baseline_probe(n, P, V, tokens=768):
     import numpy as np
     from noise_amd.synthetic import probe_inputs
@@ -217,6 +272,7 @@ def main():
     ap.add_argument('--probe-mlp', action='store_true', help='run the MLP counter-collection workload only')
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
     ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
+    ap.add_argument('--probe-chain', action='store_true', help='bench chain_chunk (own JSON line)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
@@ -231,6 +287,9 @@ def main():
         return
     if args.probe_cycle:
         bench_probe_cycle(max(args.steps, 5), args.warmup, args.no_cpu)
+        return
+    if args.probe_chain:
+        bench_probe_chain(max(args.steps, 5), args.warmup)
         return
 
     import noise_amd

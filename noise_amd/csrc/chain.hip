@@ -23,8 +23,13 @@ namespace {
 using noise::CAP_EPS32;
 using noise::CAP_K1;
 
-// One wave per row of W (a multiple of 64, at most 2048) floats: lane l holds entries l + 64 t.
-constexpr int MAXT = 32;
+// One wave per row of W (a multiple of 256, at most 2048) floats: lane l holds the float4s at
+// 4 l + 256 t, t < W / 256.
+constexpr int MAXT = 8;
+
+NOISE_DEV float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+NOISE_DEV void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+NOISE_DEV float dot4(float4 a, float4 b) { return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w); }
 
 __global__ __launch_bounds__(256) void chain_start_kernel(const float* __restrict__ e,
                                                           const float* __restrict__ x0,
@@ -35,22 +40,24 @@ __global__ __launch_bounds__(256) void chain_start_kernel(const float* __restric
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int64_t i = r / P;
-  const int nt = W / 64;
-  float u[MAXT];
+  const int nt = W / 256;
+  float4 u[MAXT];
   float sq = 0.f;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
-      u[t] = e[i * W + lane + 64 * t] + move[r * W + lane + 64 * t];
-      sq += u[t] * u[t];
+      const float4 a = ld4(e + i * W + 4 * lane + 256 * t), b = ld4(move + r * W + 4 * lane + 256 * t);
+      u[t] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+      sq += dot4(u[t], u[t]);
     }
   const float inv = rsqrtf(wave_sum(sq) / (float)W + CAP_EPS32);
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
-      const float d = u[t] * inv - x0[i * W + lane + 64 * t];
-      dx0[r * W + lane + 64 * t] = d;
-      delta[r * W + lane + 64 * t] = mix * d;
+      const float4 c = ld4(x0 + i * W + 4 * lane + 256 * t);
+      const float4 d = make_float4(u[t].x * inv - c.x, u[t].y * inv - c.y, u[t].z * inv - c.z, u[t].w * inv - c.w);
+      st4(dx0 + r * W + 4 * lane + 256 * t, d);
+      st4(delta + r * W + 4 * lane + 256 * t, make_float4(mix * d.x, mix * d.y, mix * d.z, mix * d.w));
     }
 }
 
@@ -65,23 +72,25 @@ __global__ __launch_bounds__(256) void chain_pre_kernel(float* __restrict__ delt
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int64_t i = r / P;
-  const int nt = W / 64;
-  float d[MAXT], x[MAXT];
+  const int nt = W / 256;
+  float4 d[MAXT], x[MAXT];
   float sq = 0.f, dot = 0.f, dsq = 0.f;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
-      const int64_t o = r * W + lane + 64 * t;
-      float v = delta[o];
+      const int64_t o = r * W + 4 * lane + 256 * t;
+      float4 v = ld4(delta + o);
       if (mix) {
-        v = lam_r * v + (dx0 ? lam_0 * dx0[o] : 0.f);
-        delta[o] = v;
+        const float4 z = dx0 ? ld4(dx0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v = make_float4(lam_r * v.x + lam_0 * z.x, lam_r * v.y + lam_0 * z.y, lam_r * v.z + lam_0 * z.z,
+                        lam_r * v.w + lam_0 * z.w);
+        st4(delta + o, v);
       }
       d[t] = v;
-      x[t] = mid[i * W + lane + 64 * t];
-      sq += x[t] * x[t];
-      dot += x[t] * v;
-      dsq += v * v;
+      x[t] = ld4(mid + i * W + 4 * lane + 256 * t);
+      sq += dot4(x[t], x[t]);
+      dot += dot4(x[t], v);
+      dsq += dot4(v, v);
     }
   sq = wave_sum(sq);
   dot = wave_sum(dot);
@@ -91,7 +100,12 @@ __global__ __launch_bounds__(256) void chain_pre_kernel(float* __restrict__ delt
   const float dinv = inv - inv0;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
-    if (t < nt) dz[r * W + lane + 64 * t] = f2bf(d[t] * inv + x[t] * dinv);
+    if (t < nt) {
+      const float4 a = d[t], b = x[t];
+      *reinterpret_cast<uint2*>(dz + r * W + 4 * lane + 256 * t) =
+          make_uint2(pack_bf2(a.x * inv + b.x * dinv, a.y * inv + b.y * dinv),
+                     pack_bf2(a.z * inv + b.z * dinv, a.w * inv + b.w * dinv));
+    }
 }
 
 // wf[i][kk][:] = w_fc[idx[i][kk]][:]  and  wo[i][n][kk] = w_out_t[idx[i][kk]][n], through LDS in
@@ -154,27 +168,53 @@ chain_gemm_kernel(const ChainGemm g) {
   noise::zero_acc(acc);
   noise::mma_tile<BN, NSTG, KDEPTH>(g.A + (i * g.P + p0) * g.K, g.K, g.P - p0,
                                     g.B + (i * g.N + n0) * g.K, g.K, g.K, smem, acc);
+  if constexpr (MODE == MODE_RELUDIFF) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
-      float h = 0.f;
-      if (MODE == MODE_RELUDIFF) h = g.hs[i * g.ld_hs + col];
+      for (int ni = 0; ni < 2; ++ni) {
+        const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+        const float h = g.hs[i * g.ld_hs + col];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int p = p0 + wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        if (p >= g.P) continue;
-        const float c = bf2f(f2bf(acc[mi][ni][j]));
-        const int64_t o = (i * g.P + p) * g.N + col;
-        if (MODE == MODE_RELUDIFF) {
+        for (int j = 0; j < 16; ++j) {
+          const int p = p0 + wm * 128 + mi * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          if (p >= g.P) continue;
+          const float c = bf2f(f2bf(acc[mi][ni][j]));
           const float up = fmaxf(h + c, 0.f), dn = fmaxf(h, 0.f);
-          g.G[o] = f2bf((up - dn) * (up + dn));
-        } else {
-          g.delta[o] += c;
+          g.G[(i * g.P + p) * g.N + col] = f2bf((up - dn) * (up + dn));
         }
       }
+  } else {
+    // Four rounds of 64 rows (32 per row half): each wave stages its 32 x 64 block of bf16-rounded
+    // products in LDS, then every thread adds float4s of the round's 64 x BN block into delta.
+    constexpr int SLD = 68;
+    float* stage = reinterpret_cast<float*>(smem);  // [waves][32][SLD]
+    constexpr int NT = 2 * BN;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          stage[(wave * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] =
+              bf2f(f2bf(acc[mi][ni][j]));
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < (64 * BN / 4) / NT; ++q) {
+        const int id = q * NT + threadIdx.x, rr = id / (BN / 4), c4 = (id % (BN / 4)) * 4;
+        const int h = rr >> 5, r = rr & 31;  // row half (wm) and row within the round
+        const int p = p0 + h * 128 + mi * 32 + r;
+        if (p < g.P) {
+          const float4 v = ld4(stage + ((h * WN + (c4 >> 6)) * 32 + r) * SLD + (c4 & 63));
+          float* o = g.delta + (i * g.P + p) * g.N + n0 + c4;
+          float4 d = ld4(o);
+          d.x += v.x; d.y += v.y; d.z += v.z; d.w += v.w;
+          st4(o, d);
+        }
+      }
+      if (mi < 3) __syncthreads();
     }
+  }
 }
 
 // ---------------------------------------------------------------- head
@@ -193,17 +233,17 @@ __global__ __launch_bounds__(256) void chain_head_prep_kernel(const float* __res
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int64_t i = r / P;
-  const int nt = W / 64;
+  const int nt = W / 256;
   float sq = 0.f, dot = 0.f, dsq = 0.f, ty = 0.f;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
-      const float d = delta[r * W + lane + 64 * t], x = xL[i * W + lane + 64 * t];
-      sq += x * x;
-      dot += x * d;
-      dsq += d * d;
-      ty += d * tw[i * W + lane + 64 * t];
-      dbf[r * W + lane + 64 * t] = f2bf(d);
+      const float4 d = ld4(delta + r * W + 4 * lane + 256 * t), x = ld4(xL + i * W + 4 * lane + 256 * t);
+      sq += dot4(x, x);
+      dot += dot4(x, d);
+      dsq += dot4(d, d);
+      ty += dot4(d, ld4(tw + i * W + 4 * lane + 256 * t));
+      *reinterpret_cast<uint2*>(dbf + r * W + 4 * lane + 256 * t) = make_uint2(pack_bf2(d.x, d.y), pack_bf2(d.z, d.w));
     }
   sq = wave_sum(sq);
   dot = wave_sum(dot);
@@ -330,8 +370,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 extern "C" int noise_chain_start(const float* e, const float* x0, const float* move, int m, int P, int W,
                                  float mix, float* dx0, float* delta, void* stream) {
-  NOISE_REQUIRE(m >= 0 && P > 0 && W > 0 && W % 64 == 0 && W <= 64 * MAXT,
-                "chain_start: bad sizes (m=%d P=%d W=%d; W a multiple of 64 up to 2048)", m, P, W);
+  NOISE_REQUIRE(m >= 0 && P > 0 && W > 0 && W % 256 == 0 && W <= 256 * MAXT,
+                "chain_start: bad sizes (m=%d P=%d W=%d; W a multiple of 256 up to 2048)", m, P, W);
   if (m == 0) return NOISE_OK;
   NOISE_REQUIRE(e && x0 && move && dx0 && delta, "chain_start: NULL argument");
   const int rows = m * P;
@@ -341,7 +381,7 @@ extern "C" int noise_chain_start(const float* e, const float* x0, const float* m
 
 extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
   NOISE_REQUIRE(a, "chain_block: args is NULL");
-  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 64 * MAXT && a->k > 0 &&
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 256 * MAXT && a->k > 0 &&
                     a->k % 128 == 0 && a->H > 0,
                 "chain_block: bad sizes (m=%d P=%d W=%d k=%d H=%d; W a multiple of 256 up to 2048, k of 128)",
                 a->m, a->P, a->W, a->k, a->H);
@@ -371,9 +411,10 @@ extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
 
 extern "C" int noise_chain_head(const noise_chain_head_t* a, void* stream) {
   NOISE_REQUIRE(a, "chain_head: args is NULL");
-  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 64 == 0 && a->W <= 64 * MAXT && a->V > 0 &&
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 256 * MAXT && a->V > 0 &&
                     a->V % 256 == 0,
-                "chain_head: bad sizes (m=%d P=%d W=%d V=%d; V a multiple of 256)", a->m, a->P, a->W, a->V);
+                "chain_head: bad sizes (m=%d P=%d W=%d V=%d; W a multiple of 256 up to 2048, V of 256)", a->m,
+                a->P, a->W, a->V);
   if (a->m == 0) return NOISE_OK;
   NOISE_REQUIRE(a->delta && a->xL && a->base && a->weight && a->target_w && a->y && a->scale && a->out &&
                     a->dbf && a->inv && a->zy && a->clean,
