@@ -193,38 +193,39 @@ NOISE_DEV void zero_acc(floatx16 (&acc)[4][2]) {
       for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
 }
 
+// Row-local DPP read: lane i gets v from lane i + s (row_shl:s, CTRL 0x100 + s) or i - s (row_shr:s,
+// CTRL 0x110 + s) of its 16-lane row; lanes whose source leaves the row get 0 (never used below).
+template <int CTRL>
+NOISE_DEV float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 // Sum over the 32 lanes of each half-wave of 16 per-lane values; lane q of a half ends with the
-// total of value (q >> 1) & 15 (lanes q and q ^ 1 hold the same total).
+// total of value (q >> 1) & 15 (lanes q and q ^ 1 hold the same total). Each halving step pairs
+// two values: v_permlane16_swap exchanges them across the two 16-lane rows of the half, DPP row
+// shifts fetch the partner inside a row; no LDS round trips.
 NOISE_DEV float halfwave_transpose_sum16(float (&v)[16], int lane) {
   const int q = lane & 31;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bool up = q & 16;
-    const float send = up ? v[i] : v[i + 8];
-    const float keep = up ? v[i + 8] : v[i];
-    v[i] = keep + __shfl_xor(send, 16, 64);
+  for (int i = 0; i < 8; ++i) {  // rows 0 | 1: row 0 keeps value i, row 1 value i + 8
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool up = q & 8;
-    const float send = up ? v[i] : v[i + 4];
-    const float keep = up ? v[i + 4] : v[i];
-    v[i] = keep + __shfl_xor(send, 8, 64);
+    const float x = v[i] + dpp_row<0x108>(v[i]), y = v[i + 4] + dpp_row<0x118>(v[i + 4]);
+    v[i] = (q & 8) ? y : x;
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const bool up = q & 4;
-    const float send = up ? v[i] : v[i + 2];
-    const float keep = up ? v[i + 2] : v[i];
-    v[i] = keep + __shfl_xor(send, 4, 64);
+    const float x = v[i] + dpp_row<0x104>(v[i]), y = v[i + 2] + dpp_row<0x114>(v[i + 2]);
+    v[i] = (q & 4) ? y : x;
   }
   {
-    const bool up = q & 2;
-    const float send = up ? v[0] : v[1];
-    const float keep = up ? v[1] : v[0];
-    v[0] = keep + __shfl_xor(send, 2, 64);
+    const float x = v[0] + dpp_row<0x102>(v[0]), y = v[1] + dpp_row<0x112>(v[1]);
+    v[0] = (q & 2) ? y : x;
   }
-  return v[0] + __shfl_xor(v[0], 1, 64);
+  return v[0] + dpp_row<0xB1>(v[0]);  // quad_perm [1, 0, 3, 2]: the lane's neighbour q ^ 1
 }
 
 }  // namespace noise
