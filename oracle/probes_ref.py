@@ -120,11 +120,46 @@ def norm_difference(x, delta, width=512):
     return delta * inv[..., None] + x[:, None, :] * (inv - inv0)[..., None]
 
 
+def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos, sin, width=512,
+                        policy='fp64'):
+    """train/val/run.py:282-304: the change of each token's attention output, through the output
+    projection, when only its own query moves and only the logits of its top keys per head move.
+    x (m, W) block input; delta (m, P, W); top_keys, top_values (m, h, K, d); top_p (m, h, K);
+    rest (m, h, d); w_q (W, W); w_proj_t (W, W) = c_proj.weight^T; cos, sin (T, d / 2).
+    'build' rounds where the reference casts to bf16 (dq, both einsum products, the weights)."""
+    dt = np.float32 if policy == 'build32' else np.float64
+    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32') else (lambda v: v)
+    f = lambda v: np.asarray(v, dt)
+    x, delta, w_q, keys, vals, tp, rest, w_proj_t = map(f, (x, delta, w_q, top_keys, top_values, top_p, rest,
+                                                           w_proj_t))
+    cos, sin = f(cos), f(sin)
+    pos = np.asarray(pos)
+    m, P, _ = delta.shape
+    _, heads, K, d = keys.shape
+    c, s_ = cos[pos][:, None, None, :], sin[pos][:, None, None, :]
+    rot = lambda u: np.concatenate([u[..., :d // 2] * c + u[..., d // 2:] * s_,
+                                    u[..., :d // 2] * -s_ + u[..., d // 2:] * c], -1)
+    r0 = rot((_rms(x, width) @ w_q.T).reshape(m, 1, heads, d))
+    dr = rot((norm_difference(x, delta, width) @ w_q.T).reshape(m, P, heads, d))
+    sq = np.sum(r0 * r0, -1, keepdims=True)
+    inv0 = 1.0 / np.sqrt(sq / d + EPS32)
+    inv = 1.0 / np.sqrt((sq + 2 * np.sum(r0 * dr, -1, keepdims=True) + np.sum(dr * dr, -1, keepdims=True)) / d + EPS32)
+    dq = dr * inv + r0 * (inv - inv0)
+    ds = rb(np.einsum('mphd,mhkd->mphk', rb(dq), keys)) * d ** -0.5
+    p = tp[:, None]
+    dlse = np.log1p(np.sum(p * np.expm1(ds), -1, keepdims=True))
+    dout = rb(np.einsum('mphk,mhkd->mphd', rb(p * np.expm1(ds - dlse)), vals))
+    dout = dout + np.expm1(-dlse) * rest[:, None]
+    return dout.reshape(m, P, heads * d) @ w_proj_t
+
+
 def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t,
-                base, target_logit_w, y, width=512, policy='fp64'):
-    """train/val/run.py:307-351 with own = None (every attention held): forward differences of each
-    token's loss along every move of one site, each later MLP restricted to the token's routed
-    units. policy 'fp64': float64 throughout; 'build': float64 with bfloat16 rounding where the
+                base, target_logit_w, y, own=None, width=512, policy='fp64'):
+    """train/val/run.py:307-351 with own = None (every attention held) or own = ('routed', pos,
+    inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, (cos, sin)) (each move also changes
+    its own token's attention through its own query, along its top keys; per-block lists as in
+    the reference): forward differences of each token's loss along every move of one site, each
+    later MLP restricted to the token's routed units. policy 'fp64': float64 throughout; 'build': float64 with bfloat16 rounding where the
     reference casts (dz, both routed products and their inputs, the head product and its input);
     'build32': the same casts in float32 arithmetic, so |build - build32| shows how far the casts
     alone let two correct evaluations drift (a product landing on the other side of a bf16
@@ -144,6 +179,11 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     for b in range(first, L):
         if b > first:
             delta = lam_r[b] * delta + (lam_0[b] * dx0 if dx0 is not None else 0)
+        if own is not None and (site < 0 or b > first):
+            assert own[0] == 'routed', 'only the routed own-query variant is restated'
+            _, pos, inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos_sin = own
+            delta = delta + query_change_routed(inputs[b], delta, pos, w_q[b], top_keys[b], top_values[b], top_p[b],
+                                                rest[b], w_proj_t[b], cos_sin[0], cos_sin[1], width, policy)
         dz = rb(norm_difference(f(mids[b]), delta.astype(dt), width))
         wf = f(w_fc[b])[np.asarray(idx[b])]                      # (m, k, W)
         dh = rb(np.einsum('mpd,mkd->mpk', dz, wf))

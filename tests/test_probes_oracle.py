@@ -156,3 +156,104 @@ def test_norm_difference_is_difference_of_norms():
     nrm = lambda v: v * torch.rsqrt(v.square().sum(-1, keepdim=True) / 16 + EPS)
     np.testing.assert_allclose(P.norm_difference(x.numpy(), dl.numpy(), 16),
                                (nrm(x[:, None] + dl) - nrm(x)[:, None]).numpy(), rtol=1e-12, atol=1e-14)
+
+
+def _qc_case(m=3, P_=4, W=16, heads=2, S=6, K=3, T=10, seed=0, rotary=None):
+    """Own-query inputs with explicit full key sets: clean queries from the block input, the clean
+    softmax over S keys per head, the top K keys by clean probability and the held keys' share.
+    rotary: (pos, cos, sin) shared by several blocks, else drawn here."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, dtype=F64)
+    d = W // heads
+    nrm = lambda v, n: v * torch.rsqrt(v.square().sum(-1, keepdim=True) / n + EPS)
+    x, w_q, w_proj_t = rn(m, W) * 2, rn(W, W) / W ** 0.5, rn(W, W) / W ** 0.5
+    if rotary is None:
+        pos = torch.randint(0, T, (m,), generator=g)
+        ang = rn(T, d // 2)
+        cos, sin = ang.cos(), ang.sin()
+    else:
+        pos, cos, sin = rotary
+    keys, vals = nrm(rn(m, heads, S, d), d), rn(m, heads, S, d)
+
+    def query(xx):  # q for stream(s) xx (..., W) of token i: norm, W_q, rotary, per-head RMS norm
+        r = (nrm(xx, W) @ w_q.T).view(*xx.shape[:-1], heads, d)
+        return r, lambda i: nrm(torch.cat([r[..., :d // 2] * cos[pos[i]] + r[..., d // 2:] * sin[pos[i]],
+                                           r[..., :d // 2] * -sin[pos[i]] + r[..., d // 2:] * cos[pos[i]]], -1), d)
+    probs = []
+    for i in range(m):
+        q0 = query(x[i])[1](i)                                     # (h, d)
+        probs.append(torch.softmax(torch.einsum('hd,hsd->hs', q0, keys[i]) * d ** -0.5, -1))
+    probs = torch.stack(probs)                                      # (m, h, S)
+    top = probs.topk(K, -1).indices
+    take = lambda z: torch.gather(z, 2, top[..., None].expand(-1, -1, -1, d))
+    held = torch.ones_like(probs, dtype=torch.bool).scatter(2, top, False)
+    rest = torch.einsum('mhs,mhsd->mhd', probs * held, vals)
+    case = dict(pos=pos, w_q=w_q, top_keys=take(keys), top_values=take(vals), top_p=probs.gather(2, top), rest=rest,
+                w_proj_t=w_proj_t, cos=cos, sin=sin)
+
+    def brute(i, D):
+        """Attention output change of token i, its stream moved by D, through c_proj: the top keys'
+        logits recomputed with the moved query, every other logit held."""
+        q0, q1 = query(x[i])[1](i), query(x[i] + D)[1](i)
+        s0 = torch.einsum('hd,hsd->hs', q0, keys[i]) * d ** -0.5
+        s1 = torch.where(held[i], s0, torch.einsum('hd,hsd->hs', q1, keys[i]) * d ** -0.5)
+        out = lambda s: torch.einsum('hs,hsd->hd', torch.softmax(s, -1), vals[i])
+        return (out(s1) - out(s0)).reshape(-1) @ w_proj_t
+    return x, case, brute
+
+
+def test_query_change_routed_brute_force():
+    """query_change_routed (train/val/run.py:282-304) against the moved query's full softmax with the
+    held keys' logits fixed: pins the qk-norm difference, dlse = log1p(sum p expm1(ds)) and the
+    expm1(-dlse) rescaling of the held share."""
+    m, P_, W = 3, 4, 16
+    x, c, brute = _qc_case(m, P_, W)
+    g = torch.Generator().manual_seed(1)
+    delta = torch.randn(m, P_, W, generator=g, dtype=F64) * 0.3
+    got = P.query_change_routed(x, delta, width=W, **c)
+    want = torch.stack([torch.stack([brute(i, delta[i, p]) for p in range(P_)]) for i in range(m)])
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize('site', [-1, 1])
+def test_chain_chunk_routed_brute_force(site):
+    """chain_chunk with own = ('routed', ...) (train/val/run.py:326-331): at every block the move
+    enters, its own token's attention output changes through its own query along its top keys
+    (the explicit held-logit softmax of the test above) before that block's MLP."""
+    d, nrm, weight = _chain_inputs(site)
+    m, P_, W = d['move'].shape
+    L = len(d['mids'])
+    g = torch.Generator().manual_seed(7)
+    T, dh = 10, W // 2
+    ang = torch.randn(T, dh // 2, generator=g, dtype=F64)
+    rotary = (torch.randint(0, T, (m,), generator=g), ang.cos(), ang.sin())
+    blocks = [_qc_case(m, P_, W, heads=2, S=7, K=4, seed=20 + b, rotary=rotary) for b in range(L)]
+    own = ('routed', rotary[0], [bl[0] for bl in blocks]) + tuple(
+        [bl[1][k] for bl in blocks] for k in ('w_q', 'top_keys', 'top_values', 'top_p', 'rest', 'w_proj_t')) + (
+        (rotary[1], rotary[2]),)
+    ce = lambda x, yy: F.cross_entropy(15 * torch.tanh(nrm(x) @ weight.T / 15), yy.clamp(min=0), reduction='none')
+    want = torch.zeros(m, P_, dtype=F64)
+    for i in range(m):
+        if d['y'][i] < 0:
+            continue
+        clean = ce(d['xL'][i:i + 1], d['y'][i:i + 1])
+        for p in range(P_):
+            if site < 0:
+                dx0 = nrm(d['e'][i] + d['move'][i, p]) - d['x0'][i]
+                D, first = (d['lam_r'][0] + d['lam_0'][0]) * dx0, 0
+            else:
+                D, first = d['move'][i, p], site
+            for b in range(first, L):
+                if b > first:
+                    D = d['lam_r'][b] * D + (d['lam_0'][b] * dx0 if site < 0 else 0)
+                if site < 0 or b > first:
+                    D = D + blocks[b][2](i, D)
+                rows = d['idx'][b][i]
+                hp = d['w_fc'][b][rows] @ nrm(d['mids'][b][i] + D)
+                h = d['hs'][b][i]
+                D = D + (torch.relu(hp).square() - torch.relu(h).square()) @ d['w_out_t'][b][rows]
+            want[i, p] = (ce(d['xL'][i:i + 1] + D, d['y'][i:i + 1]) - clean)[0] / d['scale'][i, p]
+    got = P.chain_chunk(site, **d, own=own, width=W)
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-11)
+    none = P.chain_chunk(site, **d, width=W)
+    assert np.abs(got - none)[[0, 2]].max() > 1e-3 * np.abs(none).max()   # the own-query term is live
