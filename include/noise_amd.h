@@ -277,6 +277,34 @@ typedef struct {
 int noise_chain_block(const noise_chain_block_t* args, void* stream);
 
 typedef struct {
+  float* delta;            /* [m * P, W] moves at the block's input, updated in place */
+  const float* dx0;        /* NULL, or [m * P, W] moves of x0 (site < 0) */
+  int mix;                 /* first delta = lam_r delta + lam_0 dx0 (then call noise_chain_block with mix 0) */
+  float lam_r, lam_0;
+  const float* x;          /* [m, W] the block's clean input stream */
+  const int64_t* pos;      /* [m] positions, in [0, T) (else NaN) */
+  const float* w_q;        /* [W, W] fp32 c_q.weight */
+  const uint16_t* top_keys;   /* [m, heads, K, 64] bf16 rotated, normed keys */
+  const uint16_t* top_values; /* [m, heads, K, 64] bf16 values */
+  const float* top_p;      /* [m, heads, K] their clean probabilities */
+  const float* rest;       /* [m, heads, 64] the held keys' share of the clean output */
+  const float* w_proj_t;   /* [W, W] fp32 c_proj.weight transposed */
+  const float* cos_t;      /* [T, 32] rotary tables */
+  const float* sin_t;
+  int T, m, P, W, heads, K; /* W = 64 heads, W % 256 == 0, W <= 2048, 1 <= K <= 64 */
+  uint16_t* a3;            /* workspace [m * P + m, 3 W] bf16 (16-byte aligned, as the next three) */
+  float* dr;               /* workspace [m * P + m, W] fp32 */
+  uint16_t* wq3;           /* workspace [W, 3 W] bf16 */
+  uint16_t* wp3;           /* workspace [W, 3 W] bf16 */
+} noise_chain_query_t;
+
+/* The own-query step of a block (run.py:284-304 and 326-331, own = ('routed', ...)): the optional
+ * mix, then delta += (change of the token's attention output when its query moves with its
+ * input stream and only its top keys' logits move) c_proj^T. Replaces query_change_routed; the
+ * two fp32 products run as three bf16 MFMA products each (hi/lo halves). */
+int noise_chain_query(const noise_chain_query_t* args, void* stream);
+
+typedef struct {
   const float* delta;      /* [m * P, W] */
   const float* xL;         /* [m, W] clean top stream */
   const float* base;       /* [m, ld_base] xL W^T */

@@ -64,6 +64,13 @@ class ChainBlock(C.Structure):
                 ('dz', P), ('wf', P), ('wo', P), ('g', P)]
 
 
+class ChainQuery(C.Structure):
+    _fields_ = [('delta', P), ('dx0', P), ('mix', INT), ('lam_r', F32), ('lam_0', F32), ('x', P), ('pos', P),
+                ('w_q', P), ('top_keys', P), ('top_values', P), ('top_p', P), ('rest', P), ('w_proj_t', P),
+                ('cos_t', P), ('sin_t', P), ('T', INT), ('m', INT), ('P', INT), ('W', INT), ('heads', INT),
+                ('K', INT), ('a3', P), ('dr', P), ('wq3', P), ('wp3', P)]
+
+
 class ChainHead(C.Structure):
     _fields_ = [('delta', P), ('xL', P), ('base', P), ('ld_base', I64), ('weight', P), ('target_w', P),
                 ('y', P), ('scale', P), ('ld_scale', I64), ('m', INT), ('P', INT), ('W', INT), ('V', INT),
@@ -91,6 +98,7 @@ SIGNATURES = {
     'noise_chain_start': [P, P, P, INT, INT, INT, F32, P, P, P],
     'noise_chain_block': [C.POINTER(ChainBlock), P],
     'noise_chain_head': [C.POINTER(ChainHead), P],
+    'noise_chain_query': [C.POINTER(ChainQuery), P],
 }
 
 _lib = None

@@ -141,7 +141,9 @@ __global__ __launch_bounds__(256) void chain_gather_kernel(const uint16_t* __res
 
 // ---------------------------------------------------------------- routed MLP products
 
-constexpr int MODE_RELUDIFF = 0, MODE_ADDROUND = 1;
+// RELUDIFF: G = the relu-square difference of bf16(acc); ADDROUND: delta += bf16(acc); ADD and
+// STORE (the own-query step's fp32 products): delta += acc, delta = acc.
+constexpr int MODE_RELUDIFF = 0, MODE_ADDROUND = 1, MODE_ADD = 2, MODE_STORE = 3;
 
 struct ChainGemm {
   const uint16_t* A;   // [m * P, K] rows of the batch at i * P
@@ -150,7 +152,7 @@ struct ChainGemm {
   const float* hs;     // MODE_RELUDIFF: [m, ld_hs] clean pre-activations
   int64_t ld_hs;
   uint16_t* G;         // MODE_RELUDIFF out [m * P, N] bf16
-  float* delta;        // MODE_ADDROUND in/out [m * P, N] fp32
+  float* delta;        // MODE_ADDROUND, MODE_ADD in/out, MODE_STORE out [m * P, N] fp32
 };
 
 template <int MODE, int BN>
@@ -197,7 +199,7 @@ chain_gemm_kernel(const ChainGemm g) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
           stage[(wave * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)) * SLD + ni * 32 + (lane & 31)] =
-              bf2f(f2bf(acc[mi][ni][j]));
+              MODE == MODE_ADDROUND ? bf2f(f2bf(acc[mi][ni][j])) : acc[mi][ni][j];
       __syncthreads();
 #pragma unroll
       for (int q = 0; q < (64 * BN / 4) / NT; ++q) {
@@ -207,13 +209,273 @@ chain_gemm_kernel(const ChainGemm g) {
         if (p < g.P) {
           const float4 v = ld4(stage + ((h * WN + (c4 >> 6)) * 32 + r) * SLD + (c4 & 63));
           float* o = g.delta + (i * g.P + p) * g.N + n0 + c4;
-          float4 d = ld4(o);
-          d.x += v.x; d.y += v.y; d.z += v.z; d.w += v.w;
-          st4(o, d);
+          if constexpr (MODE == MODE_STORE) {
+            st4(o, v);
+          } else {
+            float4 d = ld4(o);
+            d.x += v.x; d.y += v.y; d.z += v.z; d.w += v.w;
+            st4(o, d);
+          }
         }
       }
       if (mi < 3) __syncthreads();
     }
+  }
+}
+
+// ---------------------------------------------------------------- own-query step
+
+// fp32 operands of the own-query products enter the bf16 MFMA as hi + lo halves: with
+// A3 = [a_hi | a_lo | a_hi] and B3 = [b_hi | b_hi | b_lo] along K, A3 B3^T = a_hi b_hi + a_lo b_hi +
+// a_hi b_lo, which leaves out only a_lo b_lo (relative 2^-16 per product).
+NOISE_DEV void split3(uint16_t* o, int64_t W, int64_t c, float v, bool a_side) {
+  const uint16_t hi = f2bf(v), lo = f2bf(v - bf2f(hi));
+  o[c] = hi;
+  o[W + c] = a_side ? lo : hi;
+  o[2 * W + c] = a_side ? hi : lo;
+}
+
+// B3 rows of an fp32 weight read as B[n][k] = w[n * s_n + k * s_k] (N = K = W).
+__global__ __launch_bounds__(256) void chain_split_weight_kernel(const float* __restrict__ w, int64_t s_n,
+                                                                 int64_t s_k, int W, uint16_t* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)W * W) return;
+  const int64_t n = e / W, k = e % W;
+  split3(out + n * 3 * W, W, k, w[n * s_n + k * s_k], false);
+}
+
+// Rows r < m P: the optional mix of delta, then A3 of norm_difference(x_i, delta_r) (the query
+// product's input, train/val/run.py:294); rows m P + i: A3 of norm(x_i) (the clean query's).
+__global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict__ delta,
+                                                              const float* __restrict__ dx0,
+                                                              const float* __restrict__ x, int m, int P, int W,
+                                                              int mix, float lam_r, float lam_0,
+                                                              uint16_t* __restrict__ a3) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t rows = (int64_t)m * P;
+  if (r >= rows + m) return;
+  const bool clean = r >= rows;
+  const int64_t i = clean ? r - rows : r / P;
+  const int nt = W / 256;
+  float4 d[MAXT], xv[MAXT];
+  float sq = 0.f, dot = 0.f, dsq = 0.f;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      const int64_t o = r * W + 4 * lane + 256 * t;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!clean) {
+        v = ld4(delta + o);
+        if (mix) {
+          const float4 z = dx0 ? ld4(dx0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+          v = make_float4(lam_r * v.x + lam_0 * z.x, lam_r * v.y + lam_0 * z.y, lam_r * v.z + lam_0 * z.z,
+                          lam_r * v.w + lam_0 * z.w);
+          st4(delta + o, v);
+        }
+      }
+      d[t] = v;
+      xv[t] = ld4(x + i * W + 4 * lane + 256 * t);
+      sq += dot4(xv[t], xv[t]);
+      dot += dot4(xv[t], v);
+      dsq += dot4(v, v);
+    }
+  sq = wave_sum(sq);
+  dot = wave_sum(dot);
+  dsq = wave_sum(dsq);
+  const float inv0 = rsqrtf(sq / (float)W + CAP_EPS32);
+  const float inv = rsqrtf((sq + 2.f * dot + dsq) / (float)W + CAP_EPS32);
+  // clean rows: norm(x) = x inv0; moves: delta inv + x (inv - inv0)
+  const float a = clean ? 0.f : inv, b = clean ? inv0 : inv - inv0;
+  uint16_t* o = a3 + r * 3 * W;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+    if (t < nt) {
+      const int c = 4 * lane + 256 * t;
+      split3(o, W, c + 0, d[t].x * a + xv[t].x * b, true);
+      split3(o, W, c + 1, d[t].y * a + xv[t].y * b, true);
+      split3(o, W, c + 2, d[t].z * a + xv[t].z * b, true);
+      split3(o, W, c + 3, d[t].w * a + xv[t].w * b, true);
+    }
+}
+
+struct ChainQuery {
+  const float* dr;       // [m P + m, W] query products: moves' changes, then the clean rows
+  const int64_t* pos;    // [m]
+  const float* cos_t;    // [T, 32]
+  const float* sin_t;
+  const uint16_t* keys;  // [m, heads, K, 64]
+  const uint16_t* vals;  // [m, heads, K, 64]
+  const float* top_p;    // [m, heads, K]
+  const float* rest;     // [m, heads, 64]
+  int T, m, P, W, heads, K;
+  uint16_t* a3;          // out [m P, 3 W]: A3 of the attention output changes
+};
+
+constexpr int QLD = 72;  // LDS row of a 64-wide bf16 tile, padded by 16 bytes (conflict-free reads)
+
+// Workgroup (row tile, head h, token i), four waves of 32 moves each (train/val/run.py:290-303):
+//   dr, r0 rotated; inv0, inv from |r0|^2, r0.dr, |dr|^2; dq = bf16(dr inv + r0 (inv - inv0))
+//   ds = bf16(dq K^T) / 8                         (32 x 64 MFMA per wave, keys zero-padded to 64)
+//   dlse = log1p(sum_k p_k expm1(ds_k)), w = bf16(p expm1(ds - dlse))
+//   dout = bf16(w V) + expm1(-dlse) rest          (32 x 64 MFMA per wave)
+// written as A3 of the output projection's product. A position outside [0, T) gives NaN.
+__global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery g) {
+  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];     // keys [key][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * QLD];     // values transposed [dim][key]
+  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq, then w
+  __shared__ float r0s[64], ps[64], rs[64], cs[32], sn[32], dls[4][32], inv0s;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = blockIdx.z, h = blockIdx.y;
+  const int pw = blockIdx.x * 128 + wave * 32;  // first move of this wave
+  const int64_t pos = g.pos[i];
+  const bool pos_ok = pos >= 0 && pos < g.T;
+  const int64_t pc = pos_ok ? pos : 0;
+  const int64_t ih = (int64_t)i * g.heads + h;
+  const int64_t kv0 = ih * g.K * 64;
+  for (int e = tid; e < 64 * 8; e += 256) {
+    const int k = e >> 3, c = (e & 7) * 8;
+    uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = kv;
+    if (k < g.K) {
+      kv = *reinterpret_cast<const uint4*>(g.keys + kv0 + k * 64 + c);
+      vv = *reinterpret_cast<const uint4*>(g.vals + kv0 + k * 64 + c);
+    }
+    *reinterpret_cast<uint4*>(kt + k * QLD + c) = kv;
+    const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vt[(c + 2 * j) * QLD + k] = (uint16_t)(w4[j] & 0xffffu);
+      vt[(c + 2 * j + 1) * QLD + k] = (uint16_t)(w4[j] >> 16);
+    }
+  }
+  if (tid < 64) {
+    ps[tid] = tid < g.K ? g.top_p[ih * g.K + tid] : 0.f;
+    rs[tid] = g.rest[ih * 64 + tid];
+  } else if (tid < 96) {
+    cs[tid - 64] = g.cos_t[pc * 32 + tid - 64];
+    sn[tid - 64] = g.sin_t[pc * 32 + tid - 64];
+  }
+  __syncthreads();
+  if (tid < 64) {  // the clean rotated query of this head and inv0
+    const float* cr = g.dr + ((int64_t)g.m * g.P + i) * g.W + h * 64;
+    const int c = tid & 31;
+    const float u1 = cr[c], u2 = cr[c + 32];
+    const float v = tid < 32 ? u1 * cs[c] + u2 * sn[c] : -u1 * sn[c] + u2 * cs[c];
+    r0s[tid] = v;
+    const float sq = wave_sum(v * v);
+    if (tid == 0) inv0s = sq;
+  }
+  __syncthreads();
+  const float sq = inv0s, inv0 = rsqrtf(sq / 64.f + CAP_EPS32);
+
+  // dq: lanes 2 q and 2 q + 1 hold move q's dims c, c + 32 for c in [0, 16) and [16, 32)
+  {
+    const int q = lane >> 1, c0 = (lane & 1) * 16;
+    const int p = min(pw + q, g.P - 1);
+    const float* src = g.dr + ((int64_t)i * g.P + p) * g.W + h * 64;
+    float u1[16], u2[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4 a = ld4(src + c0 + 4 * t), b = ld4(src + 32 + c0 + 4 * t);
+      u1[4 * t] = a.x; u1[4 * t + 1] = a.y; u1[4 * t + 2] = a.z; u1[4 * t + 3] = a.w;
+      u2[4 * t] = b.x; u2[4 * t + 1] = b.y; u2[4 * t + 2] = b.z; u2[4 * t + 3] = b.w;
+    }
+    float dot = 0.f, dsq = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int c = c0 + t;
+      const float v1 = u1[t] * cs[c] + u2[t] * sn[c], v2 = -u1[t] * sn[c] + u2[t] * cs[c];
+      u1[t] = v1;
+      u2[t] = v2;
+      dot += r0s[c] * v1 + r0s[c + 32] * v2;
+      dsq += v1 * v1 + v2 * v2;
+    }
+    dot += noise::dpp_row<0xB1>(dot);
+    dsq += noise::dpp_row<0xB1>(dsq);
+    const float inv = rsqrtf((sq + 2.f * dot + dsq) / 64.f + CAP_EPS32), dinv = inv - inv0;
+    uint16_t* dst = at[wave] + q * QLD;
+#pragma unroll
+    for (int t = 0; t < 16; t += 8) {
+      uint4 w1, w2;
+      uint32_t* p1 = reinterpret_cast<uint32_t*>(&w1);
+      uint32_t* p2 = reinterpret_cast<uint32_t*>(&w2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int a = t + 2 * j, c = c0 + a;
+        p1[j] = pack_bf2(u1[a] * inv + r0s[c] * dinv, u1[a + 1] * inv + r0s[c + 1] * dinv);
+        p2[j] = pack_bf2(u2[a] * inv + r0s[c + 32] * dinv, u2[a + 1] * inv + r0s[c + 33] * dinv);
+      }
+      *reinterpret_cast<uint4*>(dst + c0 + t) = w1;
+      *reinterpret_cast<uint4*>(dst + 32 + c0 + t) = w2;
+    }
+  }
+  __syncthreads();
+
+  // ds = bf16(dq K^T) / 8; lane l holds keys ni * 32 + l % 32 of rows 8 (j / 4) + 4 (l / 32) + j % 4
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  floatx16 acc[2];
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
+      acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ni], 0, 0, 0);
+    }
+  }
+  const float p_0 = ps[fr], p_1 = ps[32 + fr];
+  float es[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    acc[0][j] = bf2f(f2bf(acc[0][j])) * 0.125f;
+    acc[1][j] = bf2f(f2bf(acc[1][j])) * 0.125f;
+    es[j] = p_0 * expm1f(acc[0][j]) + p_1 * expm1f(acc[1][j]);
+  }
+  {
+    const float tot = noise::halfwave_transpose_sum16(es, lane);
+    const int jj = fr >> 1;
+    if ((lane & 1) == 0) dls[wave][8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3)] = log1pf(tot);
+  }
+  __syncthreads();  // dls complete; every wave is done reading its dq tile
+  float dl[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+    dl[j] = dls[wave][row];
+    at[wave][row * QLD + fr] = f2bf(p_0 * expm1f(acc[0][j] - dl[j]));
+    at[wave][row * QLD + 32 + fr] = f2bf(p_1 * expm1f(acc[1][j] - dl[j]));
+  }
+  __syncthreads();
+
+  // dout = bf16(w V) + expm1(-dlse) rest; lane l holds dims ni * 32 + l % 32
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(vt + (ni * 32 + fr) * QLD + 16 * ks + fk);
+      acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ni], 0, 0, 0);
+    }
+  }
+  const float r_0 = rs[fr], r_1 = rs[32 + fr];
+  const float nan = __builtin_nanf("");
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int p = pw + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+    if (p >= g.P) continue;
+    const float em = expm1f(-dl[j]);
+    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64;
+    split3(o, g.W, fr, pos_ok ? bf2f(f2bf(acc[0][j])) + em * r_0 : nan, true);
+    split3(o, g.W, 32 + fr, pos_ok ? bf2f(f2bf(acc[1][j])) + em * r_1 : nan, true);
   }
 }
 
@@ -407,6 +669,49 @@ extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
   ChainGemm g2{a->g, a->wo, a->P, a->W, a->k, nullptr, 0, nullptr, a->delta};
   chain_gemm_kernel<MODE_ADDROUND, 256><<<dim3((unsigned)tiles_p, a->W / 256, a->m), 512, 0, st>>>(g2);
   return noise::check_launch("chain_block");
+}
+
+extern "C" int noise_chain_query(const noise_chain_query_t* a, void* stream) {
+  NOISE_REQUIRE(a, "chain_query: args is NULL");
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 256 * MAXT && a->heads > 0 &&
+                    a->W == 64 * a->heads && a->K >= 1 && a->K <= 64 && a->T > 0,
+                "chain_query: bad sizes (m=%d P=%d W=%d heads=%d K=%d T=%d; W = 64 heads, a multiple of 256 up "
+                "to 2048, 1 <= K <= 64)",
+                a->m, a->P, a->W, a->heads, a->K, a->T);
+  if (a->m == 0) return NOISE_OK;
+  NOISE_REQUIRE(a->delta && a->x && a->pos && a->w_q && a->top_keys && a->top_values && a->top_p && a->rest &&
+                    a->w_proj_t && a->cos_t && a->sin_t && a->a3 && a->dr && a->wq3 && a->wp3,
+                "chain_query: NULL argument");
+  NOISE_REQUIRE(aligned16(a->delta) && (!a->dx0 || aligned16(a->dx0)) && aligned16(a->x) && aligned16(a->dr) &&
+                    aligned16(a->a3) && aligned16(a->wq3) && aligned16(a->wp3) && aligned16(a->top_keys) &&
+                    aligned16(a->top_values),
+                "chain_query: delta, dx0, x, keys, values and the workspaces must be 16-byte aligned");
+  NOISE_REQUIRE(a->m <= 65535 && ((int64_t)a->m * a->P + a->m) * 3 * a->W < (1ll << 40) &&
+                    (int64_t)a->m * a->P + a->m < (1ll << 31),
+                "chain_query: at most 65535 tokens per call");
+  const hipStream_t st = (hipStream_t)stream;
+  const int W = a->W;
+  const int64_t rows = (int64_t)a->m * a->P, rows_all = rows + a->m;
+  const unsigned wblocks = (unsigned)(((int64_t)W * W + 255) / 256);
+  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(a->w_q, W, 1, W, a->wq3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(a->w_proj_t, 1, W, W, a->wp3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  chain_query_pre_kernel<<<(unsigned)((rows_all + 3) / 4), 256, 0, st>>>(a->delta, a->dx0, a->x, a->m, a->P, W,
+                                                                         a->mix, a->lam_r, a->lam_0, a->a3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  // query products of every move and of the clean rows: dr = A3 Wq3^T (fp32)
+  ChainGemm g1{a->a3, a->wq3, (int)rows_all, W, 3 * W, nullptr, 0, nullptr, a->dr};
+  chain_gemm_kernel<MODE_STORE, 256><<<dim3((unsigned)((rows_all + 255) / 256), W / 256, 1), 512, 0, st>>>(g1);
+  if (int e = noise::check_launch("chain_query")) return e;
+  ChainQuery q{a->dr, a->pos, a->cos_t, a->sin_t, a->top_keys, a->top_values, a->top_p, a->rest,
+               a->T, a->m, a->P, W, a->heads, a->K, a->a3};
+  chain_query_attn_kernel<<<dim3((unsigned)((a->P + 127) / 128), a->heads, a->m), 256, 0, st>>>(q);
+  if (int e = noise::check_launch("chain_query")) return e;
+  // delta += dout c_proj^T (fp32), over the moves' rows of A3
+  ChainGemm g2{a->a3, a->wp3, (int)rows, W, 3 * W, nullptr, 0, nullptr, a->delta};
+  chain_gemm_kernel<MODE_ADD, 256><<<dim3((unsigned)((rows + 255) / 256), W / 256, 1), 512, 0, st>>>(g2);
+  return noise::check_launch("chain_query");
 }
 
 extern "C" int noise_chain_head(const noise_chain_head_t* a, void* stream) {

@@ -1,6 +1,6 @@
 """Soft-capped log-sum-exp probes of the readout head, on the HIP kernels of libnoise_amd.
 
-Drop-in twins of three functions of the reference trainer, with the same arguments, shapes and
+Drop-in twins of four functions of the reference trainer, with the same arguments, shapes and
 float32 results (device tensors in, device tensors out, asynchronous on the current stream):
 
 * `coordinate_differences(raw, y, sigma)`  -- train/val/run.py:100-111 (speedrun/run.py:57-68)
@@ -8,7 +8,9 @@ float32 results (device tensors in, device tensors out, asynchronous on the curr
 * `row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq)`   -- train/val/run.py:170-183
 * `chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t,
   weight_t, base, target_logit_w, y, own=None)`                   -- train/val/run.py:307-351,
-  with every attention held (own = None); the own-query variants are not built here
+  with every attention held (own = None) or with the routed own-query moves (own = ('routed', ...),
+  query_change_routed, train/val/run.py:284-304); the key-window variant (own = ('window', ...))
+  is not built here
 
 The reference reads the stream width from a module constant (WIDTH = 512); here it is the keyword
 `width`. A target y < 0 masks its token (zeros, as the reference's `* (y >= 0)`); a target >= V
@@ -19,7 +21,7 @@ import ctypes as C
 import torch
 
 from . import _lib
-from ._lib import ChainBlock, ChainHead, Probe
+from ._lib import ChainBlock, ChainHead, ChainQuery, Probe
 
 WIDTH = 512
 
@@ -144,9 +146,14 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     restricted to each token's routed units (train/val/run.py:307-351). site: -1 for the raw
     embedding, else the block whose mid stream moves; move [m, P, W]; scale [m, P]; e, x0, xL
     [m, W]; mids, idx, hs per block ([m, W], [m, k], [m, k]); w_fc, w_out_t per block [H, W];
-    weight_t [W, V]; base [m, V]; target_logit_w [m, W]; y [m]. Returns float32 [m, P]."""
-    if own is not None:
-        raise NotImplementedError('chain_chunk: only own=None (every attention held) runs on libnoise_amd')
+    weight_t [W, V]; base [m, V]; target_logit_w [m, W]; y [m]. own: None, or ('routed', pos,
+    inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, (cos, sin)) as the reference's
+    strong_keys builds it: pos [m]; per block inputs [m, W], w_q [W, W], top_keys and top_values
+    [m, heads, K, 64], top_p [m, heads, K], rest [m, heads, 64], w_proj_t [W, W]; cos, sin
+    [T, 32]. Returns float32 [m, P]."""
+    if own is not None and own[0] != 'routed':
+        raise NotImplementedError(f'chain_chunk: own = {own[0]!r} is not built on libnoise_amd '
+                                  "(own = None and own = ('routed', ...) are)")
     m, P, W = move.shape
     L = len(mids)
     V = weight_t.shape[1]
@@ -179,7 +186,13 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     wf = torch.empty(m, k, W, dtype=torch.bfloat16, device=dev)
     wo = torch.empty(m, W, k, dtype=torch.bfloat16, device=dev)
     g = torch.empty(m * P, k, dtype=torch.bfloat16, device=dev)
+    query = _routed_query(own, m, P, W, L, dev) if own is not None else None
     for b in range(first, L):
+        mix = int(b > first)
+        if query is not None and (site < 0 or b > first):
+            # the move is at the block's input: its own query moves too (the step mixes first)
+            query(b, delta, dx0, mix, lr[b], l0[b])
+            mix = 0
         mid = _dev_f32(mids[b], (m, W), f'mids[{b}]')
         ib = idx[b].to(device=dev, dtype=torch.int64).contiguous()
         hb = _dev_f32(hs[b], (m, k), f'hs[{b}]')
@@ -187,7 +200,7 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
         wot = _dev_bf16(w_out_t[b], (H, W), f'w_out_t[{b}]')
         _need(tuple(ib.shape) == (m, k), f'idx[{b}]: expected shape {(m, k)}, got {tuple(ib.shape)}')
         a = ChainBlock(delta=delta.data_ptr(), dx0=dx0.data_ptr() if dx0 is not None else None,
-                       mix=int(b > first), lam_r=lr[b], lam_0=l0[b], mid=mid.data_ptr(), idx=ib.data_ptr(),
+                       mix=mix, lam_r=lr[b], lam_0=l0[b], mid=mid.data_ptr(), idx=ib.data_ptr(),
                        ld_idx=k, hs=hb.data_ptr(), ld_hs=k, w_fc=wfc.data_ptr(), w_out_t=wot.data_ptr(),
                        m=m, P=P, W=W, k=k, H=H, dz=dz.data_ptr(), wf=wf.data_ptr(), wo=wo.data_ptr(),
                        g=g.data_ptr())
@@ -202,3 +215,46 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
                   clean=clean.data_ptr())
     _lib.call('noise_chain_head', C.byref(h), stream)
     return out
+
+
+def _routed_query(own, m, P, W, L, dev):
+    """Checks own = ('routed', ...) and returns step(b, delta, dx0, mix, lam_r, lam_0), which runs
+    the block's own-query step (noise_chain_query) in place on delta."""
+    _need(len(own) == 10, "own: expected ('routed', pos, inputs, w_q, top_keys, top_values, top_p, rest, "
+                          'w_proj_t, (cos, sin))')
+    _, pos, inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos_sin = own
+    for name, v in (('inputs', inputs), ('w_q', w_q), ('top_keys', top_keys), ('top_values', top_values),
+                    ('top_p', top_p), ('rest', rest), ('w_proj_t', w_proj_t)):
+        _need(len(v) >= L, f'own {name}: one entry per block')
+    _need(W % 64 == 0, f'own: width {W} is not a whole number of 64-wide heads')
+    heads = W // 64
+    _need(top_keys[0].dim() == 4 and tuple(top_keys[0].shape[:2]) == (m, heads) and top_keys[0].shape[3] == 64,
+          f'own top_keys: expected [{m}, {heads}, K, 64], got {tuple(top_keys[0].shape)}')
+    K = top_keys[0].shape[2]
+    _need(pos.is_cuda and not pos.is_floating_point() and pos.numel() == m, f'own pos: expected {m} device integers')
+    ps = pos.reshape(m).to(torch.int64).contiguous()
+    cos, sin = cos_sin
+    _need(cos.dim() == 2 and cos.shape[1] == 32, f'own cos: expected [T, 32], got {tuple(cos.shape)}')
+    T = cos.shape[0]
+    ct, st = _dev_f32(cos, (T, 32), 'own cos'), _dev_f32(sin, (T, 32), 'own sin')
+    a3 = torch.empty(m * P + m, 3 * W, dtype=torch.bfloat16, device=dev)
+    dr = torch.empty(m * P + m, W, dtype=torch.float32, device=dev)
+    wq3 = torch.empty(W, 3 * W, dtype=torch.bfloat16, device=dev)
+    wp3 = torch.empty_like(wq3)
+
+    def step(b, delta, dx0, mix, lam_r, lam_0):
+        x = _dev_f32(inputs[b], (m, W), f'own inputs[{b}]')
+        wq = _dev_f32(w_q[b], (W, W), f'own w_q[{b}]')
+        kk = _dev_bf16(top_keys[b], (m, heads, K, 64), f'own top_keys[{b}]')
+        vv = _dev_bf16(top_values[b], (m, heads, K, 64), f'own top_values[{b}]')
+        pp = _dev_f32(top_p[b], (m, heads, K), f'own top_p[{b}]')
+        rr = _dev_f32(rest[b], (m, heads, 64), f'own rest[{b}]')
+        wp = _dev_f32(w_proj_t[b], (W, W), f'own w_proj_t[{b}]')
+        a = ChainQuery(delta=delta.data_ptr(), dx0=dx0.data_ptr() if dx0 is not None else None, mix=mix,
+                       lam_r=lam_r, lam_0=lam_0, x=x.data_ptr(), pos=ps.data_ptr(), w_q=wq.data_ptr(),
+                       top_keys=kk.data_ptr(), top_values=vv.data_ptr(), top_p=pp.data_ptr(), rest=rr.data_ptr(),
+                       w_proj_t=wp.data_ptr(), cos_t=ct.data_ptr(), sin_t=st.data_ptr(), T=T, m=m, P=P, W=W,
+                       heads=heads, K=K, a3=a3.data_ptr(), dr=dr.data_ptr(), wq3=wq3.data_ptr(),
+                       wp3=wp3.data_ptr())
+        _lib.call('noise_chain_query', C.byref(a), _stream())
+    return step

@@ -3,7 +3,7 @@
 Only tests/ and bench.py's `cpu_baseline` leg may import this module, and only as the checker.
 The shipped path (noise_amd/probes.py over libnoise_amd) never calls it.
 
-Restatements in numpy float64 (float32 when asked) of three functions of the reference trainer:
+Restatements in numpy float64 (float32 when asked) of five functions of the reference trainer:
 
 * `coordinate_differences` -- train/val/run.py:100-111 (train/speedrun/run.py:57-68): central
   differences of each token's soft-capped cross-entropy along each of its own logits, in the
@@ -12,14 +12,20 @@ Restatements in numpy float64 (float32 when asked) of three functions of the ref
   differences of each token's readout loss along every direction of a cycle, the moved stream's
   RMS norm evaluated exactly from |x|^2, x.D_j and |D_j|^2;
 * `row_derivatives`        -- train/val/run.py:170-183: the same along per-token rows of the
-  direction set.
+  direction set;
+* `query_change_routed`    -- train/val/run.py:284-304: a token's attention output change when its
+  own query moves and only its top keys' logits move;
+* `chain_chunk`            -- train/val/run.py:307-351 with own = None or ('routed', ...): moves
+  of one site carried through the later blocks' routed MLPs (and own-query attention changes) to
+  the head's loss.
 
 cap(v) = 15 tanh(v / 15); norm(x) = x rsqrt(|x|^2 / width + eps), eps = float32 machine epsilon.
 
-Pinning (tests/test_oracle.py): each function against a brute-force evaluation that never uses
-its closed form -- the moved streams / logits are built explicitly and pushed through
-torch.nn.functional.cross_entropy in float64 (one forward per probe), and row_derivatives
-against cycle_derivatives gathered at the rows.
+Pinning (tests/test_probes_oracle.py): each function against a brute-force evaluation that never
+uses its closed form -- the moved streams / logits / queries are built explicitly and pushed
+through torch.nn.functional.cross_entropy or an explicit softmax in float64 (one forward per
+probe), and row_derivatives against cycle_derivatives gathered at the rows. The 'tf32' policy's
+rounding is pinned against hand-computed values.
 """
 import numpy as np
 
@@ -106,6 +112,14 @@ def _bf16(x):
     return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).bfloat16().double().numpy()
 
 
+def _tf32(x):
+    """Round to TF32 (10 explicit mantissa bits, round to nearest, ties away from zero), returned as
+    float64: the input rounding of the reference's float32 products under
+    torch.set_float32_matmul_precision('high') (train/val/run.py:1286)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return (((b + 0x1000) & 0xFFFFE000).astype(np.uint32)).view(np.float32).astype(np.float64)
+
+
 def _rms(x, width):
     return x / np.sqrt(np.sum(x * x, -1, keepdims=True) / width + EPS32)
 
@@ -126,9 +140,12 @@ def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w
     projection, when only its own query moves and only the logits of its top keys per head move.
     x (m, W) block input; delta (m, P, W); top_keys, top_values (m, h, K, d); top_p (m, h, K);
     rest (m, h, d); w_q (W, W); w_proj_t (W, W) = c_proj.weight^T; cos, sin (T, d / 2).
-    'build' rounds where the reference casts to bf16 (dq, both einsum products, the weights)."""
+    'build' rounds where the reference casts to bf16 (dq, both einsum products, the weights);
+    'tf32' also rounds the inputs of the three float32 products to TF32, as the reference's
+    hardware does under its matmul precision setting (the envelope of its own arithmetic)."""
     dt = np.float32 if policy == 'build32' else np.float64
-    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32') else (lambda v: v)
+    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32', 'tf32') else (lambda v: v)
+    tf = _tf32 if policy == 'tf32' else (lambda v: v)
     f = lambda v: np.asarray(v, dt)
     x, delta, w_q, keys, vals, tp, rest, w_proj_t = map(f, (x, delta, w_q, top_keys, top_values, top_p, rest,
                                                            w_proj_t))
@@ -139,8 +156,8 @@ def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w
     c, s_ = cos[pos][:, None, None, :], sin[pos][:, None, None, :]
     rot = lambda u: np.concatenate([u[..., :d // 2] * c + u[..., d // 2:] * s_,
                                     u[..., :d // 2] * -s_ + u[..., d // 2:] * c], -1)
-    r0 = rot((_rms(x, width) @ w_q.T).reshape(m, 1, heads, d))
-    dr = rot((norm_difference(x, delta, width) @ w_q.T).reshape(m, P, heads, d))
+    r0 = rot((tf(_rms(x, width)) @ tf(w_q).T).reshape(m, 1, heads, d))
+    dr = rot((tf(norm_difference(x, delta, width)) @ tf(w_q).T).reshape(m, P, heads, d))
     sq = np.sum(r0 * r0, -1, keepdims=True)
     inv0 = 1.0 / np.sqrt(sq / d + EPS32)
     inv = 1.0 / np.sqrt((sq + 2 * np.sum(r0 * dr, -1, keepdims=True) + np.sum(dr * dr, -1, keepdims=True)) / d + EPS32)
@@ -150,7 +167,7 @@ def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w
     dlse = np.log1p(np.sum(p * np.expm1(ds), -1, keepdims=True))
     dout = rb(np.einsum('mphk,mhkd->mphd', rb(p * np.expm1(ds - dlse)), vals))
     dout = dout + np.expm1(-dlse) * rest[:, None]
-    return dout.reshape(m, P, heads * d) @ w_proj_t
+    return tf(dout.reshape(m, P, heads * d)) @ tf(w_proj_t)
 
 
 def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t,
@@ -163,9 +180,10 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     reference casts (dz, both routed products and their inputs, the head product and its input);
     'build32': the same casts in float32 arithmetic, so |build - build32| shows how far the casts
     alone let two correct evaluations drift (a product landing on the other side of a bf16
-    rounding boundary). Returns (m, P)."""
+    rounding boundary); 'tf32': 'build' with the own-query step's float32 products on TF32 inputs
+    (query_change_routed). Returns (m, P)."""
     dt = np.float32 if policy == 'build32' else np.float64
-    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32') else (lambda v: v)
+    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32', 'tf32') else (lambda v: v)
     f = lambda v: np.asarray(v, dt)
     move, scale, e, x0, xL, base, tw = map(f, (move, scale, e, x0, xL, base, target_logit_w))
     lam_r, lam_0 = f(lam_r), f(lam_0)

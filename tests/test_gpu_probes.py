@@ -179,13 +179,13 @@ def _to(d, device):
     return {k: ([v.to(device) for v in x] if isinstance(x, list) else x.to(device)) for k, x in d.items()}
 
 
-def _oracle_chain(site, d, rows, policy):
+def _oracle_chain(site, d, rows, policy, own=None):
     sub = {k: ([v[rows] for v in x] if k in ('mids', 'idx', 'hs') else
                (x if k in ('lam_r', 'lam_0', 'w_fc', 'w_out_t', 'weight_t') else x[rows]))
            for k, x in d.items()}
     sub = {k: ([v.double().numpy() if v.is_floating_point() else v.numpy() for v in x] if isinstance(x, list)
                else (x.double().numpy() if x.is_floating_point() else x.numpy())) for k, x in sub.items()}
-    return P.chain_chunk(site, **sub, policy=policy)
+    return P.chain_chunk(site, **sub, own=own, policy=policy)
 
 
 @pytest.mark.parametrize('site,m,P_,L', [(-1, 6, 40, 3), (1, 5, 37, 3), (0, 3, 516, 2)])
@@ -211,3 +211,111 @@ def test_chain_chunk_matches_oracle(device, site, m, P_, L):
     assert np.isfinite(got).all()
     assert err.max() <= 2 * env[ok].max() + 1e-4 * scale
     assert err.mean() <= 2 * env[ok].mean() + 1e-5 * scale
+
+
+def _routed_own(m, L, K, seed, W=512, T=1024):
+    """own = ('routed', ...) at the model's widths: per block input streams, fp32 c_q and c_proj
+    weights, unit-RMS bf16 keys, bf16 values, top-K clean probabilities from a softmax over a wider
+    key set and the held keys' share; positions and rotary tables over T."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g)
+    heads = W // 64
+    pos = torch.randint(0, T, (m,), generator=g)
+    ang = torch.arange(T)[:, None].float() * (1.0 / 1024 ** torch.linspace(0, 1, 32))[None]
+    inputs = [rn(m, W) * 3 for _ in range(L)]
+    w_q = [rn(W, W) / W ** 0.5 for _ in range(L)]
+    w_proj_t = [rn(W, W) / W ** 0.5 for _ in range(L)]
+    keys, vals, probs, rests = [], [], [], []
+    for _ in range(L):
+        k_ = rn(m, heads, K, 64)
+        keys.append((k_ * torch.rsqrt(k_.square().mean(-1, keepdim=True))).bfloat16())
+        vals.append(rn(m, heads, K, 64).bfloat16())
+        full = torch.softmax(rn(m, heads, K + 32) * 2, -1).sort(-1, descending=True).values
+        probs.append(full[..., :K].contiguous())
+        rests.append((1 - full[..., :K].sum(-1, keepdim=True)) * rn(m, heads, 64) * 0.5)
+    return ('routed', pos, inputs, w_q, keys, vals, probs, rests, w_proj_t, (ang.cos(), ang.sin()))
+
+
+def _own_to(own, device=None, rows=None):
+    """own moved to a device, or sliced to `rows` and turned into float64 numpy for the oracle."""
+    if device is not None:
+        conv = lambda t: t.to(device)
+    else:
+        conv = lambda t: t.double().numpy() if t.is_floating_point() else t.numpy()
+    sl = (lambda t: t[rows]) if rows is not None else (lambda t: t)
+    _, pos, inputs, w_q, keys, vals, probs, rests, w_proj_t, (cos, sin) = own
+    tok = lambda part: [conv(sl(t)) for t in part]   # per-token entries, sliced
+    return ('routed', conv(sl(pos)), tok(inputs), [conv(t) for t in w_q], tok(keys), tok(vals), tok(probs),
+            tok(rests), [conv(t) for t in w_proj_t], (conv(cos), conv(sin)))
+
+
+@pytest.mark.parametrize('site,m,P_,L,K', [(-1, 5, 40, 3, 64), (1, 4, 37, 3, 20), (0, 3, 516, 2, 64)])
+def test_chain_chunk_routed_matches_oracle(device, site, m, P_, L, K):
+    """chain_chunk with own = ('routed', ...): each block the move enters first changes its own
+    token's attention output through its own query along its top keys (train/val/run.py:284-304).
+    The bar adds the own-query step's tf32 envelope (its float32 products on the reference's TF32
+    inputs, see the step's own test) to the build / build32 one; the own-query term itself must
+    move the result."""
+    d = _chain_case(site, m, P_, L, seed=m + P_ + K)
+    d['y'][1] = -1
+    own = _routed_own(m, L, K, seed=K + m)
+    got = _probes().chain_chunk(site, **_to(d, device), own=_own_to(own, device)).cpu().double().numpy()
+    none = _probes().chain_chunk(site, **_to(d, device)).cpu().double().numpy()
+    torch.cuda.synchronize()
+    rows = np.arange(m)
+    sub = _own_to(own, rows=rows)
+    want = _oracle_chain(site, d, rows, 'build', own=sub)
+    env = np.abs(want - _oracle_chain(site, d, rows, 'build32', own=sub))[rows != 1]
+    etf = np.abs(want - _oracle_chain(site, d, rows, 'tf32', own=sub))[rows != 1]
+    assert np.all(got[1] == 0)
+    ok = rows != 1
+    err = np.abs(got[ok] - want[ok])
+    scale = np.abs(want[ok]).max()
+    print(f'routed chain site {site} K {K}: max |gpu - build| {err.max():.3e} (envelopes {env.max():.3e}, '
+          f'tf32 {etf.max():.3e}), mean {err.mean():.3e} (envelopes {env.mean():.3e}, tf32 {etf.mean():.3e}), '
+          f'max |want| {scale:.3e}, own term {np.abs(got - none)[ok].max():.3e}')
+    assert np.isfinite(got).all()
+    assert err.max() <= 2 * max(env.max(), etf.max()) + 1e-4 * scale
+    assert err.mean() <= 2 * env.mean() + 0.5 * etf.mean() + 1e-5 * scale
+    assert np.abs(got - none)[ok].max() > 10 * (err.max() + 1e-6 * scale)
+
+
+def test_chain_chunk_routed_bad_position_gives_nan(device):
+    """A position outside the rotary tables gives NaN for that token's moves (the reference's
+    index would fault on the device), the other tokens unchanged."""
+    site, m, P_, L, K = -1, 3, 16, 2, 8
+    d = _chain_case(site, m, P_, L, seed=3)
+    own = _routed_own(m, L, K, seed=4)
+    good = _probes().chain_chunk(site, **_to(d, device), own=_own_to(own, device)).cpu()
+    own[1][2] = 5000
+    bad = _probes().chain_chunk(site, **_to(d, device), own=_own_to(own, device)).cpu()
+    assert torch.isnan(bad[2]).all()
+    assert torch.equal(bad[:2], good[:2])
+
+
+@pytest.mark.parametrize('m,P_,K', [(4, 70, 64), (3, 300, 37), (2, 5, 1)])
+def test_chain_query_step_matches_oracle(device, m, P_, K):
+    """The own-query step alone (noise_chain_query, mix off): the change it adds to delta against
+    query_change_routed with the reference's bf16 casts (build). The reference runs the step's
+    three float32 products on TF32 inputs; the kernels run them as bf16 hi/lo triples (2^-16
+    relative against TF32's 2^-11), so the GPU is held to twice the tf32 envelope |build - tf32|
+    at its largest and to half of it on average."""
+    own = _routed_own(m, 1, K, seed=m * P_ + K)
+    g = torch.Generator().manual_seed(K)
+    delta = torch.randn(m, P_, 512, generator=g) * 0.05
+    dev_delta = delta.reshape(m * P_, 512).to(device)
+    step = _probes()._routed_query(_own_to(own, device), m, P_, 512, 1, dev_delta.device)
+    step(0, dev_delta, None, 0, 1.0, 0.0)
+    got = (dev_delta.cpu().double().reshape(m, P_, 512) - delta.double()).numpy()
+    torch.cuda.synchronize()
+    sub = _own_to(own, rows=np.arange(m))
+    args = (sub[2][0], delta.double().numpy(), sub[1], sub[3][0], sub[4][0], sub[5][0], sub[6][0], sub[7][0],
+            sub[8][0], sub[9][0], sub[9][1])
+    want = P.query_change_routed(*args, policy='build')
+    env = np.abs(want - P.query_change_routed(*args, policy='tf32'))
+    err = np.abs(got - want)
+    scale = np.abs(want).max()
+    print(f'query step m {m} P {P_} K {K}: max |gpu - build| {err.max():.3e} (tf32 envelope {env.max():.3e}), '
+          f'mean {err.mean():.3e} (tf32 envelope {env.mean():.3e}), max |want| {scale:.3e}')
+    assert err.max() <= 2 * env.max()
+    assert err.mean() <= 0.5 * env.mean()

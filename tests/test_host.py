@@ -62,6 +62,19 @@ def test_argument_errors_raise_before_launch():
     assert lib.noise_row_derivatives(C.byref(a), None) == _lib.NOISE_EINVAL        # rows is NULL
     with pytest.raises(ValueError, match='rows'):
         _lib.check(_lib.NOISE_EINVAL)
+    # Own-query step: width not 64 per head, K outside [1, 64], a NULL key set; m = 0 is a no-op.
+    q = _lib.ChainQuery(delta=256, x=256, pos=512, w_q=256, top_keys=256, top_values=256, top_p=256, rest=256,
+                        w_proj_t=256, cos_t=256, sin_t=256, T=16, m=2, P=4, W=512, heads=4, K=8, a3=256, dr=256,
+                        wq3=256, wp3=256)
+    assert lib.noise_chain_query(C.byref(q), None) == _lib.NOISE_EINVAL            # W != 64 heads
+    q.heads, q.K = 8, 65
+    assert lib.noise_chain_query(C.byref(q), None) == _lib.NOISE_EINVAL            # K > 64
+    q.K, q.top_keys = 64, None
+    assert lib.noise_chain_query(C.byref(q), None) == _lib.NOISE_EINVAL            # NULL keys
+    with pytest.raises(ValueError, match='NULL'):
+        _lib.check(_lib.NOISE_EINVAL)
+    q.m = 0
+    assert lib.noise_chain_query(C.byref(q), None) == _lib.NOISE_OK
 
 
 def test_state_dict_strict_round_trip():

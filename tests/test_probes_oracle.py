@@ -257,3 +257,13 @@ def test_chain_chunk_routed_brute_force(site):
     np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-11)
     none = P.chain_chunk(site, **d, width=W)
     assert np.abs(got - none)[[0, 2]].max() > 1e-3 * np.abs(none).max()   # the own-query term is live
+
+
+def test_tf32_rounding():
+    """_tf32 keeps 10 mantissa bits, rounding to nearest with ties away from zero."""
+    u = 2.0 ** -10
+    vals = np.array([1.0, 1 + u, 1 + u / 2, 1 + u / 2 - 2 ** -23, 1 + 3 * u / 2, -(1 + u / 2), 3.0, 1e-30])
+    want = np.array([1.0, 1 + u, 1 + u, 1.0, 1 + 2 * u, -(1 + u), 3.0, 0.0])
+    got = P._tf32(vals)
+    np.testing.assert_array_equal(got[:-1], want[:-1])
+    assert abs(got[-1] - 1e-30) <= 1e-30 * 2 ** -10
