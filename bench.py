@@ -5,6 +5,7 @@
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
     python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
     python bench.py --probe-chain    # chain_chunk (attention held) at the Cut estimator's shape, own JSON line
+    python bench.py --probe-chain --own routed   # the same with the routed own-query moves
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -168,10 +169,11 @@ def bench_probe_cycle(steps, warmup, no_cpu, n=2048, P=512, V=4096):
     print(json.dumps(line), flush=True)
 
 
-def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=4096):
-    """chain_chunk with every attention held (train/val/run.py:307-351) for one chunk of the Cut
-    estimator: 256 tokens x a full cycle of 512 moves of the raw embedding (site -1) through 8
-    blocks with 128 routed units each, then the head over V = 4096."""
+def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=4096, own=False, K=64, T=2048):
+    """chain_chunk (train/val/run.py:307-351) for one chunk of the Cut estimator: 256 tokens x a full
+    cycle of 512 moves of the raw embedding (site -1) through 8 blocks with 128 routed units each,
+    then the head over V = 4096. own: every block also moves its own token's attention through its
+    own query along its top K = 64 keys per head (own = ('routed', ...), the estimator's default)."""
     from noise_amd import probes
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
@@ -192,6 +194,20 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
                 mids=mids, xL=xL, idx=idx, hs=hs, lam_r=torch.ones(L), lam_0=torch.full((L,), 0.1), w_fc=w_fc,
                 w_out_t=w_out_t, weight_t=weight.T.bfloat16().contiguous(), base=xL @ weight.T,
                 target_logit_w=weight[y], y=y)
+    if own:
+        heads = W // 64
+        ang = torch.arange(T, device=dev)[:, None].float() * (1.0 / 1024 ** torch.linspace(0, 1, 32, device=dev))[None]
+        keys = []
+        for _ in range(L):
+            k_ = rn(m, heads, K, 64)
+            keys.append((k_ * torch.rsqrt(k_.square().mean(-1, keepdim=True))).bfloat16())
+        probs = [torch.softmax(rn(m, heads, K + 32) * 2, -1).sort(-1, descending=True).values[..., :K].contiguous()
+                 for _ in range(L)]
+        args['own'] = ('routed', torch.arange(m, device=dev) + (T - m), [rn(m, W) * 3 for _ in range(L)],
+                       [rn(W, W) / W ** 0.5 for _ in range(L)], keys,
+                       [rn(m, heads, K, 64).bfloat16() for _ in range(L)], probs,
+                       [(1 - p.sum(-1, keepdim=True)) * rn(m, heads, 64) * 0.5 for p in probs],
+                       [rn(W, W) / W ** 0.5 for _ in range(L)], (ang.cos(), ang.sin()))
     for _ in range(warmup):
         probes.chain_chunk(-1, **args)
     stream = torch.cuda.current_stream()
@@ -206,13 +222,17 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
     elapsed = time.perf_counter() - t0
     call_ms = sum(a.elapsed_time(b) for a, b in events) / steps
     flops = 2 * m * P * W * k * 2 * L + 2 * m * P * W * V
+    if own:  # per block: two float32 products as three bf16 MFMA products each, two 64 x 64 per head
+        flops += L * (2 * (m * P + m) * W * 3 * W + 2 * m * P * W * 3 * W + m * P * (W // 64) * 4 * 64 * 64)
+    workload = ('chain_chunk site -1, own-query routed (K=64): ' if own else 'chain_chunk site -1, attention held: ') + \
+        '256 tokens x 512 moves, 8 blocks, k=128, V=4096'
     line = {
         'metric': 'chain_chunk moves/sec on 1 GPU (token x move through 8 routed blocks and the soft-capped head)',
         'value': m * P * steps / elapsed, 'unit': 'moves/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
         'ms_per_step': elapsed / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
         'dtype': 'bf16', 'data': 'synthetic (random streams, bf16 block weights, Gaussian moves)',
-        'config': {'workload': 'chain_chunk site -1, attention held: 256 tokens x 512 moves, 8 blocks, k=128, V=4096',
-                   'tokens': m, 'moves': P, 'blocks': L, 'routed_units': k, 'vocab': V},
+        'config': {'workload': workload, 'tokens': m, 'moves': P, 'blocks': L, 'routed_units': k, 'vocab': V,
+                   'own': 'routed' if own else None},
         'roofline': {'bound': 'mfma', 'achieved': flops / (call_ms / 1e3) / 1e12, 'peak': PEAK_BF16 / 1e12,
                      'unit': 'TFLOP/s', 'frac': flops / (call_ms / 1e3) / PEAK_BF16, 'traffic': None,
                      'kernel': 'one chain_chunk call (start + 8 blocks + head)', 'flops_per_call': flops,
@@ -273,6 +293,8 @@ def main():
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
     ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
     ap.add_argument('--probe-chain', action='store_true', help='bench chain_chunk (own JSON line)')
+    ap.add_argument('--own', choices=['none', 'routed'], default='none',
+                    help='--probe-chain: every attention held, or the routed own-query moves')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
@@ -289,7 +311,7 @@ def main():
         bench_probe_cycle(max(args.steps, 5), args.warmup, args.no_cpu)
         return
     if args.probe_chain:
-        bench_probe_chain(max(args.steps, 5), args.warmup)
+        bench_probe_chain(max(args.steps, 5), args.warmup, own=args.own == 'routed')
         return
 
     import noise_amd

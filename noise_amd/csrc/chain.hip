@@ -235,6 +235,12 @@ NOISE_DEV void split3(uint16_t* o, int64_t W, int64_t c, float v, bool a_side) {
   o[2 * W + c] = a_side ? hi : lo;
 }
 
+// hi and lo bf16 halves of four floats, packed for one 8-byte store each.
+NOISE_DEV void split4(float4 v, uint2& hi, uint2& lo) {
+  hi = make_uint2(pack_bf2(v.x, v.y), pack_bf2(v.z, v.w));
+  lo = make_uint2(pack_bf2(v.x - bf_lo(hi.x), v.y - bf_hi(hi.x)), pack_bf2(v.z - bf_lo(hi.y), v.w - bf_hi(hi.y)));
+}
+
 // B3 rows of an fp32 weight read as B[n][k] = w[n * s_n + k * s_k] (N = K = W).
 __global__ __launch_bounds__(256) void chain_split_weight_kernel(const float* __restrict__ w, int64_t s_n,
                                                                  int64_t s_k, int W, uint16_t* __restrict__ out) {
@@ -292,10 +298,12 @@ __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict_
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
       const int c = 4 * lane + 256 * t;
-      split3(o, W, c + 0, d[t].x * a + xv[t].x * b, true);
-      split3(o, W, c + 1, d[t].y * a + xv[t].y * b, true);
-      split3(o, W, c + 2, d[t].z * a + xv[t].z * b, true);
-      split3(o, W, c + 3, d[t].w * a + xv[t].w * b, true);
+      uint2 hi, lo;
+      split4(make_float4(d[t].x * a + xv[t].x * b, d[t].y * a + xv[t].y * b, d[t].z * a + xv[t].z * b,
+                         d[t].w * a + xv[t].w * b), hi, lo);
+      *reinterpret_cast<uint2*>(o + c) = hi;
+      *reinterpret_cast<uint2*>(o + W + c) = lo;
+      *reinterpret_cast<uint2*>(o + 2 * W + c) = hi;
     }
 }
 
@@ -468,14 +476,34 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
   }
   const float r_0 = rs[fr], r_1 = rs[32 + fr];
   const float nan = __builtin_nanf("");
+  __syncthreads();  // every wave is done with kt and vt: they take the lo halves
+  uint16_t* hi_t = at[wave];
+  uint16_t* lo_t = (wave < 2 ? kt : vt) + (wave & 1) * 32 * QLD;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const int p = pw + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    if (p >= g.P) continue;
+    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
     const float em = expm1f(-dl[j]);
-    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64;
-    split3(o, g.W, fr, pos_ok ? bf2f(f2bf(acc[0][j])) + em * r_0 : nan, true);
-    split3(o, g.W, 32 + fr, pos_ok ? bf2f(f2bf(acc[1][j])) + em * r_1 : nan, true);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const float v = pos_ok ? bf2f(f2bf(acc[ni][j])) + em * (ni ? r_1 : r_0) : nan;
+      const uint16_t hv = f2bf(v);
+      hi_t[row * QLD + ni * 32 + fr] = hv;
+      lo_t[row * QLD + ni * 32 + fr] = f2bf(v - bf2f(hv));
+    }
+  }
+  __syncthreads();
+  // 16-byte stores: lane l moves chunk l % 8 of rows l / 8 + 8 t, into A3's hi, lo, hi segments
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
+    const int p = pw + row;
+    if (p >= g.P) continue;
+    const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
+    const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
+    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
+    *reinterpret_cast<uint4*>(o) = hv;
+    *reinterpret_cast<uint4*>(o + g.W) = lv;
+    *reinterpret_cast<uint4*>(o + 2 * g.W) = hv;
   }
 }
 
