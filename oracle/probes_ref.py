@@ -3,7 +3,7 @@
 Only tests/ and bench.py's `cpu_baseline` leg may import this module, and only as the checker.
 The shipped path (noise_amd/probes.py over libnoise_amd) never calls it.
 
-Restatements in numpy float64 (float32 when asked) of five functions of the reference trainer:
+Restatements in numpy float64 (float32 when asked) of six functions of the reference trainer:
 
 * `coordinate_differences` -- train/val/run.py:100-111 (train/speedrun/run.py:57-68): central
   differences of each token's soft-capped cross-entropy along each of its own logits, in the
@@ -15,9 +15,10 @@ Restatements in numpy float64 (float32 when asked) of five functions of the refe
   direction set;
 * `query_change_routed`    -- train/val/run.py:284-304: a token's attention output change when its
   own query moves and only its top keys' logits move;
-* `chain_chunk`            -- train/val/run.py:307-351 with own = None or ('routed', ...): moves
-  of one site carried through the later blocks' routed MLPs (and own-query attention changes) to
-  the head's loss.
+* `query_change`           -- train/val/run.py:256-281: the same over every key of its window;
+* `chain_chunk`            -- train/val/run.py:307-351 with own = None, ('routed', ...) or
+  ('window', ...): moves of one site carried through the later blocks' routed MLPs (and
+  own-query attention changes) to the head's loss.
 
 cap(v) = 15 tanh(v / 15); norm(x) = x rsqrt(|x|^2 / width + eps), eps = float32 machine epsilon.
 
@@ -134,6 +135,49 @@ def norm_difference(x, delta, width=512):
     return delta * inv[..., None] + x[:, None, :] * (inv - inv0)[..., None]
 
 
+def _query_moves(x, delta, pos, w_q, cos, sin, heads, d, width, tf):
+    """Clean rotated query r0 (m, 1, h, d) and its change dr (m, P, h, d), inv0, inv (qk-norm)."""
+    m, P, _ = delta.shape
+    c, s_ = cos[pos][:, None, None, :], sin[pos][:, None, None, :]
+    rot = lambda u: np.concatenate([u[..., :d // 2] * c + u[..., d // 2:] * s_,
+                                    u[..., :d // 2] * -s_ + u[..., d // 2:] * c], -1)
+    r0 = rot((tf(_rms(x, width)) @ tf(w_q).T).reshape(m, 1, heads, d))
+    dr = rot((tf(norm_difference(x, delta, width)) @ tf(w_q).T).reshape(m, P, heads, d))
+    sq = np.sum(r0 * r0, -1, keepdims=True)
+    inv0 = 1.0 / np.sqrt(sq / d + EPS32)
+    inv = 1.0 / np.sqrt((sq + 2 * np.sum(r0 * dr, -1, keepdims=True) + np.sum(dr * dr, -1, keepdims=True)) / d + EPS32)
+    return r0, dr, inv0, inv
+
+
+def query_change(x, delta, pos, rel, w_q, keys, values, w_proj_t, cos, sin, window, width=512, policy='fp64'):
+    """train/val/run.py:256-281: the change of each token's attention output, through the output
+    projection, when only its own query moves, over every key of its window. keys, values
+    (h, S, d) clean (keys rotated and normed) shared by the chunk's tokens; rel (m,) the tokens'
+    positions within those S; a key t is allowed when 0 <= rel - t <= window. Policies as
+    query_change_routed."""
+    dt = np.float32 if policy == 'build32' else np.float64
+    rb = (lambda v: _bf16(v).astype(dt)) if policy in ('build', 'build32', 'tf32') else (lambda v: v)
+    tf = _tf32 if policy == 'tf32' else (lambda v: v)
+    f = lambda v: np.asarray(v, dt)
+    x, delta, w_q, keys, vals, w_proj_t, cos, sin = map(f, (x, delta, w_q, keys, values, w_proj_t, cos, sin))
+    pos, rel = np.asarray(pos), np.asarray(rel)
+    m, P, _ = delta.shape
+    heads, S, d = keys.shape
+    r0, dr, inv0, inv = _query_moves(x, delta, pos, w_q, cos, sin, heads, d, width, tf)
+    q0, dq = r0 * inv0, dr * inv + r0 * (inv - inv0)
+    lag = rel[:, None] - np.arange(S)[None]
+    allowed = ((lag >= 0) & (lag <= window))[:, None, None, :]               # (m, 1, 1, S)
+    scores = rb(np.einsum('mphd,htd->mpht', rb(q0), keys)) * d ** -0.5
+    scores = np.where(allowed, scores, -np.inf)
+    mx = np.max(scores, -1, keepdims=True)
+    e = np.exp(scores - mx)
+    p0 = e / np.sum(e, -1, keepdims=True)                                      # (m, 1, h, S)
+    ds = rb(np.einsum('mphd,htd->mpht', rb(dq), keys)) * d ** -0.5
+    dlse = np.log1p(np.sum(p0 * np.expm1(ds), -1, keepdims=True))
+    dout = rb(np.einsum('mpht,htd->mphd', rb(p0 * np.expm1(ds - dlse)), vals))
+    return tf(dout.reshape(m, P, heads * d)) @ tf(w_proj_t)
+
+
 def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos, sin, width=512,
                         policy='fp64'):
     """train/val/run.py:282-304: the change of each token's attention output, through the output
@@ -172,10 +216,11 @@ def query_change_routed(x, delta, pos, w_q, top_keys, top_values, top_p, rest, w
 
 def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t,
                 base, target_logit_w, y, own=None, width=512, policy='fp64'):
-    """train/val/run.py:307-351 with own = None (every attention held) or own = ('routed', pos,
+    """train/val/run.py:307-351 with own = None (every attention held), own = ('routed', pos,
     inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, (cos, sin)) (each move also changes
-    its own token's attention through its own query, along its top keys; per-block lists as in
-    the reference): forward differences of each token's loss along every move of one site, each
+    its own token's attention through its own query, along its top keys) or own = ('window', pos,
+    rels, inputs, w_q, keys, values, w_proj_t, cos, sin, windows) (the same over every key of its
+    window; per-block lists as in the reference): forward differences of each token's loss along every move of one site, each
     later MLP restricted to the token's routed units. policy 'fp64': float64 throughout; 'build': float64 with bfloat16 rounding where the
     reference casts (dz, both routed products and their inputs, the head product and its input);
     'build32': the same casts in float32 arithmetic, so |build - build32| shows how far the casts
@@ -198,10 +243,16 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
         if b > first:
             delta = lam_r[b] * delta + (lam_0[b] * dx0 if dx0 is not None else 0)
         if own is not None and (site < 0 or b > first):
-            assert own[0] == 'routed', 'only the routed own-query variant is restated'
-            _, pos, inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos_sin = own
-            delta = delta + query_change_routed(inputs[b], delta, pos, w_q[b], top_keys[b], top_values[b], top_p[b],
-                                                rest[b], w_proj_t[b], cos_sin[0], cos_sin[1], width, policy)
+            if own[0] == 'routed':
+                _, pos, inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, cos_sin = own
+                delta = delta + query_change_routed(inputs[b], delta, pos, w_q[b], top_keys[b], top_values[b],
+                                                    top_p[b], rest[b], w_proj_t[b], cos_sin[0], cos_sin[1], width,
+                                                    policy)
+            else:
+                assert own[0] == 'window'
+                _, pos, rels, inputs, w_q, keys, values, w_proj_t, cos, sin, windows = own
+                delta = delta + query_change(inputs[b], delta, pos, rels[b], w_q[b], keys[b], values[b],
+                                             w_proj_t[b], cos, sin, windows[b], width, policy)
         dz = rb(norm_difference(f(mids[b]), delta.astype(dt), width))
         wf = f(w_fc[b])[np.asarray(idx[b])]                      # (m, k, W)
         dh = rb(np.einsum('mpd,mkd->mpk', dz, wf))

@@ -267,3 +267,91 @@ def test_tf32_rounding():
     got = P._tf32(vals)
     np.testing.assert_array_equal(got[:-1], want[:-1])
     assert abs(got[-1] - 1e-30) <= 1e-30 * 2 ** -10
+
+
+def _window_case(m=4, P_=3, W=16, heads=2, S=9, window=4, seed=3, rotary=None):
+    """query_change inputs: one key window of S positions shared by the chunk's tokens (keys
+    rotated and RMS-normed per head), tokens at relative positions rel (one with fewer than
+    window + 1 keys before it), and a brute force over the explicit window softmax."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, dtype=F64)
+    d = W // heads
+    nrm = lambda v, n: v * torch.rsqrt(v.square().sum(-1, keepdim=True) / n + EPS)
+    x, w_q, w_proj_t = rn(m, W) * 2, rn(W, W) / W ** 0.5, rn(W, W) / W ** 0.5
+    if rotary is None:
+        T = 20
+        ang = rn(T, d // 2)
+        pos, cos, sin = torch.randint(0, T, (m,), generator=g), ang.cos(), ang.sin()
+    else:
+        pos, cos, sin = rotary
+    keys, vals = nrm(rn(heads, S, d), d), rn(heads, S, d)
+    rel = torch.tensor([S - 1, 2, S - 3, window][:m] + [S - 1] * max(0, m - 4))
+
+    def query(xx, i):
+        r = (nrm(xx, W) @ w_q.T).view(heads, d)
+        return nrm(torch.cat([r[:, :d // 2] * cos[pos[i]] + r[:, d // 2:] * sin[pos[i]],
+                              r[:, :d // 2] * -sin[pos[i]] + r[:, d // 2:] * cos[pos[i]]], -1), d)
+
+    def brute(i, D):
+        allowed = [t for t in range(S) if 0 <= int(rel[i]) - t <= window]
+        kk, vv = keys[:, allowed], vals[:, allowed]
+        out = lambda q: torch.einsum('hs,hsd->hd', torch.softmax(torch.einsum('hd,hsd->hs', q, kk) * d ** -0.5, -1), vv)
+        return (out(query(x[i] + D, i)) - out(query(x[i], i))).reshape(-1) @ w_proj_t
+    case = dict(pos=pos, rel=rel, w_q=w_q, keys=keys, values=vals, w_proj_t=w_proj_t, cos=cos, sin=sin, window=window)
+    return x, case, brute
+
+
+def test_query_change_brute_force():
+    """query_change (train/val/run.py:256-281) against the moved query's explicit softmax over the
+    token's window (lag 0..window, inclusive), every logit in it moving."""
+    m, P_, W = 4, 3, 16
+    x, c, brute = _window_case(m, P_, W)
+    g = torch.Generator().manual_seed(2)
+    delta = torch.randn(m, P_, W, generator=g, dtype=F64) * 0.3
+    got = P.query_change(x, delta, width=W, **c)
+    want = torch.stack([torch.stack([brute(i, delta[i, p]) for p in range(P_)]) for i in range(m)])
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize('site', [-1, 0])
+def test_chain_chunk_window_brute_force(site):
+    """chain_chunk with own = ('window', ...) (train/val/run.py:332-335) against explicit moved
+    streams with the window attention change before every later MLP."""
+    d, nrm, weight = _chain_inputs(site)
+    m, P_, W = d['move'].shape
+    L = len(d['mids'])
+    g = torch.Generator().manual_seed(11)
+    T, dh = 20, W // 2
+    ang = torch.randn(T, dh // 2, generator=g, dtype=F64)
+    rotary = (torch.randint(0, T, (m,), generator=g), ang.cos(), ang.sin())
+    blocks = [_window_case(m, P_, W, heads=2, S=8 + b, window=3 + 2 * b, seed=30 + b, rotary=rotary)
+              for b in range(L)]
+    own = ('window', rotary[0], [bl[1]['rel'] for bl in blocks], [bl[0] for bl in blocks],
+           [bl[1]['w_q'] for bl in blocks], [bl[1]['keys'] for bl in blocks], [bl[1]['values'] for bl in blocks],
+           [bl[1]['w_proj_t'] for bl in blocks], rotary[1], rotary[2], [bl[1]['window'] for bl in blocks])
+    ce = lambda x, yy: F.cross_entropy(15 * torch.tanh(nrm(x) @ weight.T / 15), yy.clamp(min=0), reduction='none')
+    want = torch.zeros(m, P_, dtype=F64)
+    for i in range(m):
+        if d['y'][i] < 0:
+            continue
+        clean = ce(d['xL'][i:i + 1], d['y'][i:i + 1])
+        for p in range(P_):
+            if site < 0:
+                dx0 = nrm(d['e'][i] + d['move'][i, p]) - d['x0'][i]
+                D, first = (d['lam_r'][0] + d['lam_0'][0]) * dx0, 0
+            else:
+                D, first = d['move'][i, p], site
+            for b in range(first, L):
+                if b > first:
+                    D = d['lam_r'][b] * D + (d['lam_0'][b] * dx0 if site < 0 else 0)
+                if site < 0 or b > first:
+                    D = D + blocks[b][2](i, D)
+                rows = d['idx'][b][i]
+                hp = d['w_fc'][b][rows] @ nrm(d['mids'][b][i] + D)
+                h = d['hs'][b][i]
+                D = D + (torch.relu(hp).square() - torch.relu(h).square()) @ d['w_out_t'][b][rows]
+            want[i, p] = (ce(d['xL'][i:i + 1] + D, d['y'][i:i + 1]) - clean)[0] / d['scale'][i, p]
+    got = P.chain_chunk(site, **d, own=own, width=W)
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-9, atol=1e-11)
+    none = P.chain_chunk(site, **d, width=W)
+    assert np.abs(got - none)[[0, 2]].max() > 1e-3 * np.abs(none).max()
