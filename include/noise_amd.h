@@ -305,6 +305,32 @@ typedef struct {
 int noise_chain_query(const noise_chain_query_t* args, void* stream);
 
 typedef struct {
+  float* delta;            /* [m * P, W] moves at the block's input, updated in place */
+  const float* dx0;        /* NULL, or [m * P, W] moves of x0 (site < 0) */
+  int mix;                 /* first delta = lam_r delta + lam_0 dx0 (then call noise_chain_block with mix 0) */
+  float lam_r, lam_0;
+  const float* x;          /* [m, W] the block's clean input stream */
+  const int64_t* pos;      /* [m] positions, in [0, T) (else NaN) */
+  const int64_t* rel;      /* [m] the same positions within the key window (no allowed key: NaN) */
+  const float* w_q;        /* [W, W] fp32 c_q.weight */
+  const uint16_t* keys;    /* [heads, S, 64] bf16 rotated, normed keys of the chunk's key window */
+  const uint16_t* values;  /* [heads, S, 64] bf16 values */
+  const float* w_proj_t;   /* [W, W] fp32 c_proj.weight transposed */
+  const float* cos_t;      /* [T, 32] rotary tables */
+  const float* sin_t;
+  int T, m, P, W, heads, S, window; /* W = 64 heads, W % 256 == 0, W <= 2048, 0 <= window < 4096 */
+  uint16_t* a3;            /* workspaces as in noise_chain_query_t */
+  float* dr;
+  uint16_t* wq3;
+  uint16_t* wp3;
+} noise_chain_query_window_t;
+
+/* The own-query step with own = ('window', ...) (run.py:256-281 and 332-335): as
+ * noise_chain_query, over every key t of the token's window (0 <= rel - t <= window) with the
+ * clean softmax p0 computed per token. Replaces query_change. */
+int noise_chain_query_window(const noise_chain_query_window_t* args, void* stream);
+
+typedef struct {
   const float* delta;      /* [m * P, W] */
   const float* xL;         /* [m, W] clean top stream */
   const float* base;       /* [m, ld_base] xL W^T */

@@ -71,6 +71,13 @@ class ChainQuery(C.Structure):
                 ('K', INT), ('a3', P), ('dr', P), ('wq3', P), ('wp3', P)]
 
 
+class ChainQueryWindow(C.Structure):
+    _fields_ = [('delta', P), ('dx0', P), ('mix', INT), ('lam_r', F32), ('lam_0', F32), ('x', P), ('pos', P),
+                ('rel', P), ('w_q', P), ('keys', P), ('values', P), ('w_proj_t', P), ('cos_t', P), ('sin_t', P),
+                ('T', INT), ('m', INT), ('P', INT), ('W', INT), ('heads', INT), ('S', INT), ('window', INT),
+                ('a3', P), ('dr', P), ('wq3', P), ('wp3', P)]
+
+
 class ChainHead(C.Structure):
     _fields_ = [('delta', P), ('xL', P), ('base', P), ('ld_base', I64), ('weight', P), ('target_w', P),
                 ('y', P), ('scale', P), ('ld_scale', I64), ('m', INT), ('P', INT), ('W', INT), ('V', INT),
@@ -99,6 +106,7 @@ SIGNATURES = {
     'noise_chain_block': [C.POINTER(ChainBlock), P],
     'noise_chain_head': [C.POINTER(ChainHead), P],
     'noise_chain_query': [C.POINTER(ChainQuery), P],
+    'noise_chain_query_window': [C.POINTER(ChainQueryWindow), P],
 }
 
 _lib = None

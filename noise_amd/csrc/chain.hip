@@ -507,6 +507,275 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
   }
 }
 
+struct ChainQueryWin {
+  const float* dr;       // [m P + m, W] query products: moves' changes, then the clean rows
+  const int64_t* pos;    // [m]
+  const int64_t* rel;    // [m] positions within the key window
+  const float* cos_t;    // [T, 32]
+  const float* sin_t;
+  const uint16_t* keys;  // [heads, S, 64]
+  const uint16_t* vals;  // [heads, S, 64]
+  int T, m, P, W, heads, S, window;
+  uint16_t* a3;          // out [m P, 3 W]
+};
+
+constexpr int QWMAX = 4096;  // keys of one token's window (clean probabilities held in LDS)
+
+NOISE_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Loads keys [k0, k0 + 64) of the window (rows past `n` as zeros) into kt and, when vt is given,
+// the values transposed into vt.
+NOISE_DEV void load_key_block(const uint16_t* keys, const uint16_t* vals, int64_t base, int k0, int n,
+                              uint16_t* kt, uint16_t* vt) {
+  for (int e = threadIdx.x; e < 64 * 8; e += 256) {
+    const int k = e >> 3, c = (e & 7) * 8;
+    const bool ok = k0 + k < n;
+    const int64_t o = base + (int64_t)(k0 + k) * 64 + c;
+    *reinterpret_cast<uint4*>(kt + k * QLD + c) =
+        ok ? *reinterpret_cast<const uint4*>(keys + o) : make_uint4(0u, 0u, 0u, 0u);
+    if (vt) {
+      const uint4 vv = ok ? *reinterpret_cast<const uint4*>(vals + o) : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vt[(c + 2 * j) * QLD + k] = (uint16_t)(w4[j] & 0xffffu);
+        vt[(c + 2 * j + 1) * QLD + k] = (uint16_t)(w4[j] >> 16);
+      }
+    }
+  }
+}
+
+// Workgroup (row tile, head h, token i), four waves of 32 moves each, over the n keys t with
+// 0 <= rel_i - t <= window (train/val/run.py:264-281):
+//   q0 = bf16(r0 inv0); p0 = softmax over the window of bf16(q0 K^T) / 8   (per token, on VALU)
+//   dq as in the routed step; pass 1 over 64-key blocks: dlse = log1p(sum_t p0 expm1(ds_t)),
+//   ds = bf16(dq K^T) / 8 (MFMA); pass 2 recomputes ds and accumulates bf16(w) V with
+//   w = p0 expm1(ds - dlse); dout = bf16(sum) written as A3 of the output projection's product.
+// A position outside [0, T) or a window with no key gives NaN.
+__global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQueryWin g) {
+  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * QLD];
+  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];
+  __shared__ float p0s[QWMAX];
+  __shared__ float r0s[64], cs[32], sn[32], dls[4][32], red[8], inv0s;
+  __shared__ __attribute__((aligned(16))) uint16_t q0s[64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = blockIdx.z, h = blockIdx.y;
+  const int pw = blockIdx.x * 128 + wave * 32;
+  const int64_t pos = g.pos[i], rl = g.rel[i];
+  const int64_t lo64 = rl - g.window > 0 ? rl - g.window : 0;
+  const int64_t hi64 = rl < g.S - 1 ? rl : g.S - 1;
+  const int n = hi64 >= lo64 ? (int)(hi64 - lo64 + 1) : 0;  // <= window + 1 <= QWMAX
+  const bool ok = pos >= 0 && pos < g.T && n > 0;
+  const int64_t pc = ok ? pos : 0;
+  const int64_t kbase = ((int64_t)h * g.S + (n > 0 ? lo64 : 0)) * 64;
+  if (tid < 32) {
+    cs[tid] = g.cos_t[pc * 32 + tid];
+    sn[tid] = g.sin_t[pc * 32 + tid];
+  }
+  __syncthreads();
+  if (tid < 64) {  // the clean rotated query of this head, inv0 and q0 = bf16(r0 inv0)
+    const float* cr = g.dr + ((int64_t)g.m * g.P + i) * g.W + h * 64;
+    const int c = tid & 31;
+    const float u1 = cr[c], u2 = cr[c + 32];
+    const float v = tid < 32 ? u1 * cs[c] + u2 * sn[c] : -u1 * sn[c] + u2 * cs[c];
+    r0s[tid] = v;
+    const float sq = wave_sum(v * v);
+    q0s[tid] = f2bf(v * rsqrtf(sq / 64.f + CAP_EPS32));
+    if (tid == 0) inv0s = sq;
+  }
+  __syncthreads();
+  // clean scores of the window, then its softmax
+  float mx = -INFINITY;
+  for (int t = tid; t < n; t += 256) {
+    const uint16_t* kr = g.keys + kbase + (int64_t)t * 64;
+    float sc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 64; c += 8) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(kr + c);
+      const uint4 qv = *reinterpret_cast<const uint4*>(q0s + c);
+      sc += bf_lo(qv.x) * bf_lo(kv.x) + bf_hi(qv.x) * bf_hi(kv.x) + bf_lo(qv.y) * bf_lo(kv.y) +
+            bf_hi(qv.y) * bf_hi(kv.y) + bf_lo(qv.z) * bf_lo(kv.z) + bf_hi(qv.z) * bf_hi(kv.z) +
+            bf_lo(qv.w) * bf_lo(kv.w) + bf_hi(qv.w) * bf_hi(kv.w);
+    }
+    sc = bf2f(f2bf(sc)) * 0.125f;
+    p0s[t] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float z = 0.f;
+  for (int t = tid; t < n; t += 256) {
+    const float e = expf(p0s[t] - mx);
+    p0s[t] = e;
+    z += e;
+  }
+  z = wave_sum(z);
+  if (lane == 0) red[4 + wave] = z;
+  __syncthreads();
+  z = (red[4] + red[5]) + (red[6] + red[7]);
+  for (int t = tid; t < n; t += 256) p0s[t] = p0s[t] / z;
+  const float sq = inv0s, inv0 = rsqrtf(sq / 64.f + CAP_EPS32);
+
+  // dq: lanes 2 q and 2 q + 1 hold move q's dims c, c + 32 for c in [0, 16) and [16, 32)
+  {
+    const int q = lane >> 1, c0 = (lane & 1) * 16;
+    const int p = min(pw + q, g.P - 1);
+    const float* src = g.dr + ((int64_t)i * g.P + p) * g.W + h * 64;
+    float u1[16], u2[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4 a = ld4(src + c0 + 4 * t), b = ld4(src + 32 + c0 + 4 * t);
+      u1[4 * t] = a.x; u1[4 * t + 1] = a.y; u1[4 * t + 2] = a.z; u1[4 * t + 3] = a.w;
+      u2[4 * t] = b.x; u2[4 * t + 1] = b.y; u2[4 * t + 2] = b.z; u2[4 * t + 3] = b.w;
+    }
+    float dot = 0.f, dsq = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int c = c0 + t;
+      const float v1 = u1[t] * cs[c] + u2[t] * sn[c], v2 = -u1[t] * sn[c] + u2[t] * cs[c];
+      u1[t] = v1;
+      u2[t] = v2;
+      dot += r0s[c] * v1 + r0s[c + 32] * v2;
+      dsq += v1 * v1 + v2 * v2;
+    }
+    dot += noise::dpp_row<0xB1>(dot);
+    dsq += noise::dpp_row<0xB1>(dsq);
+    const float inv = rsqrtf((sq + 2.f * dot + dsq) / 64.f + CAP_EPS32), dinv = inv - inv0;
+    uint16_t* dst = at[wave] + q * QLD;
+#pragma unroll
+    for (int t = 0; t < 16; t += 8) {
+      uint4 w1, w2;
+      uint32_t* p1 = reinterpret_cast<uint32_t*>(&w1);
+      uint32_t* p2 = reinterpret_cast<uint32_t*>(&w2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int a = t + 2 * j, c = c0 + a;
+        p1[j] = pack_bf2(u1[a] * inv + r0s[c] * dinv, u1[a + 1] * inv + r0s[c + 1] * dinv);
+        p2[j] = pack_bf2(u2[a] * inv + r0s[c + 32] * dinv, u2[a + 1] * inv + r0s[c + 33] * dinv);
+      }
+      *reinterpret_cast<uint4*>(dst + c0 + t) = w1;
+      *reinterpret_cast<uint4*>(dst + 32 + c0 + t) = w2;
+    }
+  }
+  __syncthreads();  // dq tiles and p0 complete
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  bf16x8 aq[4];  // this wave's dq fragments, held for both passes
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) aq[ks] = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+
+  // pass 1: sum_t p0 expm1(ds_t) per move
+  float es[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) es[j] = 0.f;
+  for (int k0 = 0; k0 < n; k0 += 64) {
+    __syncthreads();
+    load_key_block(g.keys, g.vals, kbase, k0, n, kt, nullptr);
+    __syncthreads();
+    floatx16 acc[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[ks], b, acc[ni], 0, 0, 0);
+      }
+    const float p_0 = k0 + fr < n ? p0s[k0 + fr] : 0.f, p_1 = k0 + 32 + fr < n ? p0s[k0 + 32 + fr] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      es[j] += p_0 * expm1f(bf2f(f2bf(acc[0][j])) * 0.125f) + p_1 * expm1f(bf2f(f2bf(acc[1][j])) * 0.125f);
+  }
+  {
+    const float tot = noise::halfwave_transpose_sum16(es, lane);
+    const int jj = fr >> 1;
+    if ((lane & 1) == 0) dls[wave][8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3)] = log1pf(tot);
+  }
+  __syncthreads();
+  float dl[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) dl[j] = dls[wave][8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
+
+  // pass 2: dout = sum over blocks of bf16(p0 expm1(ds - dlse)) V
+  floatx16 out[2];
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) out[ni][j] = 0.f;
+  for (int k0 = 0; k0 < n; k0 += 64) {
+    __syncthreads();
+    load_key_block(g.keys, g.vals, kbase, k0, n, kt, vt);
+    __syncthreads();
+    floatx16 acc[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[ks], b, acc[ni], 0, 0, 0);
+      }
+    const float p_0 = k0 + fr < n ? p0s[k0 + fr] : 0.f, p_1 = k0 + 32 + fr < n ? p0s[k0 + 32 + fr] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+      at[wave][row * QLD + fr] = f2bf(p_0 * expm1f(bf2f(f2bf(acc[0][j])) * 0.125f - dl[j]));
+      at[wave][row * QLD + 32 + fr] = f2bf(p_1 * expm1f(bf2f(f2bf(acc[1][j])) * 0.125f - dl[j]));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(vt + (ni * 32 + fr) * QLD + 16 * ks + fk);
+        out[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, out[ni], 0, 0, 0);
+      }
+    }
+  }
+  const float nan = __builtin_nanf("");
+  __syncthreads();  // kt, vt and the w tiles are free: hi halves in at, lo halves in kt / vt
+  uint16_t* hi_t = at[wave];
+  uint16_t* lo_t = (wave < 2 ? kt : vt) + (wave & 1) * 32 * QLD;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const float v = ok ? bf2f(f2bf(out[ni][j])) : nan;
+      const uint16_t hv = f2bf(v);
+      hi_t[row * QLD + ni * 32 + fr] = hv;
+      lo_t[row * QLD + ni * 32 + fr] = f2bf(v - bf2f(hv));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
+    const int p = pw + row;
+    if (p >= g.P) continue;
+    const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
+    const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
+    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
+    *reinterpret_cast<uint4*>(o) = hv;
+    *reinterpret_cast<uint4*>(o + g.W) = lv;
+    *reinterpret_cast<uint4*>(o + 2 * g.W) = hv;
+  }
+}
+
 // ---------------------------------------------------------------- head
 
 // Per row: inv = rsqrt((|xL|^2 + 2 xL.delta + |delta|^2) / W + eps), zy = (base_y + delta.tw) inv
@@ -699,6 +968,46 @@ extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
   return noise::check_launch("chain_block");
 }
 
+namespace {
+
+// The parts of an own-query step around its attention kernel: the weights' hi/lo triples, the
+// mix and A3 rows (moves, then the m clean rows), and dr = A3 W_q3^T.
+int query_products(float* delta, const float* dx0, int mix, float lam_r, float lam_0, const float* x,
+                   const float* w_q, const float* w_proj_t, int m, int P, int W, uint16_t* a3, float* dr,
+                   uint16_t* wq3, uint16_t* wp3, hipStream_t st) {
+  const int64_t rows_all = (int64_t)m * P + m;
+  const unsigned wblocks = (unsigned)(((int64_t)W * W + 255) / 256);
+  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(w_q, W, 1, W, wq3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(w_proj_t, 1, W, W, wp3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  chain_query_pre_kernel<<<(unsigned)((rows_all + 3) / 4), 256, 0, st>>>(delta, dx0, x, m, P, W, mix, lam_r, lam_0,
+                                                                         a3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  ChainGemm g1{a3, wq3, (int)rows_all, W, 3 * W, nullptr, 0, nullptr, dr};
+  chain_gemm_kernel<MODE_STORE, 256><<<dim3((unsigned)((rows_all + 255) / 256), W / 256, 1), 512, 0, st>>>(g1);
+  return noise::check_launch("chain_query");
+}
+
+// delta += dout c_proj^T (fp32), over the moves' rows of A3.
+int query_output(float* delta, const uint16_t* a3, const uint16_t* wp3, int m, int P, int W, hipStream_t st) {
+  const int64_t rows = (int64_t)m * P;
+  ChainGemm g2{a3, wp3, (int)rows, W, 3 * W, nullptr, 0, nullptr, delta};
+  chain_gemm_kernel<MODE_ADD, 256><<<dim3((unsigned)((rows + 255) / 256), W / 256, 1), 512, 0, st>>>(g2);
+  return noise::check_launch("chain_query");
+}
+
+}  // namespace
+
+#define CHAIN_QUERY_COMMON_CHECKS(a, name)                                                                   \
+  NOISE_REQUIRE(a->delta && a->x && a->pos && a->w_q && a->w_proj_t && a->cos_t && a->sin_t && a->a3 &&      \
+                    a->dr && a->wq3 && a->wp3,                                                               \
+                name ": NULL argument");                                                                     \
+  NOISE_REQUIRE(aligned16(a->delta) && (!a->dx0 || aligned16(a->dx0)) && aligned16(a->x) && aligned16(a->dr) && \
+                    aligned16(a->a3) && aligned16(a->wq3) && aligned16(a->wp3),                              \
+                name ": delta, dx0, x and the workspaces must be 16-byte aligned");                          \
+  NOISE_REQUIRE(a->m <= 65535 && (int64_t)a->m * a->P + a->m < (1ll << 31), name ": at most 65535 tokens per call")
+
 extern "C" int noise_chain_query(const noise_chain_query_t* a, void* stream) {
   NOISE_REQUIRE(a, "chain_query: args is NULL");
   NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 256 * MAXT && a->heads > 0 &&
@@ -707,39 +1016,40 @@ extern "C" int noise_chain_query(const noise_chain_query_t* a, void* stream) {
                 "to 2048, 1 <= K <= 64)",
                 a->m, a->P, a->W, a->heads, a->K, a->T);
   if (a->m == 0) return NOISE_OK;
-  NOISE_REQUIRE(a->delta && a->x && a->pos && a->w_q && a->top_keys && a->top_values && a->top_p && a->rest &&
-                    a->w_proj_t && a->cos_t && a->sin_t && a->a3 && a->dr && a->wq3 && a->wp3,
-                "chain_query: NULL argument");
-  NOISE_REQUIRE(aligned16(a->delta) && (!a->dx0 || aligned16(a->dx0)) && aligned16(a->x) && aligned16(a->dr) &&
-                    aligned16(a->a3) && aligned16(a->wq3) && aligned16(a->wp3) && aligned16(a->top_keys) &&
-                    aligned16(a->top_values),
-                "chain_query: delta, dx0, x, keys, values and the workspaces must be 16-byte aligned");
-  NOISE_REQUIRE(a->m <= 65535 && ((int64_t)a->m * a->P + a->m) * 3 * a->W < (1ll << 40) &&
-                    (int64_t)a->m * a->P + a->m < (1ll << 31),
-                "chain_query: at most 65535 tokens per call");
+  NOISE_REQUIRE(a->top_keys && a->top_values && a->top_p && a->rest, "chain_query: NULL argument");
+  NOISE_REQUIRE(aligned16(a->top_keys) && aligned16(a->top_values), "chain_query: keys and values must be 16-byte aligned");
+  CHAIN_QUERY_COMMON_CHECKS(a, "chain_query");
   const hipStream_t st = (hipStream_t)stream;
-  const int W = a->W;
-  const int64_t rows = (int64_t)a->m * a->P, rows_all = rows + a->m;
-  const unsigned wblocks = (unsigned)(((int64_t)W * W + 255) / 256);
-  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(a->w_q, W, 1, W, a->wq3);
-  if (int e = noise::check_launch("chain_query")) return e;
-  chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(a->w_proj_t, 1, W, W, a->wp3);
-  if (int e = noise::check_launch("chain_query")) return e;
-  chain_query_pre_kernel<<<(unsigned)((rows_all + 3) / 4), 256, 0, st>>>(a->delta, a->dx0, a->x, a->m, a->P, W,
-                                                                         a->mix, a->lam_r, a->lam_0, a->a3);
-  if (int e = noise::check_launch("chain_query")) return e;
-  // query products of every move and of the clean rows: dr = A3 Wq3^T (fp32)
-  ChainGemm g1{a->a3, a->wq3, (int)rows_all, W, 3 * W, nullptr, 0, nullptr, a->dr};
-  chain_gemm_kernel<MODE_STORE, 256><<<dim3((unsigned)((rows_all + 255) / 256), W / 256, 1), 512, 0, st>>>(g1);
-  if (int e = noise::check_launch("chain_query")) return e;
+  if (int e = query_products(a->delta, a->dx0, a->mix, a->lam_r, a->lam_0, a->x, a->w_q, a->w_proj_t, a->m, a->P,
+                             a->W, a->a3, a->dr, a->wq3, a->wp3, st))
+    return e;
   ChainQuery q{a->dr, a->pos, a->cos_t, a->sin_t, a->top_keys, a->top_values, a->top_p, a->rest,
-               a->T, a->m, a->P, W, a->heads, a->K, a->a3};
+               a->T, a->m, a->P, a->W, a->heads, a->K, a->a3};
   chain_query_attn_kernel<<<dim3((unsigned)((a->P + 127) / 128), a->heads, a->m), 256, 0, st>>>(q);
   if (int e = noise::check_launch("chain_query")) return e;
-  // delta += dout c_proj^T (fp32), over the moves' rows of A3
-  ChainGemm g2{a->a3, a->wp3, (int)rows, W, 3 * W, nullptr, 0, nullptr, a->delta};
-  chain_gemm_kernel<MODE_ADD, 256><<<dim3((unsigned)((rows + 255) / 256), W / 256, 1), 512, 0, st>>>(g2);
-  return noise::check_launch("chain_query");
+  return query_output(a->delta, a->a3, a->wp3, a->m, a->P, a->W, st);
+}
+
+extern "C" int noise_chain_query_window(const noise_chain_query_window_t* a, void* stream) {
+  NOISE_REQUIRE(a, "chain_query_window: args is NULL");
+  NOISE_REQUIRE(a->m >= 0 && a->P > 0 && a->W > 0 && a->W % 256 == 0 && a->W <= 256 * MAXT && a->heads > 0 &&
+                    a->W == 64 * a->heads && a->S > 0 && a->window >= 0 && a->window < QWMAX && a->T > 0,
+                "chain_query_window: bad sizes (m=%d P=%d W=%d heads=%d S=%d window=%d T=%d; W = 64 heads, a "
+                "multiple of 256 up to 2048, 0 <= window < %d)",
+                a->m, a->P, a->W, a->heads, a->S, a->window, a->T, QWMAX);
+  if (a->m == 0) return NOISE_OK;
+  NOISE_REQUIRE(a->rel && a->keys && a->values, "chain_query_window: NULL argument");
+  NOISE_REQUIRE(aligned16(a->keys) && aligned16(a->values), "chain_query_window: keys and values must be 16-byte aligned");
+  CHAIN_QUERY_COMMON_CHECKS(a, "chain_query_window");
+  const hipStream_t st = (hipStream_t)stream;
+  if (int e = query_products(a->delta, a->dx0, a->mix, a->lam_r, a->lam_0, a->x, a->w_q, a->w_proj_t, a->m, a->P,
+                             a->W, a->a3, a->dr, a->wq3, a->wp3, st))
+    return e;
+  ChainQueryWin q{a->dr, a->pos, a->rel, a->cos_t, a->sin_t, a->keys, a->values,
+                  a->T, a->m, a->P, a->W, a->heads, a->S, a->window, a->a3};
+  chain_query_window_kernel<<<dim3((unsigned)((a->P + 127) / 128), a->heads, a->m), 256, 0, st>>>(q);
+  if (int e = noise::check_launch("chain_query_window")) return e;
+  return query_output(a->delta, a->a3, a->wp3, a->m, a->P, a->W, st);
 }
 
 extern "C" int noise_chain_head(const noise_chain_head_t* a, void* stream) {

@@ -8,9 +8,9 @@ float32 results (device tensors in, device tensors out, asynchronous on the curr
 * `row_derivatives(base, C, rows, y, steps, sq, dots, dir_sq)`   -- train/val/run.py:170-183
 * `chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t,
   weight_t, base, target_logit_w, y, own=None)`                   -- train/val/run.py:307-351,
-  with every attention held (own = None) or with the routed own-query moves (own = ('routed', ...),
-  query_change_routed, train/val/run.py:284-304); the key-window variant (own = ('window', ...))
-  is not built here
+  with every attention held (own = None), with the routed own-query moves (own = ('routed', ...),
+  query_change_routed, train/val/run.py:284-304) or over whole key windows (own = ('window', ...),
+  query_change, train/val/run.py:256-281)
 
 The reference reads the stream width from a module constant (WIDTH = 512); here it is the keyword
 `width`. A target y < 0 masks its token (zeros, as the reference's `* (y >= 0)`); a target >= V
@@ -21,7 +21,7 @@ import ctypes as C
 import torch
 
 from . import _lib
-from ._lib import ChainBlock, ChainHead, ChainQuery, Probe
+from ._lib import ChainBlock, ChainHead, ChainQuery, ChainQueryWindow, Probe
 
 WIDTH = 512
 
@@ -150,10 +150,10 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     inputs, w_q, top_keys, top_values, top_p, rest, w_proj_t, (cos, sin)) as the reference's
     strong_keys builds it: pos [m]; per block inputs [m, W], w_q [W, W], top_keys and top_values
     [m, heads, K, 64], top_p [m, heads, K], rest [m, heads, 64], w_proj_t [W, W]; cos, sin
-    [T, 32]. Returns float32 [m, P]."""
-    if own is not None and own[0] != 'routed':
-        raise NotImplementedError(f'chain_chunk: own = {own[0]!r} is not built on libnoise_amd '
-                                  "(own = None and own = ('routed', ...) are)")
+    [T, 32]; or ('window', pos, rels, inputs, w_q, keys, values, w_proj_t, cos, sin, windows) as
+    own_query_window builds it: per block rels [m], keys and values [heads, S, 64], windows (int).
+    Returns float32 [m, P]."""
+    _need(own is None or own[0] in ('routed', 'window'), "own: expected None, ('routed', ...) or ('window', ...)")
     m, P, W = move.shape
     L = len(mids)
     V = weight_t.shape[1]
@@ -186,7 +186,7 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     wf = torch.empty(m, k, W, dtype=torch.bfloat16, device=dev)
     wo = torch.empty(m, W, k, dtype=torch.bfloat16, device=dev)
     g = torch.empty(m * P, k, dtype=torch.bfloat16, device=dev)
-    query = _routed_query(own, m, P, W, L, dev) if own is not None else None
+    query = None if own is None else (_routed_query if own[0] == 'routed' else _window_query)(own, m, P, W, L, dev)
     for b in range(first, L):
         mix = int(b > first)
         if query is not None and (site < 0 or b > first):
@@ -217,6 +217,57 @@ def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc,
     return out
 
 
+def _query_workspaces(m, P, W, dev):
+    return (torch.empty(m * P + m, 3 * W, dtype=torch.bfloat16, device=dev),
+            torch.empty(m * P + m, W, dtype=torch.float32, device=dev),
+            torch.empty(W, 3 * W, dtype=torch.bfloat16, device=dev),
+            torch.empty(W, 3 * W, dtype=torch.bfloat16, device=dev))
+
+
+def _rotary(pos, cos, sin, m):
+    _need(pos.is_cuda and not pos.is_floating_point() and pos.numel() == m, f'own pos: expected {m} device integers')
+    _need(cos.dim() == 2 and cos.shape[1] == 32, f'own cos: expected [T, 32], got {tuple(cos.shape)}')
+    T = cos.shape[0]
+    return (pos.reshape(m).to(torch.int64).contiguous(), _dev_f32(cos, (T, 32), 'own cos'),
+            _dev_f32(sin, (T, 32), 'own sin'), T)
+
+
+def _window_query(own, m, P, W, L, dev):
+    """Checks own = ('window', ...) and returns step(b, delta, dx0, mix, lam_r, lam_0), which runs
+    the block's own-query step over each token's key window (noise_chain_query_window)."""
+    _need(len(own) == 11, "own: expected ('window', pos, rels, inputs, w_q, keys, values, w_proj_t, cos, sin, "
+                          'windows)')
+    _, pos, rels, inputs, w_q, keys, values, w_proj_t, cos, sin, windows = own
+    for name, v in (('rels', rels), ('inputs', inputs), ('w_q', w_q), ('keys', keys), ('values', values),
+                    ('w_proj_t', w_proj_t), ('windows', windows)):
+        _need(len(v) >= L, f'own {name}: one entry per block')
+    _need(W % 64 == 0, f'own: width {W} is not a whole number of 64-wide heads')
+    heads = W // 64
+    ps, ct, st, T = _rotary(pos, cos, sin, m)
+    a3, dr, wq3, wp3 = _query_workspaces(m, P, W, dev)
+
+    def step(b, delta, dx0, mix, lam_r, lam_0):
+        _need(keys[b].dim() == 3 and keys[b].shape[0] == heads and keys[b].shape[2] == 64,
+              f'own keys[{b}]: expected [{heads}, S, 64], got {tuple(keys[b].shape)}')
+        S = keys[b].shape[1]
+        rb = rels[b]
+        _need(rb.is_cuda and not rb.is_floating_point() and rb.numel() == m, f'own rels[{b}]: expected {m} device integers')
+        rr = rb.reshape(m).to(torch.int64).contiguous()
+        x = _dev_f32(inputs[b], (m, W), f'own inputs[{b}]')
+        wq = _dev_f32(w_q[b], (W, W), f'own w_q[{b}]')
+        kk = _dev_bf16(keys[b], (heads, S, 64), f'own keys[{b}]')
+        vv = _dev_bf16(values[b], (heads, S, 64), f'own values[{b}]')
+        wp = _dev_f32(w_proj_t[b], (W, W), f'own w_proj_t[{b}]')
+        a = ChainQueryWindow(delta=delta.data_ptr(), dx0=dx0.data_ptr() if dx0 is not None else None, mix=mix,
+                             lam_r=lam_r, lam_0=lam_0, x=x.data_ptr(), pos=ps.data_ptr(), rel=rr.data_ptr(),
+                             w_q=wq.data_ptr(), keys=kk.data_ptr(), values=vv.data_ptr(), w_proj_t=wp.data_ptr(),
+                             cos_t=ct.data_ptr(), sin_t=st.data_ptr(), T=T, m=m, P=P, W=W, heads=heads, S=S,
+                             window=int(windows[b]), a3=a3.data_ptr(), dr=dr.data_ptr(), wq3=wq3.data_ptr(),
+                             wp3=wp3.data_ptr())
+        _lib.call('noise_chain_query_window', C.byref(a), _stream())
+    return step
+
+
 def _routed_query(own, m, P, W, L, dev):
     """Checks own = ('routed', ...) and returns step(b, delta, dx0, mix, lam_r, lam_0), which runs
     the block's own-query step (noise_chain_query) in place on delta."""
@@ -231,16 +282,8 @@ def _routed_query(own, m, P, W, L, dev):
     _need(top_keys[0].dim() == 4 and tuple(top_keys[0].shape[:2]) == (m, heads) and top_keys[0].shape[3] == 64,
           f'own top_keys: expected [{m}, {heads}, K, 64], got {tuple(top_keys[0].shape)}')
     K = top_keys[0].shape[2]
-    _need(pos.is_cuda and not pos.is_floating_point() and pos.numel() == m, f'own pos: expected {m} device integers')
-    ps = pos.reshape(m).to(torch.int64).contiguous()
-    cos, sin = cos_sin
-    _need(cos.dim() == 2 and cos.shape[1] == 32, f'own cos: expected [T, 32], got {tuple(cos.shape)}')
-    T = cos.shape[0]
-    ct, st = _dev_f32(cos, (T, 32), 'own cos'), _dev_f32(sin, (T, 32), 'own sin')
-    a3 = torch.empty(m * P + m, 3 * W, dtype=torch.bfloat16, device=dev)
-    dr = torch.empty(m * P + m, W, dtype=torch.float32, device=dev)
-    wq3 = torch.empty(W, 3 * W, dtype=torch.bfloat16, device=dev)
-    wp3 = torch.empty_like(wq3)
+    ps, ct, st, T = _rotary(pos, cos_sin[0], cos_sin[1], m)
+    a3, dr, wq3, wp3 = _query_workspaces(m, P, W, dev)
 
     def step(b, delta, dx0, mix, lam_r, lam_0):
         x = _dev_f32(inputs[b], (m, W), f'own inputs[{b}]')

@@ -319,3 +319,109 @@ def test_chain_query_step_matches_oracle(device, m, P_, K):
           f'mean {err.mean():.3e} (tf32 envelope {env.mean():.3e}), max |want| {scale:.3e}')
     assert err.max() <= 2 * env.max()
     assert err.mean() <= 0.5 * env.mean()
+
+
+def _window_own(m, L, S, windows, seed, W=512, T=2048):
+    """own = ('window', ...) at the model's widths: per block one key window of S positions
+    (unit-RMS bf16 keys, bf16 values) shared by the chunk's tokens, at relative positions that
+    cover the window's start (fewer than window + 1 keys), its inclusive bound and its end."""
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g)
+    heads = W // 64
+    ang = torch.arange(T)[:, None].float() * (1.0 / 1024 ** torch.linspace(0, 1, 32))[None]
+    rels, keys, vals = [], [], []
+    for b in range(L):
+        w = windows[b]
+        base = [0, 5, w - 1, w, w + 1, S - 1]
+        rels.append(torch.tensor([max(0, min(S - 1, base[t % len(base)] + t // len(base))) for t in range(m)]))
+        k_ = rn(heads, S, 64)
+        keys.append((k_ * torch.rsqrt(k_.square().mean(-1, keepdim=True))).bfloat16())
+        vals.append(rn(heads, S, 64).bfloat16())
+    pos = rels[0] + (T - S)
+    return ('window', pos, rels, [rn(m, W) * 3 for _ in range(L)], [rn(W, W) / W ** 0.5 for _ in range(L)], keys,
+            vals, [rn(W, W) / W ** 0.5 for _ in range(L)], ang.cos(), ang.sin(), list(windows))
+
+
+def _window_to(own, device=None):
+    """own ('window', ...) moved to a device, or as float64 numpy for the oracle."""
+    conv = (lambda t: t.to(device)) if device is not None else (
+        lambda t: t.double().numpy() if t.is_floating_point() else t.numpy())
+    _, pos, rels, inputs, w_q, keys, vals, w_proj_t, cos, sin, windows = own
+    lst = lambda part: [conv(t) for t in part]
+    return ('window', conv(pos), lst(rels), lst(inputs), lst(w_q), lst(keys), lst(vals), lst(w_proj_t), conv(cos),
+            conv(sin), windows)
+
+
+@pytest.mark.parametrize('m,P_,S,window', [(6, 70, 300, 128), (4, 150, 1100, 1024), (3, 5, 40, 0)])
+def test_chain_query_window_step_matches_oracle(device, m, P_, S, window):
+    """The key-window own-query step alone (noise_chain_query_window, mix off) against query_change
+    with the reference's bf16 casts: windows of 129 and 1025 keys (17 blocks of 64), tokens at the
+    window's start, bound and end. Bar as the routed step: twice the tf32 envelope at its largest,
+    half of it on average. Window 0 (the token's own key only): a softmax over one key cannot
+    change, so the step must add (float32 rounding of) nothing."""
+    own = _window_own(m, 1, S, [window], seed=m * P_ + S)
+    g = torch.Generator().manual_seed(S)
+    delta = torch.randn(m, P_, 512, generator=g) * 0.05
+    dev_delta = delta.reshape(m * P_, 512).to(device)
+    step = _probes()._window_query(_window_to(own, device), m, P_, 512, 1, dev_delta.device)
+    step(0, dev_delta, None, 0, 1.0, 0.0)
+    got = (dev_delta.cpu().double().reshape(m, P_, 512) - delta.double()).numpy()
+    torch.cuda.synchronize()
+    o = _window_to(own)
+    args = (o[3][0], delta.double().numpy(), o[1], o[2][0], o[4][0], o[5][0], o[6][0], o[7][0], o[8], o[9], window)
+    want = P.query_change(*args, policy='build')
+    if window == 0:
+        print(f'window step m {m} P {P_} window 0: max |gpu| {np.abs(got).max():.3e}')
+        assert np.abs(got).max() <= 1e-6
+        return
+    env = np.abs(want - P.query_change(*args, policy='tf32'))
+    err = np.abs(got - want)
+    scale = np.abs(want).max()
+    print(f'window step m {m} P {P_} S {S} window {window}: max |gpu - build| {err.max():.3e} (tf32 envelope '
+          f'{env.max():.3e}), mean {err.mean():.3e} (tf32 envelope {env.mean():.3e}), max |want| {scale:.3e}')
+    assert np.isfinite(got).all()
+    assert err.max() <= 2 * env.max()
+    assert err.mean() <= 0.5 * env.mean()
+
+
+@pytest.mark.parametrize('site,m,P_,L', [(-1, 5, 40, 3), (0, 4, 37, 2)])
+def test_chain_chunk_window_matches_oracle(device, site, m, P_, L):
+    """chain_chunk with own = ('window', ...) (train/val/run.py:332-335) against the oracle: the bar
+    of the routed chain."""
+    d = _chain_case(site, m, P_, L, seed=m + P_ + 7)
+    d['y'][1] = -1
+    own = _window_own(m, L, 300, [128, 256, 100][:L], seed=m + 17)
+    got = _probes().chain_chunk(site, **_to(d, device), own=_window_to(own, device)).cpu().double().numpy()
+    none = _probes().chain_chunk(site, **_to(d, device)).cpu().double().numpy()
+    torch.cuda.synchronize()
+    rows = np.arange(m)
+    o = _window_to(own)
+    want = _oracle_chain(site, d, rows, 'build', own=o)
+    env = np.abs(want - _oracle_chain(site, d, rows, 'build32', own=o))[rows != 1]
+    etf = np.abs(want - _oracle_chain(site, d, rows, 'tf32', own=o))[rows != 1]
+    assert np.all(got[1] == 0)
+    ok = rows != 1
+    err = np.abs(got[ok] - want[ok])
+    scale = np.abs(want[ok]).max()
+    print(f'window chain site {site}: max |gpu - build| {err.max():.3e} (envelopes {env.max():.3e}, '
+          f'tf32 {etf.max():.3e}), mean {err.mean():.3e} (envelopes {env.mean():.3e}, tf32 {etf.mean():.3e}), '
+          f'max |want| {scale:.3e}, own term {np.abs(got - none)[ok].max():.3e}')
+    assert np.isfinite(got).all()
+    assert err.max() <= 2 * max(env.max(), etf.max()) + 1e-4 * scale
+    assert err.mean() <= 2 * env.mean() + 0.5 * etf.mean() + 1e-5 * scale
+    assert np.abs(got - none)[ok].max() > 10 * (err.max() + 1e-6 * scale)
+
+
+def test_chain_query_window_without_keys_gives_nan(device):
+    """A token whose window holds no key (rel < 0) gets NaN; the others are unchanged."""
+    m, P_ = 3, 8
+    own = _window_own(m, 1, 64, [16], seed=5)
+    g = torch.Generator().manual_seed(1)
+    delta = (torch.randn(m * P_, 512, generator=g) * 0.05).to(device)
+    run = lambda o: (lambda dd: (_probes()._window_query(_window_to(o, device), m, P_, 512, 1, dd.device)(
+        0, dd, None, 0, 1.0, 0.0), dd.cpu())[1])(delta.clone())
+    good = run(own)
+    own[2][0][2] = -1
+    bad = run(own).reshape(m, P_, 512)
+    assert torch.isnan(bad[2]).all()
+    assert torch.equal(bad[:2], good.reshape(m, P_, 512)[:2])

@@ -75,6 +75,14 @@ def test_argument_errors_raise_before_launch():
         _lib.check(_lib.NOISE_EINVAL)
     q.m = 0
     assert lib.noise_chain_query(C.byref(q), None) == _lib.NOISE_OK
+    w = _lib.ChainQueryWindow(delta=256, x=256, pos=512, rel=512, w_q=256, keys=256, values=256, w_proj_t=256,
+                              cos_t=256, sin_t=256, T=16, m=2, P=4, W=512, heads=8, S=32, window=4096, a3=256,
+                              dr=256, wq3=256, wp3=256)
+    assert lib.noise_chain_query_window(C.byref(w), None) == _lib.NOISE_EINVAL   # window + 1 > 4096 keys
+    w.window, w.rel = 1024, None
+    assert lib.noise_chain_query_window(C.byref(w), None) == _lib.NOISE_EINVAL   # NULL rel
+    w.m = 0
+    assert lib.noise_chain_query_window(C.byref(w), None) == _lib.NOISE_OK
 
 
 def test_state_dict_strict_round_trip():
