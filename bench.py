@@ -6,6 +6,7 @@
     python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
     python bench.py --probe-chain    # chain_chunk (attention held) at the Cut estimator's shape, own JSON line
     python bench.py --probe-chain --own routed   # the same with the routed own-query moves
+    python bench.py --probe-chain --own window   # ... or with own-query moves over whole key windows
 
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
@@ -169,11 +170,14 @@ def bench_probe_cycle(steps, warmup, no_cpu, n=2048, P=512, V=4096):
     print(json.dumps(line), flush=True)
 
 
-def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=4096, own=False, K=64, T=2048):
+def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=4096, own=None, K=64, T=2048):
     """chain_chunk (train/val/run.py:307-351) for one chunk of the Cut estimator: 256 tokens x a full
     cycle of 512 moves of the raw embedding (site -1) through 8 blocks with 128 routed units each,
     then the head over V = 4096. own: every block also moves its own token's attention through its
-    own query along its top K = 64 keys per head (own = ('routed', ...), the estimator's default)."""
+    own query along its top K = 64 keys per head (own = 'routed', the estimator's default) or over
+    its whole key window (own = 'window': the chunk of the last 256 positions of a 2048-token
+    sequence, windows 1024 / 2048 by layer, key windows cut to multiples of 256 as the reference's
+    own_query_window does)."""
     from noise_amd import probes
     dev = torch.device('cuda', 0)
     torch.cuda.set_device(dev)
@@ -194,7 +198,23 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
                 mids=mids, xL=xL, idx=idx, hs=hs, lam_r=torch.ones(L), lam_0=torch.full((L,), 0.1), w_fc=w_fc,
                 w_out_t=w_out_t, weight_t=weight.T.bfloat16().contiguous(), base=xL @ weight.T,
                 target_logit_w=weight[y], y=y)
-    if own:
+    if own == 'window':
+        heads = W // 64
+        ang = torch.arange(T, device=dev)[:, None].float() * (1.0 / 1024 ** torch.linspace(0, 1, 32, device=dev))[None]
+        windows = [1024, 1024, 1024, 2048, 1024, 1024, 1024, 2048][:L]
+        t0, t1 = T - m, T
+        rels, keys, vals = [], [], []
+        for w in windows:
+            length = min(T, -(-(t1 - max(0, t0 - w)) // 256) * 256)
+            start = max(0, t1 - length)
+            rels.append(torch.arange(t0, t1, device=dev) - start)
+            k_ = rn(heads, length, 64)
+            keys.append((k_ * torch.rsqrt(k_.square().mean(-1, keepdim=True))).bfloat16())
+            vals.append(rn(heads, length, 64).bfloat16())
+        args['own'] = ('window', torch.arange(t0, t1, device=dev), rels, [rn(m, W) * 3 for _ in range(L)],
+                       [rn(W, W) / W ** 0.5 for _ in range(L)], keys, vals, [rn(W, W) / W ** 0.5 for _ in range(L)],
+                       ang.cos(), ang.sin(), windows)
+    elif own == 'routed':
         heads = W // 64
         ang = torch.arange(T, device=dev)[:, None].float() * (1.0 / 1024 ** torch.linspace(0, 1, 32, device=dev))[None]
         keys = []
@@ -222,9 +242,18 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
     elapsed = time.perf_counter() - t0
     call_ms = sum(a.elapsed_time(b) for a, b in events) / steps
     flops = 2 * m * P * W * k * 2 * L + 2 * m * P * W * V
-    if own:  # per block: two float32 products as three bf16 MFMA products each, two 64 x 64 per head
-        flops += L * (2 * (m * P + m) * W * 3 * W + 2 * m * P * W * 3 * W + m * P * (W // 64) * 4 * 64 * 64)
-    workload = ('chain_chunk site -1, own-query routed (K=64): ' if own else 'chain_chunk site -1, attention held: ') + \
+    if own:  # per block: two float32 products as three bf16 MFMA products each, then per head the
+        # routed 64-key products (2 x 64 x 64) or the window's two passes (3 x keys x 64, 64-key blocks)
+        flops += L * (2 * (m * P + m) * W * 3 * W + 2 * m * P * W * 3 * W)
+        if own == 'routed':
+            flops += L * m * P * (W // 64) * 4 * 64 * 64
+        else:
+            keys_seen = sum(sum(-(-(min(int(r), S - 1) - max(0, int(r) - w) + 1) // 64) * 64
+                                for r in rel.tolist()) for rel, w, S in
+                            zip(args['own'][2], args['own'][10], [kk.shape[1] for kk in args['own'][5]]))
+            flops += P * (W // 64) * 6 * 64 * keys_seen
+    workload = {None: 'chain_chunk site -1, attention held: ', 'routed': 'chain_chunk site -1, own-query routed (K=64): ',
+                'window': 'chain_chunk site -1, own-query over key windows (1024/2048): '}[own] + \
         '256 tokens x 512 moves, 8 blocks, k=128, V=4096'
     line = {
         'metric': 'chain_chunk moves/sec on 1 GPU (token x move through 8 routed blocks and the soft-capped head)',
@@ -232,7 +261,7 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
         'ms_per_step': elapsed / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
         'dtype': 'bf16', 'data': 'synthetic (random streams, bf16 block weights, Gaussian moves)',
         'config': {'workload': workload, 'tokens': m, 'moves': P, 'blocks': L, 'routed_units': k, 'vocab': V,
-                   'own': 'routed' if own else None},
+                   'own': own},
         'roofline': {'bound': 'mfma', 'achieved': flops / (call_ms / 1e3) / 1e12, 'peak': PEAK_BF16 / 1e12,
                      'unit': 'TFLOP/s', 'frac': flops / (call_ms / 1e3) / PEAK_BF16, 'traffic': None,
                      'kernel': 'one chain_chunk call (start + 8 blocks + head)', 'flops_per_call': flops,
@@ -293,8 +322,8 @@ def main():
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
     ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
     ap.add_argument('--probe-chain', action='store_true', help='bench chain_chunk (own JSON line)')
-    ap.add_argument('--own', choices=['none', 'routed'], default='none',
-                    help='--probe-chain: every attention held, or the routed own-query moves')
+    ap.add_argument('--own', choices=['none', 'routed', 'window'], default='none',
+                    help='--probe-chain: every attention held, the routed own-query moves, or over key windows')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). '
@@ -311,7 +340,7 @@ def main():
         bench_probe_cycle(max(args.steps, 5), args.warmup, args.no_cpu)
         return
     if args.probe_chain:
-        bench_probe_chain(max(args.steps, 5), args.warmup, own=args.own == 'routed')
+        bench_probe_chain(max(args.steps, 5), args.warmup, own=None if args.own == 'none' else args.own)
         return
 
     import noise_amd

@@ -442,7 +442,11 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
   for (int j = 0; j < 16; ++j) {
     acc[0][j] = bf2f(f2bf(acc[0][j])) * 0.125f;
     acc[1][j] = bf2f(f2bf(acc[1][j])) * 0.125f;
-    es[j] = p_0 * expm1f(acc[0][j]) + p_1 * expm1f(acc[1][j]);
+  }
+  {
+    const floatx16 e0 = noise::expm1_small16(acc[0]), e1 = noise::expm1_small16(acc[1]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) es[j] = p_0 * e0[j] + p_1 * e1[j];
   }
   {
     const float tot = noise::halfwave_transpose_sum16(es, lane);
@@ -453,10 +457,18 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
   float dl[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    dl[j] = dls[wave][row];
-    at[wave][row * QLD + fr] = f2bf(p_0 * expm1f(acc[0][j] - dl[j]));
-    at[wave][row * QLD + 32 + fr] = f2bf(p_1 * expm1f(acc[1][j] - dl[j]));
+    dl[j] = dls[wave][8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
+    acc[0][j] -= dl[j];
+    acc[1][j] -= dl[j];
+  }
+  {
+    const floatx16 e0 = noise::expm1_small16(acc[0]), e1 = noise::expm1_small16(acc[1]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+      at[wave][row * QLD + fr] = f2bf(p_0 * e0[j]);
+      at[wave][row * QLD + 32 + fr] = f2bf(p_1 * e1[j]);
+    }
   }
   __syncthreads();
 
@@ -482,7 +494,7 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    const float em = expm1f(-dl[j]);
+    const float em = noise::expm1_small(-dl[j]);
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
       const float v = pos_ok ? bf2f(f2bf(acc[ni][j])) + em * (ni ? r_1 : r_0) : nan;
@@ -527,41 +539,33 @@ NOISE_DEV float wave_max(float v) {
   return v;
 }
 
-// Loads keys [k0, k0 + 64) of the window (rows past `n` as zeros) into kt and, when vt is given,
-// the values transposed into vt.
-NOISE_DEV void load_key_block(const uint16_t* keys, const uint16_t* vals, int64_t base, int k0, int n,
-                              uint16_t* kt, uint16_t* vt) {
-  for (int e = threadIdx.x; e < 64 * 8; e += 256) {
-    const int k = e >> 3, c = (e & 7) * 8;
-    const bool ok = k0 + k < n;
-    const int64_t o = base + (int64_t)(k0 + k) * 64 + c;
-    *reinterpret_cast<uint4*>(kt + k * QLD + c) =
-        ok ? *reinterpret_cast<const uint4*>(keys + o) : make_uint4(0u, 0u, 0u, 0u);
-    if (vt) {
-      const uint4 vv = ok ? *reinterpret_cast<const uint4*>(vals + o) : make_uint4(0u, 0u, 0u, 0u);
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vt[(c + 2 * j) * QLD + k] = (uint16_t)(w4[j] & 0xffffu);
-        vt[(c + 2 * j + 1) * QLD + k] = (uint16_t)(w4[j] >> 16);
-      }
-    }
-  }
-}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// Value tiles [64 keys][64 dims] with chunk c (8 dims) of row r at c ^ (2 (r & 3)): the
+// transposing reads below (16 lanes: 4 consecutive keys x 2 adjacent chunks) touch 8 distinct
+// chunk positions.
+NOISE_DEV int vswz(int row, int chunk) { return row * 64 + ((chunk ^ (2 * (row & 3))) << 3); }
 
 // Workgroup (row tile, head h, token i), four waves of 32 moves each, over the n keys t with
 // 0 <= rel_i - t <= window (train/val/run.py:264-281):
 //   q0 = bf16(r0 inv0); p0 = softmax over the window of bf16(q0 K^T) / 8   (per token, on VALU)
-//   dq as in the routed step; pass 1 over 64-key blocks: dlse = log1p(sum_t p0 expm1(ds_t)),
-//   ds = bf16(dq K^T) / 8 (MFMA); pass 2 recomputes ds and accumulates bf16(w) V with
-//   w = p0 expm1(ds - dlse); dout = bf16(sum) written as A3 of the output projection's product.
-// A position outside [0, T) or a window with no key gives NaN.
+//   dq as in the routed step. Scores are formed transposed, ds^T = K dq^T (MFMA, K the A operand
+//   from LDS, dq the B operand held in registers), so a lane owns one move and 16 keys of every
+//   32-key half-block: per-move sums need no cross-lane traffic until the end.
+//   pass 1 over 64-key blocks: dlse = log1p(sum_t p0 expm1(ds_t)), ds = bf16(dq k_t) / 8;
+//   pass 2 recomputes ds, packs w = bf16(p0 expm1(ds - dlse)) in registers as the B operand of
+//   dout^T += V^T w^T, V^T read from the row-major value tile with ds_read_b64_tr_b16 (lane
+//   4a + b of each 16-lane group receives element b of the rows addressed by lanes a, a + 4,
+//   a + 8, a + 12) in the key order the score accumulators hold.
+// dout = bf16(sum) is written as A3 of the output projection's product. A position outside
+// [0, T) or a window with no key gives NaN.
 __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQueryWin g) {
-  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * QLD];
-  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];
-  __shared__ float p0s[QWMAX];
-  __shared__ float r0s[64], cs[32], sn[32], dls[4][32], red[8], inv0s;
+  __shared__ __attribute__((aligned(16))) uint16_t kts[2][64 * QLD];  // keys [key][dim], padded rows
+  __shared__ __attribute__((aligned(16))) uint16_t vts[2][64 * 64];   // values [key][dim], vswz chunks
+  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq
+  __shared__ __attribute__((aligned(16))) float p0s[QWMAX + 64];
+  __shared__ float r0s[64], cs[32], sn[32], red[8], inv0s;
   __shared__ __attribute__((aligned(16))) uint16_t q0s[64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -571,6 +575,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
   const int64_t lo64 = rl - g.window > 0 ? rl - g.window : 0;
   const int64_t hi64 = rl < g.S - 1 ? rl : g.S - 1;
   const int n = hi64 >= lo64 ? (int)(hi64 - lo64 + 1) : 0;  // <= window + 1 <= QWMAX
+  const int nb = (n + 63) & ~63;                               // keys swept, in blocks of 64
   const bool ok = pos >= 0 && pos < g.T && n > 0;
   const int64_t pc = ok ? pos : 0;
   const int64_t kbase = ((int64_t)h * g.S + (n > 0 ? lo64 : 0)) * 64;
@@ -590,7 +595,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
     if (tid == 0) inv0s = sq;
   }
   __syncthreads();
-  // clean scores of the window, then its softmax
+  // clean scores of the window, then its softmax (zeros past the window up to nb)
   float mx = -INFINITY;
   for (int t = tid; t < n; t += 256) {
     const uint16_t* kr = g.keys + kbase + (int64_t)t * 64;
@@ -621,7 +626,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
   if (lane == 0) red[4 + wave] = z;
   __syncthreads();
   z = (red[4] + red[5]) + (red[6] + red[7]);
-  for (int t = tid; t < n; t += 256) p0s[t] = p0s[t] / z;
+  for (int t = tid; t < nb; t += 256) p0s[t] = t < n ? p0s[t] / z : 0.f;
   const float sq = inv0s, inv0 = rsqrtf(sq / 64.f + CAP_EPS32);
 
   // dq: lanes 2 q and 2 q + 1 hold move q's dims c, c + 32 for c in [0, 16) and [16, 32)
@@ -666,113 +671,146 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
     }
   }
   __syncthreads();  // dq tiles and p0 complete
-  const int fr = lane & 31, fk = 8 * (lane >> 5);
-  bf16x8 aq[4];  // this wave's dq fragments, held for both passes
+  const int fr = lane & 31, half = lane >> 5, fk = 8 * half;
+  bf16x8 qf[4];  // B operand: this lane's move fr, dims 16 ks + 8 half .. + 7
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) aq[ks] = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
-
-  // pass 1: sum_t p0 expm1(ds_t) per move
-  float es[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) es[j] = 0.f;
-  for (int k0 = 0; k0 < n; k0 += 64) {
-    __syncthreads();
-    load_key_block(g.keys, g.vals, kbase, k0, n, kt, nullptr);
-    __syncthreads();
-    floatx16 acc[2];
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[ks], b, acc[ni], 0, 0, 0);
-      }
-    const float p_0 = k0 + fr < n ? p0s[k0 + fr] : 0.f, p_1 = k0 + 32 + fr < n ? p0s[k0 + 32 + fr] : 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      es[j] += p_0 * expm1f(bf2f(f2bf(acc[0][j])) * 0.125f) + p_1 * expm1f(bf2f(f2bf(acc[1][j])) * 0.125f);
-  }
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+  // V^T fragment offsets (within the value tile): in 16-lane group gq, lane a + 4 e addresses
+  // key 4 (gq >> 1) + e (+ 16 kk + 32 kb2, + 8 for the second read), dims 32 db + 16 (gq & 1) + 4 a;
+  // the lane then holds dim 32 db + lane % 32 for the keys its w values hold.
+  int vfo[2];
   {
-    const float tot = noise::halfwave_transpose_sum16(es, lane);
-    const int jj = fr >> 1;
-    if ((lane & 1) == 0) dls[wave][8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3)] = log1pf(tot);
+    const int s16 = lane & 15, a = s16 & 3, e = s16 >> 2, gq = lane >> 4;
+    const int key = 4 * (gq >> 1) + e;
+#pragma unroll
+    for (int db = 0; db < 2; ++db) vfo[db] = vswz(key, 4 * db + 2 * (gq & 1) + (a >> 1)) + 4 * (a & 1);
   }
-  __syncthreads();
-  float dl[16];
+  // ds^T of one 32-key half-block: key 32 kb2 + 8 (j / 4) + 4 half + j % 4 for move fr
+  auto scores = [&](const uint16_t* kt, int kb2) {
+    floatx16 acc;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) dl[j] = dls[wave][8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
-
-  // pass 2: dout = sum over blocks of bf16(p0 expm1(ds - dlse)) V
-  floatx16 out[2];
-#pragma unroll
-  for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) out[ni][j] = 0.f;
-  for (int k0 = 0; k0 < n; k0 += 64) {
-    __syncthreads();
-    load_key_block(g.keys, g.vals, kbase, k0, n, kt, vt);
-    __syncthreads();
-    floatx16 acc[2];
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq[ks], b, acc[ni], 0, 0, 0);
-      }
-    const float p_0 = k0 + fr < n ? p0s[k0 + fr] : 0.f, p_1 = k0 + 32 + fr < n ? p0s[k0 + 32 + fr] : 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      at[wave][row * QLD + fr] = f2bf(p_0 * expm1f(bf2f(f2bf(acc[0][j])) * 0.125f - dl[j]));
-      at[wave][row * QLD + 32 + fr] = f2bf(p_1 * expm1f(bf2f(f2bf(acc[1][j])) * 0.125f - dl[j]));
-    }
-    __syncthreads();
+    for (int j = 0; j < 16; ++j) acc[j] = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + (32 * kb2 + fr) * QLD + 16 * ks + fk);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], acc, 0, 0, 0);
+    }
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(vt + (ni * 32 + fr) * QLD + 16 * ks + fk);
-        out[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, out[ni], 0, 0, 0);
+    for (int j = 0; j < 16; ++j) acc[j] = bf2f(f2bf(acc[j])) * 0.125f;
+    return acc;
+  };
+  // Blocks of 64 keys go global -> registers one block ahead, then into one of two LDS buffers
+  // (one barrier per block). Thread tid moves chunk tid % 8 of keys tid / 8 and tid / 8 + 32.
+  uint4 rk[2], rv[2];
+  auto fetch = [&](int k0, bool with_values) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int k = (tid >> 3) + 32 * r, c = tid & 7;
+      const bool in = k0 + k < n;
+      const int64_t o = kbase + (int64_t)(in ? k0 + k : 0) * 64 + 8 * c;
+      rk[r] = *reinterpret_cast<const uint4*>(g.keys + o);
+      if (with_values) rv[r] = *reinterpret_cast<const uint4*>(g.vals + o);
+      if (!in) rk[r] = rv[r] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto stash = [&](int buf, bool with_values) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int k = (tid >> 3) + 32 * r, c = tid & 7;
+      *reinterpret_cast<uint4*>(kts[buf] + k * QLD + 8 * c) = rk[r];
+      if (with_values) *reinterpret_cast<uint4*>(vts[buf] + vswz(k, c)) = rv[r];
+    }
+  };
+
+  // pass 1
+  float es = 0.f;
+  if (nb) fetch(0, false);
+  for (int k0 = 0, buf = 0; k0 < nb; k0 += 64, buf ^= 1) {
+    stash(buf, false);
+    if (k0 + 64 < nb) fetch(k0 + 64, false);
+    __syncthreads();
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      const floatx16 em = noise::expm1_small16(scores(kts[buf], kb2));
+      const float* pp = p0s + k0 + 32 * kb2 + 4 * half;
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const float4 p = *reinterpret_cast<const float4*>(pp + 8 * g4);
+        es += p.x * em[4 * g4] + p.y * em[4 * g4 + 1] + p.z * em[4 * g4 + 2] + p.w * em[4 * g4 + 3];
       }
     }
   }
-  const float nan = __builtin_nanf("");
-  __syncthreads();  // kt, vt and the w tiles are free: hi halves in at, lo halves in kt / vt
-  uint16_t* hi_t = at[wave];
-  uint16_t* lo_t = (wave < 2 ? kt : vt) + (wave & 1) * 32 * QLD;
+  const float dl = log1pf(es + __shfl_xor(es, 32, 64));
+
+  // pass 2
+  floatx16 o[2];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+  for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const float v = ok ? bf2f(f2bf(out[ni][j])) : nan;
-      const uint16_t hv = f2bf(v);
-      hi_t[row * QLD + ni * 32 + fr] = hv;
-      lo_t[row * QLD + ni * 32 + fr] = f2bf(v - bf2f(hv));
+    for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
+  __syncthreads();  // pass 1 is done with both key buffers
+  if (nb) fetch(0, true);
+  for (int k0 = 0, buf = 0; k0 < nb; k0 += 64, buf ^= 1) {
+    stash(buf, true);
+    if (k0 + 64 < nb) fetch(k0 + 64, true);
+    __syncthreads();
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      floatx16 ds = scores(kts[buf], kb2);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ds[j] -= dl;
+      const floatx16 em = noise::expm1_small16(ds);
+      const float* pp = p0s + k0 + 32 * kb2 + 4 * half;
+      bf16x8 pf[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const float4 pa = *reinterpret_cast<const float4*>(pp + 16 * kk);
+        const float4 pb = *reinterpret_cast<const float4*>(pp + 16 * kk + 8);
+        const int j0 = 8 * kk;
+        u32x4 pk;
+        pk[0] = pack_bf2(pa.x * em[j0], pa.y * em[j0 + 1]);
+        pk[1] = pack_bf2(pa.z * em[j0 + 2], pa.w * em[j0 + 3]);
+        pk[2] = pack_bf2(pb.x * em[j0 + 4], pb.y * em[j0 + 5]);
+        pk[3] = pack_bf2(pb.z * em[j0 + 6], pb.w * em[j0 + 7]);
+        pf[kk] = __builtin_bit_cast(bf16x8, pk);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const uint16_t* a0 = vts[buf] + 32 * kb2 * 64 + 16 * kk * 64 + vfo[db];
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0));
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0 + 8 * 64));
+          u32x4 u;
+          u[0] = __builtin_bit_cast(u32x2, lo)[0];
+          u[1] = __builtin_bit_cast(u32x2, lo)[1];
+          u[2] = __builtin_bit_cast(u32x2, hi)[0];
+          u[3] = __builtin_bit_cast(u32x2, hi)[1];
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u), pf[kk], o[db], 0, 0, 0);
+        }
     }
   }
-  __syncthreads();
+  // lane: move fr, dims 32 db + 8 (j / 4) + 4 half + j % 4
+  const int p = pw + fr;
+  if (p < g.P) {
+    const float nan = __builtin_nanf("");
+    uint16_t* orow = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + 4 * half;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
-    const int p = pw + row;
-    if (p >= g.P) continue;
-    const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
-    const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
-    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
-    *reinterpret_cast<uint4*>(o) = hv;
-    *reinterpret_cast<uint4*>(o + g.W) = lv;
-    *reinterpret_cast<uint4*>(o + 2 * g.W) = hv;
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float4 v;
+        v.x = ok ? bf2f(f2bf(o[db][4 * g4])) : nan;
+        v.y = ok ? bf2f(f2bf(o[db][4 * g4 + 1])) : nan;
+        v.z = ok ? bf2f(f2bf(o[db][4 * g4 + 2])) : nan;
+        v.w = ok ? bf2f(f2bf(o[db][4 * g4 + 3])) : nan;
+        uint2 hv, lv;
+        split4(v, hv, lv);
+        uint16_t* q = orow + 32 * db + 8 * g4;
+        *reinterpret_cast<uint2*>(q) = hv;
+        *reinterpret_cast<uint2*>(q + g.W) = lv;
+        *reinterpret_cast<uint2*>(q + 2 * g.W) = hv;
+      }
   }
 }
 

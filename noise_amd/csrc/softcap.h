@@ -19,6 +19,39 @@ NOISE_DEV float capexp(float u, float ik) {
 
 NOISE_DEV float cap(float z) { return 15.f * tanhf(z / 15.f); }
 
+// e^x - 1 for the small logit changes of the own-query steps: the Taylor series to x^8 / 8! in
+// Horner form for |x| <= 0.5 (truncation below 1.1e-8 relative; about 2 ulp measured in float32
+// without fma), expf(x) - 1 beyond (no cancellation there: |e^x - 1| >= 0.39).
+NOISE_DEV float expm1_series(float x) {
+  float r = fmaf(x, 1.f / 40320.f, 1.f / 5040.f);
+  r = fmaf(x, r, 1.f / 720.f);
+  r = fmaf(x, r, 1.f / 120.f);
+  r = fmaf(x, r, 1.f / 24.f);
+  r = fmaf(x, r, 1.f / 6.f);
+  r = fmaf(x, r, 0.5f);
+  r = fmaf(x, r, 1.f);
+  return r * x;
+}
+
+NOISE_DEV float expm1_small(float x) { return fabsf(x) <= 0.5f ? expm1_series(x) : expf(x) - 1.f; }
+
+// The same on 16 values with one branch: the series everywhere, then expf(x) - 1 where |x| > 0.5
+// (or NaN) only if some lane of the wave has such a value.
+NOISE_DEV floatx16 expm1_small16(floatx16 x) {
+  floatx16 r;
+  bool big = false;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    r[j] = expm1_series(x[j]);
+    big |= !(fabsf(x[j]) <= 0.5f);
+  }
+  if (big) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) r[j] = fabsf(x[j]) <= 0.5f ? r[j] : expf(x[j]) - 1.f;
+  }
+  return r;
+}
+
 // cap(z1) - cap(z0), accurate when z1 is close to z0: tanh(a) - tanh(b) = tanh(a - b)(1 - tanh a tanh b).
 NOISE_DEV float cap_difference(float z1, float z0) {
   return 15.f * tanhf((z1 - z0) / 15.f) * (1.f - tanhf(z1 / 15.f) * tanhf(z0 / 15.f));
