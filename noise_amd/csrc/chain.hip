@@ -250,8 +250,8 @@ __global__ __launch_bounds__(256) void chain_split_weight_kernel(const float* __
   split3(out + n * 3 * W, W, k, w[n * s_n + k * s_k], false);
 }
 
-// Rows r < m P: the optional mix of delta, then A3 of norm_difference(x_i, delta_r) (the query
-// product's input, train/val/run.py:294); rows m P + i: A3 of norm(x_i) (the clean query's).
+// Row r < m P: the optional mix of delta, then A3 of norm_difference(x_i, delta_r) (the query
+// product's input, train/val/run.py:294).
 __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict__ delta,
                                                               const float* __restrict__ dx0,
                                                               const float* __restrict__ x, int m, int P, int W,
@@ -260,9 +260,8 @@ __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t rows = (int64_t)m * P;
-  if (r >= rows + m) return;
-  const bool clean = r >= rows;
-  const int64_t i = clean ? r - rows : r / P;
+  if (r >= rows) return;
+  const int64_t i = r / P;
   const int nt = W / 256;
   float4 d[MAXT], xv[MAXT];
   float sq = 0.f, dot = 0.f, dsq = 0.f;
@@ -270,15 +269,12 @@ __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict_
   for (int t = 0; t < MAXT; ++t)
     if (t < nt) {
       const int64_t o = r * W + 4 * lane + 256 * t;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!clean) {
-        v = ld4(delta + o);
-        if (mix) {
-          const float4 z = dx0 ? ld4(dx0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
-          v = make_float4(lam_r * v.x + lam_0 * z.x, lam_r * v.y + lam_0 * z.y, lam_r * v.z + lam_0 * z.z,
-                          lam_r * v.w + lam_0 * z.w);
-          st4(delta + o, v);
-        }
+      float4 v = ld4(delta + o);
+      if (mix) {
+        const float4 z = dx0 ? ld4(dx0 + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v = make_float4(lam_r * v.x + lam_0 * z.x, lam_r * v.y + lam_0 * z.y, lam_r * v.z + lam_0 * z.z,
+                        lam_r * v.w + lam_0 * z.w);
+        st4(delta + o, v);
       }
       d[t] = v;
       xv[t] = ld4(x + i * W + 4 * lane + 256 * t);
@@ -291,8 +287,7 @@ __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict_
   dsq = wave_sum(dsq);
   const float inv0 = rsqrtf(sq / (float)W + CAP_EPS32);
   const float inv = rsqrtf((sq + 2.f * dot + dsq) / (float)W + CAP_EPS32);
-  // clean rows: norm(x) = x inv0; moves: delta inv + x (inv - inv0)
-  const float a = clean ? 0.f : inv, b = clean ? inv0 : inv - inv0;
+  const float a = inv, b = inv - inv0;  // delta inv + x (inv - inv0)
   uint16_t* o = a3 + r * 3 * W;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
@@ -305,6 +300,45 @@ __global__ __launch_bounds__(256) void chain_query_pre_kernel(float* __restrict_
       *reinterpret_cast<uint2*>(o + W + c) = lo;
       *reinterpret_cast<uint2*>(o + 2 * W + c) = hi;
     }
+}
+
+// The clean query products r0_i = norm(x_i) W_q^T (train/val/run.py:293) in float32 on VALU,
+// written to rows m P + i of dr. Workgroup: 8 tokens x 64 outputs; lane l of wave w forms the
+// outputs 64 blockIdx.x + 16 w + l % 16 for tokens 8 blockIdx.y + l / 16 and + 4.
+__global__ __launch_bounds__(256) void chain_query_clean_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ w_q, int m, int W,
+                                                                float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float xs[8][256 * MAXT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.y * 8;
+  const int nt = W / 256;
+  for (int tt = wave; tt < 8; tt += 4) {  // norm(x) of tokens t0 + tt into LDS
+    const int tok = min(t0 + tt, m - 1);
+    float4 v[MAXT];
+    float sq = 0.f;
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t)
+      if (t < nt) {
+        v[t] = ld4(x + (int64_t)tok * W + 4 * lane + 256 * t);
+        sq += dot4(v[t], v[t]);
+      }
+    const float inv0 = rsqrtf(wave_sum(sq) / (float)W + CAP_EPS32);
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t)
+      if (t < nt)
+        st4(&xs[tt][4 * lane + 256 * t], make_float4(v[t].x * inv0, v[t].y * inv0, v[t].z * inv0, v[t].w * inv0));
+  }
+  __syncthreads();
+  const int n = blockIdx.x * 64 + wave * 16 + (lane & 15), ta = lane >> 4;
+  const float* wr = w_q + (int64_t)n * W;
+  float s0 = 0.f, s1 = 0.f;
+  for (int k = 0; k < W; k += 4) {
+    const float4 wv = ld4(wr + k);
+    s0 += dot4(wv, ld4(&xs[ta][k]));
+    s1 += dot4(wv, ld4(&xs[ta + 4][k]));
+  }
+  if (t0 + ta < m) out[(int64_t)(t0 + ta) * W + n] = s0;
+  if (t0 + ta + 4 < m) out[(int64_t)(t0 + ta + 4) * W + n] = s1;
 }
 
 struct ChainQuery {
@@ -1009,21 +1043,23 @@ extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
 namespace {
 
 // The parts of an own-query step around its attention kernel: the weights' hi/lo triples, the
-// mix and A3 rows (moves, then the m clean rows), and dr = A3 W_q3^T.
+// clean query products (rows m P + i of dr), the mix and A3 rows of the moves, and their
+// dr = A3 W_q3^T.
 int query_products(float* delta, const float* dx0, int mix, float lam_r, float lam_0, const float* x,
                    const float* w_q, const float* w_proj_t, int m, int P, int W, uint16_t* a3, float* dr,
                    uint16_t* wq3, uint16_t* wp3, hipStream_t st) {
-  const int64_t rows_all = (int64_t)m * P + m;
+  const int64_t rows = (int64_t)m * P;
   const unsigned wblocks = (unsigned)(((int64_t)W * W + 255) / 256);
   chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(w_q, W, 1, W, wq3);
   if (int e = noise::check_launch("chain_query")) return e;
   chain_split_weight_kernel<<<wblocks, 256, 0, st>>>(w_proj_t, 1, W, W, wp3);
   if (int e = noise::check_launch("chain_query")) return e;
-  chain_query_pre_kernel<<<(unsigned)((rows_all + 3) / 4), 256, 0, st>>>(delta, dx0, x, m, P, W, mix, lam_r, lam_0,
-                                                                         a3);
+  chain_query_clean_kernel<<<dim3(W / 64, (unsigned)((m + 7) / 8)), 256, 0, st>>>(x, w_q, m, W, dr + rows * W);
   if (int e = noise::check_launch("chain_query")) return e;
-  ChainGemm g1{a3, wq3, (int)rows_all, W, 3 * W, nullptr, 0, nullptr, dr};
-  chain_gemm_kernel<MODE_STORE, 256><<<dim3((unsigned)((rows_all + 255) / 256), W / 256, 1), 512, 0, st>>>(g1);
+  chain_query_pre_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(delta, dx0, x, m, P, W, mix, lam_r, lam_0, a3);
+  if (int e = noise::check_launch("chain_query")) return e;
+  ChainGemm g1{a3, wq3, (int)rows, W, 3 * W, nullptr, 0, nullptr, dr};
+  chain_gemm_kernel<MODE_STORE, 256><<<dim3((unsigned)((rows + 255) / 256), W / 256, 1), 512, 0, st>>>(g1);
   return noise::check_launch("chain_query");
 }
 
