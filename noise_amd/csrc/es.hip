@@ -54,7 +54,9 @@ __global__ __launch_bounds__(FT) void fitness_kernel(const float* __restrict__ l
   if (tid == 0 && status) *status = nbad > 0.f ? NOISE_ENONFINITE : NOISE_OK;
 }
 
-// 64 x 64 output tile per workgroup of 256 threads, 4 x 4 outputs per thread, 16 pairs per stage.
+// 64 x 64 output tile per workgroup of 256 threads, 4 x 4 outputs per thread, 32 pairs per stage.
+// The next stage's scaled noise goes global -> registers while the current one is summed from
+// one of two LDS buffers (one barrier per stage). Every output sums its pairs in ascending order.
 __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restrict__ w, int n,
                                                           const float* __restrict__ a_base,
                                                           const int64_t* __restrict__ a_off,
@@ -62,40 +64,49 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
                                                           const int64_t* __restrict__ b_off, int out,
                                                           int in, float scale, int accumulate,
                                                           float* __restrict__ G) {
-  __shared__ float As[16][64];
-  __shared__ float Bs[16][64];
+  constexpr int SJ = 32;
+  __shared__ __attribute__((aligned(16))) float As[2][SJ][64];
+  __shared__ __attribute__((aligned(16))) float Bs[2][SJ][64];
   const int tid = threadIdx.x;
   const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
   const int tx = tid & 15, ty = tid >> 4;
   float acc[4][4] = {};
-  const int lj = tid >> 4, lc = (tid & 15) * 4;
-  for (int j0 = 0; j0 < n; j0 += 16) {
+  // loader: pair lj of the stage, columns lc .. lc + 7
+  const int lj = tid >> 3, lc = (tid & 7) * 8;
+  float ra[8], rb[8];
+  auto fetch = [&](int j0) {
     const int j = j0 + lj;
+    const bool live = j < n;
+    const float wj = live ? w[j] : 0.f;
+    const int64_t ao = live ? a_off[j] : 0, bo = live && b_base ? b_off[j] : 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 8; ++e) {
       const int o = o0 + lc + e, i = i0 + lc + e;
-      float av = 0.f, bv = 0.f;
-      if (j < n) {
-        if (o < out) av = w[j] * a_base[a_off[j] + o];
-        if (i < in) bv = b_base ? b_base[b_off[j] + i] : 1.0f;
-      }
-      As[lj][lc + e] = av;
-      Bs[lj][lc + e] = bv;
+      ra[e] = live && o < out ? wj * a_base[ao + o] : 0.f;
+      rb[e] = live && i < in ? (b_base ? b_base[bo + i] : 1.0f) : 0.f;
     }
+  };
+  auto stash = [&](int buf) {
+    *reinterpret_cast<float4*>(&As[buf][lj][lc]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
+    *reinterpret_cast<float4*>(&As[buf][lj][lc + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
+    *reinterpret_cast<float4*>(&Bs[buf][lj][lc]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
+    *reinterpret_cast<float4*>(&Bs[buf][lj][lc + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
+  };
+  if (n > 0) fetch(0);
+  for (int j0 = 0, buf = 0; j0 < n; j0 += SJ, buf ^= 1) {
+    stash(buf);
+    if (j0 + SJ < n) fetch(j0 + SJ);
     __syncthreads();
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      float ar[4], br[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ar[r] = As[jj][ty * 4 + r];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) br[c] = Bs[jj][tx * 4 + c];
+#pragma unroll 8
+    for (int jj = 0; jj < SJ; ++jj) {
+      const float4 a4 = *reinterpret_cast<const float4*>(&As[buf][jj][ty * 4]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&Bs[buf][jj][tx * 4]);
+      const float ar[4] = {a4.x, a4.y, a4.z, a4.w}, br[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[r][c] += ar[r] * br[c];
     }
-    __syncthreads();
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
