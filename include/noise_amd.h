@@ -191,7 +191,12 @@ int noise_fitness(const float* losses, int n_losses, int pairs, float* weight,
  * parameter is out = L, in = 1 with b_j = 1 when b_base is NULL). */
 int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t* a_off,
                       const float* b_base, const int64_t* b_off, int out, int in, float scale,
-                      int accumulate, float* G, void* stream);
+                      int accumulate, float* G, float* work, int64_t work_elems, void* stream);
+
+/* Floats of `work` with which noise_es_gradient splits the pair sum over more workgroups (a
+ * fixed split and a fixed-order reduction: the same result on every call); with less (or NULL)
+ * it makes one pass over every pair. No counterpart in the reference: workspace sizing. */
+int64_t noise_es_gradient_work(int n, int out, int in);
 
 /* AdamW over a flat fp32 buffer (torch.optim.AdamW semantics, eggroll.py:164-167, 205):
  * param *= 1 - lr wd; m = lerp(m, g, 1 - b1); v = b2 v + (1 - b2) g^2;

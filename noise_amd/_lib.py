@@ -96,7 +96,8 @@ SIGNATURES = {
     'noise_head_ce': [C.POINTER(Head), P],
     'noise_member_mean': [P, INT, INT, P, P],
     'noise_fitness': [P, INT, INT, P, P, P],
-    'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
+    'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P, I64, P],
+    'noise_es_gradient_work': [INT, INT, INT],
     'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],
     'noise_cast_bf16': [P, I64, P, P, P],
     'noise_coordinate_differences': [P, INT, I64, P, INT, INT, F32, P, I64, P],
@@ -126,6 +127,7 @@ def load():
         fn.restype = INT
     lib.noise_last_error.argtypes = []
     lib.noise_last_error.restype = C.c_char_p
+    lib.noise_es_gradient_work.restype = I64  # a size, not a status
     _lib = lib
     return lib
 

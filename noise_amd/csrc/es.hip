@@ -57,13 +57,16 @@ __global__ __launch_bounds__(FT) void fitness_kernel(const float* __restrict__ l
 // 64 x 64 output tile per workgroup of 256 threads, 4 x 4 outputs per thread, 32 pairs per stage.
 // The next stage's scaled noise goes global -> registers while the current one is summed from
 // one of two LDS buffers (one barrier per stage). Every output sums its pairs in ascending order.
+// With splits > 1, workgroup z sums pairs [z per, (z + 1) per) into its own slice of `partial`
+// and es_gradient_reduce_kernel adds the slices in order: the same sums on every run.
 __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restrict__ w, int n,
                                                           const float* __restrict__ a_base,
                                                           const int64_t* __restrict__ a_off,
                                                           const float* __restrict__ b_base,
                                                           const int64_t* __restrict__ b_off, int out,
                                                           int in, float scale, int accumulate,
-                                                          float* __restrict__ G) {
+                                                          float* __restrict__ G, int per,
+                                                          float* __restrict__ partial) {
   constexpr int SJ = 32;
   __shared__ __attribute__((aligned(16))) float As[2][SJ][64];
   __shared__ __attribute__((aligned(16))) float Bs[2][SJ][64];
@@ -73,10 +76,11 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
   float acc[4][4] = {};
   // loader: pair lj of the stage, columns lc .. lc + 7
   const int lj = tid >> 3, lc = (tid & 7) * 8;
+  const int jb = blockIdx.z * per, je = min(n, jb + per);  // this workgroup's pairs
   float ra[8], rb[8];
   auto fetch = [&](int j0) {
     const int j = j0 + lj;
-    const bool live = j < n;
+    const bool live = j < je;
     const float wj = live ? w[j] : 0.f;
     const int64_t ao = live ? a_off[j] : 0, bo = live && b_base ? b_off[j] : 0;
 #pragma unroll
@@ -92,10 +96,10 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
     *reinterpret_cast<float4*>(&Bs[buf][lj][lc]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
     *reinterpret_cast<float4*>(&Bs[buf][lj][lc + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
   };
-  if (n > 0) fetch(0);
-  for (int j0 = 0, buf = 0; j0 < n; j0 += SJ, buf ^= 1) {
+  if (jb < je) fetch(jb);
+  for (int j0 = jb, buf = 0; j0 < je; j0 += SJ, buf ^= 1) {
     stash(buf);
-    if (j0 + SJ < n) fetch(j0 + SJ);
+    if (j0 + SJ < je) fetch(j0 + SJ);
     __syncthreads();
 #pragma unroll 8
     for (int jj = 0; jj < SJ; ++jj) {
@@ -116,11 +120,36 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
     for (int c = 0; c < 4; ++c) {
       const int i = i0 + tx * 4 + c;
       if (i >= in) continue;
-      float* dst = G + (int64_t)o * in + i;
-      const float v = scale * acc[r][c];
-      *dst = accumulate ? *dst + v : v;
+      if (partial) {
+        partial[((int64_t)blockIdx.z * out + o) * in + i] = acc[r][c];
+      } else {
+        float* dst = G + (int64_t)o * in + i;
+        const float v = scale * acc[r][c];
+        *dst = accumulate ? *dst + v : v;
+      }
     }
   }
+}
+
+__global__ __launch_bounds__(256) void es_gradient_reduce_kernel(const float* __restrict__ partial, int splits,
+                                                                 int64_t elems, float scale, int accumulate,
+                                                                 float* __restrict__ G) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= elems) return;
+  float s = 0.f;
+  for (int z = 0; z < splits; ++z) s += partial[z * elems + e];
+  const float v = scale * s;
+  G[e] = accumulate ? G[e] + v : v;
+}
+
+// Pair splits for an (out, in) gradient: enough workgroups to fill the chip (the pair loop of a
+// lone workgroup is latency-bound), at least two 32-pair stages each.
+int es_splits(int n, int out, int in) {
+  const int64_t wgs = (int64_t)((in + 63) / 64) * ((out + 63) / 64);
+  int split = (int)((2048 + wgs - 1) / wgs);
+  split = split < 16 ? split : 16;
+  const int max_by_pairs = n / 64 > 1 ? n / 64 : 1;
+  return split < max_by_pairs ? split : max_by_pairs;
 }
 
 NOISE_DEV float lerp_torch(float start, float end, float weight) {
@@ -157,16 +186,33 @@ extern "C" int noise_fitness(const float* losses, int n_losses, int pairs, float
   return noise::check_launch("fitness");
 }
 
+extern "C" int64_t noise_es_gradient_work(int n, int out, int in) {
+  if (n <= 0 || out <= 0 || in <= 0) return 0;
+  const int split = es_splits(n, out, in);
+  return split > 1 ? (int64_t)split * out * in : 0;
+}
+
 extern "C" int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t* a_off,
                                  const float* b_base, const int64_t* b_off, int out, int in, float scale,
-                                 int accumulate, float* G, void* stream) {
+                                 int accumulate, float* G, float* work, int64_t work_elems, void* stream) {
   NOISE_REQUIRE(w && a_base && a_off && G && n >= 0 && out > 0 && in > 0, "es_gradient: bad arguments");
   NOISE_REQUIRE(!b_base || b_off, "es_gradient: b_base needs b_off");
   NOISE_REQUIRE(b_base || in == 1, "es_gradient: a vector parameter (no b) needs in == 1");
-  dim3 grid((in + 63) / 64, (out + 63) / 64);
+  NOISE_REQUIRE(work_elems >= 0 && (work || work_elems == 0), "es_gradient: work_elems without work");
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t elems = (int64_t)out * in;
+  int split = es_splits(n, out, in);
+  if (split > 1 && work_elems < split * elems) split = 1;  // no room: one pass over every pair
+  const int per = split > 1 ? ((n + split - 1) / split + 31) / 32 * 32 : (n > 0 ? n : 1);
+  split = split > 1 ? (n + per - 1) / per : 1;
+  dim3 grid((in + 63) / 64, (out + 63) / 64, split);
   NOISE_REQUIRE(grid.y < 65536, "es_gradient: out=%d too large", out);
-  es_gradient_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(w, n, a_base, a_off, b_base, b_off, out, in, scale,
-                                                            accumulate, G);
+  es_gradient_kernel<<<grid, 256, 0, st>>>(w, n, a_base, a_off, b_base, b_off, out, in, scale, accumulate, G, per,
+                                           split > 1 ? work : nullptr);
+  if (int e = noise::check_launch("es_gradient")) return e;
+  if (split == 1) return NOISE_OK;
+  es_gradient_reduce_kernel<<<(unsigned)((elems + 255) / 256), 256, 0, st>>>(work, split, elems, scale, accumulate,
+                                                                             G);
   return noise::check_launch("es_gradient");
 }
 

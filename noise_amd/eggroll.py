@@ -52,6 +52,7 @@ class Eggroll:
             self.grads[name] = self.grad_flat[off:off + n].view(shape)
             off += n
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.grad_work = None  # es_gradient's split-sum workspace, sized on the first step
 
     def offsets(self, step):
         g = torch.Generator(self.device).manual_seed(1_000_003 * self.seed + step)
@@ -110,13 +111,17 @@ class Eggroll:
         n = losses.numel() // 2
         weight = torch.empty(pairs, device=self.device)
         K.fitness(losses, pairs, weight, self.status)
+        need = max(K.es_gradient_work(pairs, s[0], s[1] if len(s) == 2 else 1) for s in self.shapes.values())
+        if self.grad_work is None or self.grad_work.numel() < need:
+            self.grad_work = torch.empty(max(need, 1), device=self.device)
         for name, shape in self.shapes.items():
             off = offsets[name]
             if len(shape) == 2:
                 K.es_gradient(weight, self.buffer, off, self.buffer, off + shape[0], shape[0], shape[1], -1.0 / n,
-                              self.grads[name])
+                              self.grads[name], work=self.grad_work)
             else:
-                K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name])
+                K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name],
+                              work=self.grad_work)
         if int(self.status.item()) != 0:  # checked before the weights move
             raise FloatingPointError('non-finite member loss in the population step')
         optimizer.zero_grad(set_to_none=True)

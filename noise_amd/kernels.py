@@ -202,10 +202,18 @@ def fitness(losses, pairs, weight, status):
     _lib.call('noise_fitness', _ptr(losses), losses.numel(), pairs, _ptr(weight), _ptr(status), _stream())
 
 
-def es_gradient(w, a_base, a_off, b_base, b_off, out, inn, scale, G, accumulate=False):
+def es_gradient_work(n, out, inn):
+    """Floats of workspace with which es_gradient splits its pair sum over more workgroups."""
+    return int(_lib.load().noise_es_gradient_work(n, out, inn))
+
+
+def es_gradient(w, a_base, a_off, b_base, b_off, out, inn, scale, G, accumulate=False, work=None):
     _on_gpu(w, a_base, a_off, G)
+    _need(work is None or (work.is_cuda and work.dtype == torch.float32 and work.is_contiguous()),
+          'es_gradient: work must be a contiguous fp32 device tensor')
     _lib.call('noise_es_gradient', _ptr(w), w.numel(), _ptr(a_base), _ptr(a_off), _ptr(b_base), _ptr(b_off),
-              out, inn, scale, int(accumulate), _ptr(G), _stream())
+              out, inn, scale, int(accumulate), _ptr(G), _ptr(work), 0 if work is None else work.numel(),
+              _stream())
 
 
 def adamw(param, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, step):

@@ -327,6 +327,32 @@ def test_fitness_gradient_adamw(device):
     torch.testing.assert_close(dp.cpu(), refp.detach(), rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize('out,inn', [(512, 512), (70, 90), (300, 1)])
+def test_es_gradient_split_pairs(device, out, inn):
+    """The gradient with the pair sum split over more workgroups (1536 pairs, as the population
+    step has them) against float64 sums, against the one-pass path, and identical on a second call."""
+    from oracle import es_ref
+    g = _gen(out + inn)
+    pairs = 1536
+    buf = torch.randn(200000, generator=g)
+    off = torch.randint(0, buf.numel() - out - inn, (pairs,), generator=g)
+    w_in = torch.randn(pairs, generator=g)
+    a = torch.stack([buf[o:o + out] for o in off.tolist()])
+    b = torch.stack([buf[o + out:o + out + inn] for o in off.tolist()]) if inn > 1 else None
+    ref = es_ref.gradient(w_in.double(), {'m': (a, b) if b is not None else a}, pairs)['m']
+    work = torch.empty(max(nk.es_gradient_work(pairs, out, inn), 1), device=device)
+    assert nk.es_gradient_work(pairs, out, inn) > 0
+    dbuf, doff, dw = buf.to(device), off.to(device), w_in.to(device)
+    bb, bo = (dbuf, doff + out) if inn > 1 else (None, None)
+    G1, G2, G0 = (torch.empty(out, inn, device=device) for _ in range(3))
+    nk.es_gradient(dw, dbuf, doff, bb, bo, out, inn, -1.0 / pairs, G1, work=work)
+    nk.es_gradient(dw, dbuf, doff, bb, bo, out, inn, -1.0 / pairs, G2, work=work)
+    nk.es_gradient(dw, dbuf, doff, bb, bo, out, inn, -1.0 / pairs, G0)
+    torch.testing.assert_close(G1.cpu().double(), ref.reshape(out, inn), rtol=1e-5, atol=1e-6)
+    assert torch.equal(G1, G2)
+    torch.testing.assert_close(G1, G0, rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize('window', [1024, 2048])
 def test_config2_attention_full_size(device, window):
     """Config 2 at its full shape: q, k, v [256 members, 8 heads, 2048 tokens, 64] ~ N(0, 1) bf16.
