@@ -53,6 +53,7 @@ class Eggroll:
             off += n
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.grad_work = None  # es_gradient's split-sum workspace, sized on the first step
+        self._layout = None    # column layout of the per-chunk noise gather
 
     def offsets(self, step):
         g = torch.Generator(self.device).manual_seed(1_000_003 * self.seed + step)
@@ -69,13 +70,27 @@ class Eggroll:
         return out
 
     def _pair_rows(self, offsets, directions):
+        """name -> NoiseRows for the pairs `directions`: one gather of every parameter's [out + in]
+        block side by side (each block's first column a multiple of 4 floats, so every a and b view
+        starts 16-byte aligned), instead of one gather per parameter."""
+        if self._layout is None:
+            widths = [sum(s) for s in self.shapes.values()]
+            padded = [-(-w // 4) * 4 for w in widths]
+            starts = [sum(padded[:k]) for k in range(len(padded))]
+            # column c of the block reads buffer[offset of parameter pid[c] + local[c]]; the pad
+            # columns repeat their block's last element and are never read
+            pid = torch.cat([torch.full((p,), k, dtype=torch.int64) for k, p in enumerate(padded)])
+            local = torch.cat([torch.arange(p).clamp(max=w - 1) for w, p in zip(widths, padded)])
+            self._layout = (pid.to(self.device), local.to(self.device), starts)
+        pid, local, starts = self._layout
+        table = torch.stack([offsets[name] for name in self.shapes])[:, directions].t()   # [n, params]
+        block = self.buffer[table[:, pid] + local]
         out = {}
-        for name, shape in self.shapes.items():
-            rows = self.buffer[offsets[name][directions, None] + torch.arange(sum(shape), device=self.device)]
+        for (name, shape), st in zip(self.shapes.items(), starts):
             if len(shape) == 2:
-                out[name] = NoiseRows(a=rows[:, :shape[0]], b=rows[:, shape[0]:], shift=1)
+                out[name] = NoiseRows(a=block[:, st:st + shape[0]], b=block[:, st + shape[0]:st + sum(shape)], shift=1)
             else:
-                out[name] = NoiseRows(eps=rows, shift=1)
+                out[name] = NoiseRows(eps=block[:, st:st + shape[0]], shift=1)
         return out
 
     @torch.no_grad()
