@@ -293,29 +293,29 @@ def test_chain_chunk_routed_bad_position_gives_nan(device):
     assert torch.equal(bad[:2], good[:2])
 
 
-@pytest.mark.parametrize('m,P_,K', [(4, 70, 64), (3, 300, 37), (2, 5, 1)])
-def test_chain_query_step_matches_oracle(device, m, P_, K):
+@pytest.mark.parametrize('m,P_,K,W', [(4, 70, 64, 512), (3, 300, 37, 512), (2, 5, 1, 512), (3, 40, 64, 256)])
+def test_chain_query_step_matches_oracle(device, m, P_, K, W):
     """The own-query step alone (noise_chain_query, mix off): the change it adds to delta against
     query_change_routed with the reference's bf16 casts (build). The reference runs the step's
     three float32 products on TF32 inputs; the kernels run them as bf16 hi/lo triples (2^-16
     relative against TF32's 2^-11), so the GPU is held to twice the tf32 envelope |build - tf32|
     at its largest and to half of it on average."""
-    own = _routed_own(m, 1, K, seed=m * P_ + K)
+    own = _routed_own(m, 1, K, seed=m * P_ + K, W=W)
     g = torch.Generator().manual_seed(K)
-    delta = torch.randn(m, P_, 512, generator=g) * 0.05
-    dev_delta = delta.reshape(m * P_, 512).to(device)
-    step = _probes()._routed_query(_own_to(own, device), m, P_, 512, 1, dev_delta.device)
+    delta = torch.randn(m, P_, W, generator=g) * 0.05
+    dev_delta = delta.reshape(m * P_, W).to(device)
+    step = _probes()._routed_query(_own_to(own, device), m, P_, W, 1, dev_delta.device)
     step(0, dev_delta, None, 0, 1.0, 0.0)
-    got = (dev_delta.cpu().double().reshape(m, P_, 512) - delta.double()).numpy()
+    got = (dev_delta.cpu().double().reshape(m, P_, W) - delta.double()).numpy()
     torch.cuda.synchronize()
     sub = _own_to(own, rows=np.arange(m))
     args = (sub[2][0], delta.double().numpy(), sub[1], sub[3][0], sub[4][0], sub[5][0], sub[6][0], sub[7][0],
-            sub[8][0], sub[9][0], sub[9][1])
+            sub[8][0], sub[9][0], sub[9][1], W)
     want = P.query_change_routed(*args, policy='build')
     env = np.abs(want - P.query_change_routed(*args, policy='tf32'))
     err = np.abs(got - want)
     scale = np.abs(want).max()
-    print(f'query step m {m} P {P_} K {K}: max |gpu - build| {err.max():.3e} (tf32 envelope {env.max():.3e}), '
+    print(f'query step m {m} P {P_} K {K} W {W}: max |gpu - build| {err.max():.3e} (tf32 envelope {env.max():.3e}), '
           f'mean {err.mean():.3e} (tf32 envelope {env.mean():.3e}), max |want| {scale:.3e}')
     assert err.max() <= 2 * env.max()
     assert err.mean() <= 0.5 * env.mean()
@@ -352,23 +352,25 @@ def _window_to(own, device=None):
             conv(sin), windows)
 
 
-@pytest.mark.parametrize('m,P_,S,window', [(6, 70, 300, 128), (4, 150, 1100, 1024), (3, 5, 40, 0)])
-def test_chain_query_window_step_matches_oracle(device, m, P_, S, window):
+@pytest.mark.parametrize('m,P_,S,window,W', [(6, 70, 300, 128, 512), (4, 150, 1100, 1024, 512), (3, 5, 40, 0, 512),
+                                            (3, 33, 50, 20, 256)])
+def test_chain_query_window_step_matches_oracle(device, m, P_, S, window, W):
     """The key-window own-query step alone (noise_chain_query_window, mix off) against query_change
     with the reference's bf16 casts: windows of 129 and 1025 keys (17 blocks of 64), tokens at the
     window's start, bound and end. Bar as the routed step: twice the tf32 envelope at its largest,
     half of it on average. Window 0 (the token's own key only): a softmax over one key cannot
     change, so the step must add (float32 rounding of) nothing."""
-    own = _window_own(m, 1, S, [window], seed=m * P_ + S)
+    own = _window_own(m, 1, S, [window], seed=m * P_ + S, W=W)
     g = torch.Generator().manual_seed(S)
-    delta = torch.randn(m, P_, 512, generator=g) * 0.05
-    dev_delta = delta.reshape(m * P_, 512).to(device)
-    step = _probes()._window_query(_window_to(own, device), m, P_, 512, 1, dev_delta.device)
+    delta = torch.randn(m, P_, W, generator=g) * 0.05
+    dev_delta = delta.reshape(m * P_, W).to(device)
+    step = _probes()._window_query(_window_to(own, device), m, P_, W, 1, dev_delta.device)
     step(0, dev_delta, None, 0, 1.0, 0.0)
-    got = (dev_delta.cpu().double().reshape(m, P_, 512) - delta.double()).numpy()
+    got = (dev_delta.cpu().double().reshape(m, P_, W) - delta.double()).numpy()
     torch.cuda.synchronize()
     o = _window_to(own)
-    args = (o[3][0], delta.double().numpy(), o[1], o[2][0], o[4][0], o[5][0], o[6][0], o[7][0], o[8], o[9], window)
+    args = (o[3][0], delta.double().numpy(), o[1], o[2][0], o[4][0], o[5][0], o[6][0], o[7][0], o[8], o[9], window,
+            W)
     want = P.query_change(*args, policy='build')
     if window == 0:
         print(f'window step m {m} P {P_} window 0: max |gpu| {np.abs(got).max():.3e}')
