@@ -356,17 +356,28 @@ struct ChainQuery {
 
 constexpr int QLD = 72;  // LDS row of a 64-wide bf16 tile, padded by 16 bytes (conflict-free reads)
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// Value tiles [64 keys][64 dims] with chunk c (8 dims) of row r at c ^ (2 (r & 3)): the
+// transposing reads below (16 lanes: 4 consecutive keys x 2 adjacent chunks) touch 8 distinct
+// chunk positions.
+NOISE_DEV int vswz(int row, int chunk) { return row * 64 + ((chunk ^ (2 * (row & 3))) << 3); }
+
 // Workgroup (row tile, head h, token i), four waves of 32 moves each (train/val/run.py:290-303):
 //   dr, r0 rotated; inv0, inv from |r0|^2, r0.dr, |dr|^2; dq = bf16(dr inv + r0 (inv - inv0))
-//   ds = bf16(dq K^T) / 8                         (32 x 64 MFMA per wave, keys zero-padded to 64)
-//   dlse = log1p(sum_k p_k expm1(ds_k)), w = bf16(p expm1(ds - dlse))
-//   dout = bf16(w V) + expm1(-dlse) rest          (32 x 64 MFMA per wave)
+//   ds = bf16(dq k_t) / 8 for the token's K <= 64 top keys (zero-padded to 64, p = 0 there),
+//   formed transposed, ds^T = K dq^T, so a lane owns one move and 16 keys of each 32-key half
+//   dlse = log1p(sum_t p_t expm1(ds_t)), w = bf16(p expm1(ds - dlse)) packed in registers as the
+//   B operand of dout^T = V^T w^T (V^T read with ds_read_b64_tr_b16, as in the window step)
+//   dout = bf16(w V) + expm1(-dlse) rest
 // written as A3 of the output projection's product. A position outside [0, T) gives NaN.
 __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery g) {
-  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];     // keys [key][dim]
-  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * QLD];     // values transposed [dim][key]
-  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq, then w
-  __shared__ float r0s[64], ps[64], rs[64], cs[32], sn[32], dls[4][32], inv0s;
+  __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];     // keys [key][dim], padded rows
+  __shared__ __attribute__((aligned(16))) uint16_t vts[64 * 64];     // values [key][dim], vswz chunks
+  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq
+  __shared__ __attribute__((aligned(16))) float ps[64];
+  __shared__ float r0s[64], rs[64], cs[32], sn[32], inv0s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = blockIdx.z, h = blockIdx.y;
@@ -377,19 +388,14 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
   const int64_t ih = (int64_t)i * g.heads + h;
   const int64_t kv0 = ih * g.K * 64;
   for (int e = tid; e < 64 * 8; e += 256) {
-    const int k = e >> 3, c = (e & 7) * 8;
+    const int k = e >> 3, c = e & 7;
     uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = kv;
     if (k < g.K) {
-      kv = *reinterpret_cast<const uint4*>(g.keys + kv0 + k * 64 + c);
-      vv = *reinterpret_cast<const uint4*>(g.vals + kv0 + k * 64 + c);
+      kv = *reinterpret_cast<const uint4*>(g.keys + kv0 + k * 64 + 8 * c);
+      vv = *reinterpret_cast<const uint4*>(g.vals + kv0 + k * 64 + 8 * c);
     }
-    *reinterpret_cast<uint4*>(kt + k * QLD + c) = kv;
-    const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      vt[(c + 2 * j) * QLD + k] = (uint16_t)(w4[j] & 0xffffu);
-      vt[(c + 2 * j + 1) * QLD + k] = (uint16_t)(w4[j] >> 16);
-    }
+    *reinterpret_cast<uint4*>(kt + k * QLD + 8 * c) = kv;
+    *reinterpret_cast<uint4*>(vts + vswz(k, c)) = vv;
   }
   if (tid < 64) {
     ps[tid] = tid < g.K ? g.top_p[ih * g.K + tid] : 0.f;
@@ -399,7 +405,7 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
     sn[tid - 64] = g.sin_t[pc * 32 + tid - 64];
   }
   __syncthreads();
-  if (tid < 64) {  // the clean rotated query of this head and inv0
+  if (tid < 64) {  // the clean rotated query of this head and |r0|^2
     const float* cr = g.dr + ((int64_t)g.m * g.P + i) * g.W + h * 64;
     const int c = tid & 31;
     const float u1 = cr[c], u2 = cr[c + 32];
@@ -452,104 +458,122 @@ __global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery 
       *reinterpret_cast<uint4*>(dst + 32 + c0 + t) = w2;
     }
   }
-  __syncthreads();
-
-  // ds = bf16(dq K^T) / 8; lane l holds keys ni * 32 + l % 32 of rows 8 (j / 4) + 4 (l / 32) + j % 4
-  const int fr = lane & 31, fk = 8 * (lane >> 5);
-  floatx16 acc[2];
+  __syncthreads();  // dq tiles complete
+  const int fr = lane & 31, half = lane >> 5, fk = 8 * half;
+  bf16x8 qf[4];  // B operand: move fr, dims 16 ks + 8 half .. + 7
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni)
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+  // ds^T of both 32-key halves: key 32 kb2 + 8 (j / 4) + 4 half + j % 4 for move fr
+  floatx16 ds[2];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+  for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+    for (int j = 0; j < 16; ++j) ds[kb2][j] = 0.f;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(kt + (ni * 32 + fr) * QLD + 16 * ks + fk);
-      acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ni], 0, 0, 0);
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + (32 * kb2 + fr) * QLD + 16 * ks + fk);
+      ds[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], ds[kb2], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ds[kb2][j] = bf2f(f2bf(ds[kb2][j])) * 0.125f;
+  }
+  float es = 0.f;
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2) {
+    const floatx16 em = noise::expm1_small16(ds[kb2]);
+    const float* pp = ps + 32 * kb2 + 4 * half;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const float4 p = *reinterpret_cast<const float4*>(pp + 8 * g4);
+      es += p.x * em[4 * g4] + p.y * em[4 * g4 + 1] + p.z * em[4 * g4 + 2] + p.w * em[4 * g4 + 3];
     }
   }
-  const float p_0 = ps[fr], p_1 = ps[32 + fr];
-  float es[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    acc[0][j] = bf2f(f2bf(acc[0][j])) * 0.125f;
-    acc[1][j] = bf2f(f2bf(acc[1][j])) * 0.125f;
-  }
+  const float dl = log1pf(es + __shfl_xor(es, 32, 64));
+  // V^T fragment offsets: as in the window step
+  int vfo[2];
   {
-    const floatx16 e0 = noise::expm1_small16(acc[0]), e1 = noise::expm1_small16(acc[1]);
+    const int s16 = lane & 15, a = s16 & 3, e = s16 >> 2, gq = lane >> 4;
+    const int key = 4 * (gq >> 1) + e;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) es[j] = p_0 * e0[j] + p_1 * e1[j];
+    for (int db = 0; db < 2; ++db) vfo[db] = vswz(key, 4 * db + 2 * (gq & 1) + (a >> 1)) + 4 * (a & 1);
   }
-  {
-    const float tot = noise::halfwave_transpose_sum16(es, lane);
-    const int jj = fr >> 1;
-    if ((lane & 1) == 0) dls[wave][8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3)] = log1pf(tot);
-  }
-  __syncthreads();  // dls complete; every wave is done reading its dq tile
-  float dl[16];
+  floatx16 o[2];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    dl[j] = dls[wave][8 * (j >> 2) + 4 * (lane >> 5) + (j & 3)];
-    acc[0][j] -= dl[j];
-    acc[1][j] -= dl[j];
-  }
-  {
-    const floatx16 e0 = noise::expm1_small16(acc[0]), e1 = noise::expm1_small16(acc[1]);
+  for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-      at[wave][row * QLD + fr] = f2bf(p_0 * e0[j]);
-      at[wave][row * QLD + 32 + fr] = f2bf(p_1 * e1[j]);
+    for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2) {
+    floatx16 x = ds[kb2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] -= dl;
+    const floatx16 em = noise::expm1_small16(x);
+    const float* pp = ps + 32 * kb2 + 4 * half;
+    bf16x8 pf[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const float4 pa = *reinterpret_cast<const float4*>(pp + 16 * kk);
+      const float4 pb = *reinterpret_cast<const float4*>(pp + 16 * kk + 8);
+      const int j0 = 8 * kk;
+      u32x4 pk;
+      pk[0] = pack_bf2(pa.x * em[j0], pa.y * em[j0 + 1]);
+      pk[1] = pack_bf2(pa.z * em[j0 + 2], pa.w * em[j0 + 3]);
+      pk[2] = pack_bf2(pb.x * em[j0 + 4], pb.y * em[j0 + 5]);
+      pk[3] = pack_bf2(pb.z * em[j0 + 6], pb.w * em[j0 + 7]);
+      pf[kk] = __builtin_bit_cast(bf16x8, pk);
     }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const uint16_t* a0 = vts + 32 * kb2 * 64 + 16 * kk * 64 + vfo[db];
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(a0 + 8 * 64));
+        u32x4 u;
+        u[0] = __builtin_bit_cast(u32x2, lo)[0];
+        u[1] = __builtin_bit_cast(u32x2, lo)[1];
+        u[2] = __builtin_bit_cast(u32x2, hi)[0];
+        u[3] = __builtin_bit_cast(u32x2, hi)[1];
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u), pf[kk], o[db], 0, 0, 0);
+      }
   }
+  // lane: move fr, dims 32 db + 8 (j / 4) + 4 half + j % 4; the hi and lo halves go through LDS
+  // (at for hi; kt or vts, free once every wave is past its products, for lo) for 16-byte stores
   __syncthreads();
-
-  // dout = bf16(w V) + expm1(-dlse) rest; lane l holds dims ni * 32 + l % 32
+  {
+    const float nan = __builtin_nanf("");
+    const float em = noise::expm1_small(-dl);
+    uint16_t* hi_t = at[wave];
+    uint16_t* lo_t = wave < 2 ? kt + (wave & 1) * 32 * QLD : vts + (wave & 1) * 32 * 64;
+    const int lls = wave < 2 ? QLD : 64;
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[ni][j] = 0.f;
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * db + 8 * g4 + 4 * half;
+        float4 v;
+        v.x = pos_ok ? bf2f(f2bf(o[db][4 * g4])) + em * rs[d0] : nan;
+        v.y = pos_ok ? bf2f(f2bf(o[db][4 * g4 + 1])) + em * rs[d0 + 1] : nan;
+        v.z = pos_ok ? bf2f(f2bf(o[db][4 * g4 + 2])) + em * rs[d0 + 2] : nan;
+        v.w = pos_ok ? bf2f(f2bf(o[db][4 * g4 + 3])) + em * rs[d0 + 3] : nan;
+        uint2 hv, lv;
+        split4(v, hv, lv);
+        *reinterpret_cast<uint2*>(hi_t + fr * QLD + d0) = hv;
+        *reinterpret_cast<uint2*>(lo_t + fr * lls + d0) = lv;
+      }
+    __syncthreads();
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(vt + (ni * 32 + fr) * QLD + 16 * ks + fk);
-      acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ni], 0, 0, 0);
+    for (int t = 0; t < 4; ++t) {
+      const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
+      const int p = pw + row;
+      if (p >= g.P) continue;
+      const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
+      const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * lls + c);
+      uint16_t* q = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
+      *reinterpret_cast<uint4*>(q) = hv;
+      *reinterpret_cast<uint4*>(q + g.W) = lv;
+      *reinterpret_cast<uint4*>(q + 2 * g.W) = hv;
     }
-  }
-  const float r_0 = rs[fr], r_1 = rs[32 + fr];
-  const float nan = __builtin_nanf("");
-  __syncthreads();  // every wave is done with kt and vt: they take the lo halves
-  uint16_t* hi_t = at[wave];
-  uint16_t* lo_t = (wave < 2 ? kt : vt) + (wave & 1) * 32 * QLD;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int row = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-    const float em = noise::expm1_small(-dl[j]);
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const float v = pos_ok ? bf2f(f2bf(acc[ni][j])) + em * (ni ? r_1 : r_0) : nan;
-      const uint16_t hv = f2bf(v);
-      hi_t[row * QLD + ni * 32 + fr] = hv;
-      lo_t[row * QLD + ni * 32 + fr] = f2bf(v - bf2f(hv));
-    }
-  }
-  __syncthreads();
-  // 16-byte stores: lane l moves chunk l % 8 of rows l / 8 + 8 t, into A3's hi, lo, hi segments
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
-    const int p = pw + row;
-    if (p >= g.P) continue;
-    const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
-    const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
-    uint16_t* o = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
-    *reinterpret_cast<uint4*>(o) = hv;
-    *reinterpret_cast<uint4*>(o + g.W) = lv;
-    *reinterpret_cast<uint4*>(o + 2 * g.W) = hv;
   }
 }
 
@@ -573,13 +597,6 @@ NOISE_DEV float wave_max(float v) {
   return v;
 }
 
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-// Value tiles [64 keys][64 dims] with chunk c (8 dims) of row r at c ^ (2 (r & 3)): the
-// transposing reads below (16 lanes: 4 consecutive keys x 2 adjacent chunks) touch 8 distinct
-// chunk positions.
-NOISE_DEV int vswz(int row, int chunk) { return row * 64 + ((chunk ^ (2 * (row & 3))) << 3); }
 
 // Workgroup (row tile, head h, token i), four waves of 32 moves each, over the n keys t with
 // 0 <= rel_i - t <= window (train/val/run.py:264-281):
@@ -824,15 +841,18 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
         }
     }
   }
-  // lane: move fr, dims 32 db + 8 (j / 4) + 4 half + j % 4
-  const int p = pw + fr;
-  if (p < g.P) {
+  // lane: move fr, dims 32 db + 8 (j / 4) + 4 half + j % 4; the hi and lo halves go through LDS
+  // (at for hi, the key buffers for lo once every wave is past its products) for 16-byte stores
+  __syncthreads();
+  {
     const float nan = __builtin_nanf("");
-    uint16_t* orow = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + 4 * half;
+    uint16_t* hi_t = at[wave];
+    uint16_t* lo_t = kts[wave >> 1] + (wave & 1) * 32 * QLD;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * db + 8 * g4 + 4 * half;
         float4 v;
         v.x = ok ? bf2f(f2bf(o[db][4 * g4])) : nan;
         v.y = ok ? bf2f(f2bf(o[db][4 * g4 + 1])) : nan;
@@ -840,11 +860,22 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
         v.w = ok ? bf2f(f2bf(o[db][4 * g4 + 3])) : nan;
         uint2 hv, lv;
         split4(v, hv, lv);
-        uint16_t* q = orow + 32 * db + 8 * g4;
-        *reinterpret_cast<uint2*>(q) = hv;
-        *reinterpret_cast<uint2*>(q + g.W) = lv;
-        *reinterpret_cast<uint2*>(q + 2 * g.W) = hv;
+        *reinterpret_cast<uint2*>(hi_t + fr * QLD + d0) = hv;
+        *reinterpret_cast<uint2*>(lo_t + fr * QLD + d0) = lv;
       }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int row = (lane >> 3) + 8 * t, c = (lane & 7) * 8;
+      const int p = pw + row;
+      if (p >= g.P) continue;
+      const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
+      const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
+      uint16_t* q = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
+      *reinterpret_cast<uint4*>(q) = hv;
+      *reinterpret_cast<uint4*>(q + g.W) = lv;
+      *reinterpret_cast<uint4*>(q + 2 * g.W) = hv;
+    }
   }
 }
 
