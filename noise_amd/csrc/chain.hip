@@ -611,11 +611,12 @@ NOISE_DEV float wave_max(float v) {
 //   a + 8, a + 12) in the key order the score accumulators hold.
 // dout = bf16(sum) is written as A3 of the output projection's product. A position outside
 // [0, T) or a window with no key gives NaN.
-__global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQueryWin g) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void chain_query_window_kernel(const ChainQueryWin g) {
   __shared__ __attribute__((aligned(16))) uint16_t kts[2][64 * QLD];  // keys [key][dim], padded rows
   __shared__ __attribute__((aligned(16))) uint16_t vts[2][64 * 64];   // values [key][dim], vswz chunks
-  __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq
   __shared__ __attribute__((aligned(16))) float p0s[QWMAX + 64];
+  // per wave: the dq tile, in the key buffers (free until the first key block lands)
+  uint16_t(*at)[32 * QLD] = reinterpret_cast<uint16_t(*)[32 * QLD]>(&kts[0][0]);
   __shared__ float r0s[64], cs[32], sn[32], red[8], inv0s;
   __shared__ __attribute__((aligned(16))) uint16_t q0s[64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -726,6 +727,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
   bf16x8 qf[4];  // B operand: this lane's move fr, dims 16 ks + 8 half .. + 7
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(at[wave] + fr * QLD + 16 * ks + fk);
+  __syncthreads();  // every wave holds its dq fragments: the key buffers take key blocks from here
   // V^T fragment offsets (within the value tile): in 16-lane group gq, lane a + 4 e addresses
   // key 4 (gq >> 1) + e (+ 16 kk + 32 kb2, + 8 for the second read), dims 32 db + 16 (gq & 1) + 4 a;
   // the lane then holds dim 32 db + lane % 32 for the keys its w values hold.
@@ -842,12 +844,13 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
     }
   }
   // lane: move fr, dims 32 db + 8 (j / 4) + 4 half + j % 4; the hi and lo halves go through LDS
-  // (at for hi, the key buffers for lo once every wave is past its products) for 16-byte stores
+  // (the key buffers for hi, the value buffers for lo, once every wave is past its products) for
+  // 16-byte stores
   __syncthreads();
   {
     const float nan = __builtin_nanf("");
     uint16_t* hi_t = at[wave];
-    uint16_t* lo_t = kts[wave >> 1] + (wave & 1) * 32 * QLD;
+    uint16_t* lo_t = &vts[0][0] + wave * 32 * 64;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -861,7 +864,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
         uint2 hv, lv;
         split4(v, hv, lv);
         *reinterpret_cast<uint2*>(hi_t + fr * QLD + d0) = hv;
-        *reinterpret_cast<uint2*>(lo_t + fr * QLD + d0) = lv;
+        *reinterpret_cast<uint2*>(lo_t + fr * 64 + d0) = lv;
       }
     __syncthreads();
 #pragma unroll
@@ -870,7 +873,7 @@ __global__ __launch_bounds__(256) void chain_query_window_kernel(const ChainQuer
       const int p = pw + row;
       if (p >= g.P) continue;
       const uint4 hv = *reinterpret_cast<const uint4*>(hi_t + row * QLD + c);
-      const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * QLD + c);
+      const uint4 lv = *reinterpret_cast<const uint4*>(lo_t + row * 64 + c);
       uint16_t* q = g.a3 + ((int64_t)i * g.P + p) * 3 * g.W + h * 64 + c;
       *reinterpret_cast<uint4*>(q) = hv;
       *reinterpret_cast<uint4*>(q + g.W) = lv;
