@@ -372,7 +372,7 @@ NOISE_DEV int vswz(int row, int chunk) { return row * 64 + ((chunk ^ (2 * (row &
 //   B operand of dout^T = V^T w^T (V^T read with ds_read_b64_tr_b16, as in the window step)
 //   dout = bf16(w V) + expm1(-dlse) rest
 // written as A3 of the output projection's product. A position outside [0, T) gives NaN.
-__global__ __launch_bounds__(256) void chain_query_attn_kernel(const ChainQuery g) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void chain_query_attn_kernel(const ChainQuery g) {
   __shared__ __attribute__((aligned(16))) uint16_t kt[64 * QLD];     // keys [key][dim], padded rows
   __shared__ __attribute__((aligned(16))) uint16_t vts[64 * 64];     // values [key][dim], vswz chunks
   __shared__ __attribute__((aligned(16))) uint16_t at[4][32 * QLD];  // per wave: dq
