@@ -83,6 +83,14 @@ def test_argument_errors_raise_before_launch():
     assert lib.noise_chain_query_window(C.byref(w), None) == _lib.NOISE_EINVAL   # NULL rel
     w.m = 0
     assert lib.noise_chain_query_window(C.byref(w), None) == _lib.NOISE_OK
+    # es_gradient: a workspace size without a workspace is rejected; the split sizing rule gives
+    # up to 16 pair splits per 64 x 64 tile and none for a handful of pairs.
+    assert lib.noise_es_gradient(fake, 1536, fake, fake, fake, fake, 512, 512, -1.0, 0, fake, None, 10,
+                                 None) == _lib.NOISE_EINVAL
+    assert lib.noise_es_gradient_work(1536, 512, 512) == 16 * 512 * 512
+    assert lib.noise_es_gradient_work(1536, 4096, 512) == 4 * 4096 * 512
+    assert lib.noise_es_gradient_work(37, 70, 90) == 0
+    assert lib.noise_es_gradient_work(0, 70, 90) == 0
 
 
 def test_state_dict_strict_round_trip():
