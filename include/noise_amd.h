@@ -267,8 +267,8 @@ typedef struct {
   int64_t ld_idx;
   const float* hs;         /* [m, ld_hs] their clean pre-activations */
   int64_t ld_hs;
-  const uint16_t* w_fc;    /* [H, W] bf16 c_fc.weight */
-  const uint16_t* w_out_t; /* [H, W] bf16 c_proj.weight transposed */
+  const uint16_t* w_fc;    /* [H, W] bf16 c_fc.weight (16-byte aligned) */
+  const uint16_t* w_out_t; /* [H, W] bf16 c_proj.weight transposed (16-byte aligned) */
   int m, P, W, k, H;       /* W % 256 == 0, W <= 2048, k % 128 == 0 */
   uint16_t* dz;            /* workspace [m * P, W] bf16 (16-byte aligned, as the next three) */
   uint16_t* wf;            /* workspace [m, k, W] bf16 */

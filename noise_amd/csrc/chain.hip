@@ -109,31 +109,35 @@ __global__ __launch_bounds__(256) void chain_pre_kernel(float* __restrict__ delt
 }
 
 // wf[i][kk][:] = w_fc[idx[i][kk]][:]  and  wo[i][n][kk] = w_out_t[idx[i][kk]][n], through LDS in
-// blocks of 64 columns. An index outside [0, H) gathers NaN.
+// blocks of 64 columns, in 16-byte pieces (8 bf16) both ways. An index outside [0, H) gathers NaN.
 __global__ __launch_bounds__(256) void chain_gather_kernel(const uint16_t* __restrict__ w_fc,
                                                            const uint16_t* __restrict__ w_out_t,
                                                            const int64_t* __restrict__ idx, int64_t ld_idx,
                                                            int k, int H, int W, uint16_t* __restrict__ wf,
                                                            uint16_t* __restrict__ wo) {
-  __shared__ uint16_t tile[256][65];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[256][72];  // [unit][column], padded rows
   const int64_t i = blockIdx.y;
   const int c0 = blockIdx.x * 64;
   const int tid = threadIdx.x;
-  const uint16_t NANBF = 0x7fc0;
+  const uint4 NAN8 = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
   for (int kb = 0; kb < k; kb += 256) {
-    const int kn = min(256, k - kb);
-    // rows kb .. kb + kn of the gathered sets, columns c0 .. c0 + 63
-    for (int e = tid; e < kn * 64; e += 256) {
-      const int kk = e / 64, c = e % 64;
+    const int kn = min(256, k - kb);  // a multiple of 8 (k is a multiple of 128)
+    for (int e = tid; e < kn * 8; e += 256) {  // unit kk, 8-column piece c8
+      const int kk = e >> 3, c8 = (e & 7) * 8;
       const int64_t u = idx[i * ld_idx + kb + kk];
       const bool ok = u >= 0 && u < H;
-      wf[(i * k + kb + kk) * W + c0 + c] = ok ? w_fc[u * W + c0 + c] : NANBF;
-      tile[kk][c] = ok ? w_out_t[u * W + c0 + c] : NANBF;
+      const uint4 a = ok ? *reinterpret_cast<const uint4*>(w_fc + u * W + c0 + c8) : NAN8;
+      const uint4 b = ok ? *reinterpret_cast<const uint4*>(w_out_t + u * W + c0 + c8) : NAN8;
+      *reinterpret_cast<uint4*>(wf + (i * k + kb + kk) * W + c0 + c8) = a;
+      *reinterpret_cast<uint4*>(&tile[kk][c8]) = b;
     }
     __syncthreads();
-    for (int e = tid; e < kn * 64; e += 256) {
-      const int c = e / kn, kk = e % kn;
-      wo[(i * W + c0 + c) * k + kb + kk] = tile[kk][c];
+    for (int e = tid; e < 64 * (kn >> 3); e += 256) {  // column c, 8-unit piece k8
+      const int c = e / (kn >> 3), k8 = (e % (kn >> 3)) * 8;
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (uint32_t)tile[k8 + 2 * j][c] | ((uint32_t)tile[k8 + 2 * j + 1][c] << 16);
+      *reinterpret_cast<uint4*>(wo + (i * W + c0 + c) * k + kb + k8) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     __syncthreads();
   }
@@ -1056,6 +1060,7 @@ extern "C" int noise_chain_block(const noise_chain_block_t* a, void* stream) {
   NOISE_REQUIRE(a->ld_idx >= a->k && a->ld_hs >= a->k, "chain_block: ld_idx / ld_hs below k");
   NOISE_REQUIRE(aligned16(a->dz) && aligned16(a->wf) && aligned16(a->wo) && aligned16(a->g),
                 "chain_block: workspace buffers must be 16-byte aligned");
+  NOISE_REQUIRE(aligned16(a->w_fc) && aligned16(a->w_out_t), "chain_block: w_fc and w_out_t must be 16-byte aligned");
   NOISE_REQUIRE(a->m <= 65535 && (int64_t)a->m * a->P < (1ll << 31), "chain_block: at most 65535 tokens per call");
   const hipStream_t st = (hipStream_t)stream;
   const int rows = a->m * a->P;

@@ -137,7 +137,8 @@ def _dev_f32(t, shape, name):
 def _dev_bf16(t, shape, name):
     _need(t.is_cuda, f'{name}: libnoise_amd kernels take device tensors')
     _need(tuple(t.shape) == tuple(shape), f'{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}')
-    return t.to(torch.bfloat16).contiguous()
+    t = t.to(torch.bfloat16).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()  # the kernels read 16-byte pieces
 
 
 def chain_chunk(site, move, scale, e, x0, mids, xL, idx, hs, lam_r, lam_0, w_fc, w_out_t, weight_t, base,
