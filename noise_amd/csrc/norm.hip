@@ -16,7 +16,7 @@ constexpr int D = 512;
 
 // Sum over a fully active wave: 16-lane row sums by DPP (quad_perm [1,0,3,2], quad_perm
 // [2,3,0,1], row_half_mirror, row_mirror), then the four rows' totals through readlane. No LDS
-// traffic, unlike the shuffle-based sum (measured on the step: 5 ms less per step in mix_norm).
+// traffic, unlike the shuffle-based sum.
 template <int CTRL>
 NOISE_DEV float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
