@@ -267,8 +267,47 @@ def bench_probe_chain(steps, warmup, m=256, P=512, L=8, W=512, H=2048, k=128, V=
                      'kernel': 'one chain_chunk call (start + 8 blocks + head)', 'flops_per_call': flops,
                      'call_ms': call_ms},
         'finite': bool(torch.isfinite(out).all()),
+        'cpu_baseline': cpu_baseline_chain(args, P, tokens=2 if own == 'window' else 8),
     }
     print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_chain(args, P, tokens=8):
+    """The oracle's chain_chunk (numpy float32 with the reference's bf16 casts) on the first
+    `tokens` tokens of the same chunk, every move, the same own mode."""
+    from oracle import probes_ref as R
+    sl = slice(0, tokens)
+    f = lambda t: t.detach().cpu().double().numpy() if t.is_floating_point() else t.detach().cpu().numpy()
+    tok = {'move', 'scale', 'e', 'x0', 'xL', 'base', 'target_logit_w', 'y'}
+    per_tok_lists = {'mids', 'idx', 'hs'}
+    kw = {}
+    for key, v in args.items():
+        if key == 'own':
+            continue
+        if key in tok:
+            kw[key] = f(v[sl])
+        elif key in per_tok_lists:
+            kw[key] = [f(t[sl]) for t in v]
+        elif isinstance(v, list):
+            kw[key] = [f(t) for t in v]
+        else:
+            kw[key] = f(v)
+    own = args.get('own')
+    if own is not None and own[0] == 'routed':
+        _, pos, inputs, w_q, keys, vals, probs, rests, w_proj_t, (cos, sin) = own
+        kw['own'] = ('routed', f(pos[sl]), [f(t[sl]) for t in inputs], [f(t) for t in w_q], [f(t[sl]) for t in keys],
+                     [f(t[sl]) for t in vals], [f(t[sl]) for t in probs], [f(t[sl]) for t in rests],
+                     [f(t) for t in w_proj_t], (f(cos), f(sin)))
+    elif own is not None:
+        _, pos, rels, inputs, w_q, keys, vals, w_proj_t, cos, sin, windows = own
+        kw['own'] = ('window', f(pos[sl]), [f(t[sl]) for t in rels], [f(t[sl]) for t in inputs], [f(t) for t in w_q],
+                     [f(t) for t in keys], [f(t) for t in vals], [f(t) for t in w_proj_t], f(cos), f(sin), windows)
+    t0 = time.perf_counter()
+    R.chain_chunk(-1, **kw, policy='build32')
+    dt = time.perf_counter() - t0
+    return {'value': tokens * P / dt, 'unit': 'moves/s', 'cores': os.cpu_count() or 1, 'kind': 'port',
+            'sample': f'oracle chain_chunk in numpy float32 (bf16 casts kept) on {tokens} tokens x {P} moves of '
+                      'the same chunk, same own mode; numpy may use every host core'}
 
 
 def cpu_baseline_probe(n, P, V, tokens=768):
