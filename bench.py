@@ -1,7 +1,7 @@
 """Benchmark: perturbed member-tokens/s of one MI355X on the full EGGROLL population step.
 
     python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
-    python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the MLP pair
+    python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the fused MLP
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
     python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
     python bench.py --probe-chain    # chain_chunk (attention held) at the Cut estimator's shape, own JSON line
@@ -15,9 +15,10 @@ the fitness, the rank-1 gradient rebuild and an AdamW update of all weights. A s
 `Eggroll.step`. Weights are the seeded initialisation; tokens are synthetic.
 
 Printed: one JSON line. `value` = members * tokens * steps / wall time of the timed steps (inputs
-resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (c_fc GEMM with the
-rank-1 + relu^2 epilogue, then the c_proj GEMM with the rank-1 + residual epilogue): algorithmic
-FLOPs per launch pair / its mean duration, timed live with HIP events on the launch stream.
+resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (`mlp_fused`: norm,
+c_fc with its rank-1 term, relu^2, c_proj with its rank-1 term and the residual add in one launch,
+the hidden kept on chip): algorithmic FLOPs per launch / its mean duration, timed live with HIP
+events on the launch stream.
 `cpu_baseline` times the CPU oracle (oracle/model_ref.py, float32) on a bounded sample of the same
 workload on this host.
 """
@@ -33,12 +34,12 @@ import torch
 
 PEAK_BF16 = 2.5e15  # dense bf16 MFMA, MI355X
 ROOT = Path(__file__).resolve().parent
-TRAFFIC_FILE = ROOT / 'profiles' / 'lowrank_gemm_mlp_pair_traffic.md'
+TRAFFIC_FILE = ROOT / 'profiles' / 'mlp_fused_traffic.md'
 
 
 def mlp_flops(rows, d=512, f=2048):
-    """Algorithmic FLOPs of one fused-MLP launch pair over `rows` member-token rows: both GEMMs
-    (2 d f each) plus the two rank-1 epilogues (2 f + 2 d), per row."""
+    """Algorithmic FLOPs of one fused-MLP launch over `rows` member-token rows: both GEMMs (2 d f
+    each) plus the two rank-1 terms (2 f + 2 d), per row."""
     return rows * (4 * d * f + 2 * (d + f))
 
 
@@ -53,18 +54,41 @@ def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 
 
 
 def mlp_traffic():
-    """HBM bytes per fused-MLP launch pair measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    """HBM bytes per fused-MLP launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (scaled by the same counters on a copy of known size), as recorded in the profile summary."""
     if not TRAFFIC_FILE.exists():
         return None
-    m = re.search(r'^traffic_bytes_per_launch_pair:\s*([0-9]+)', TRAFFIC_FILE.read_text(), re.M)
+    m = re.search(r'^traffic_bytes_per_launch:\s*([0-9]+)', TRAFFIC_FILE.read_text(), re.M)
     return int(m.group(1)) if m else None
 
 
-def probe_mlp(rows=512 * 2048, d=512, f=2048, reps=3):
+def mlp_inputs(rows=512 * 2048, d=512, f=2048, seed=0):
+    """The fused MLP's inputs at the bench shape: 512 members x 2048 tokens of an N(0, 1) fp32
+    stream, N(0, 1/fan_in) weights, pair-shared N(0, 1) noise rows, sigma = 1e-3."""
+    from noise_amd import kernels as K
+    from noise_amd.kernels import NoiseRows
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    members, T = rows // 2048, 2048
+    nrows = members // 2
+    w_fc32 = torch.randn(f, d, device=dev, generator=g) / d ** 0.5
+    w_pr32 = torch.randn(d, f, device=dev, generator=g) / f ** 0.5
+    w_fc = torch.empty(K.MLP_PACKED_ELEMS, device=dev, dtype=torch.bfloat16)
+    w_pr = torch.empty(K.MLP_PACKED_ELEMS, device=dev, dtype=torch.bfloat16)
+    K.mlp_pack(w_fc32, w_fc, w_pr32, w_pr)
+    sign = torch.tensor([1e-3, -1e-3], device=dev).repeat(members // 2)
+    fc = NoiseRows(a=torch.randn(nrows, f, device=dev, generator=g), b=torch.randn(nrows, d, device=dev, generator=g),
+                   shift=1)
+    pr = NoiseRows(a=torch.randn(nrows, d, device=dev, generator=g), b=torch.randn(nrows, f, device=dev, generator=g),
+                   shift=1)
+    x = torch.randn(rows, d, device=dev, generator=g)
+    return dict(x=x, T=T, members=members, w_fc=w_fc, w_pr=w_pr, sign=sign, fc=fc, pr=pr)
+
+
+def probe_mlp(reps=3):
     """Counter-collection workload: `reps` copies of a 1 GiB fp32 buffer (1 GiB read + 1 GiB
-    written per dispatch), then `reps` fused-MLP launch pairs at the bench shape (512 members x
-    2048 tokens, pair-shared noise rows), with the same kernels and epilogues as the step."""
+    written per dispatch), then `reps` fused-MLP launches at the bench shape (512 members x 2048
+    tokens, pair-shared noise rows), the step's kernel and flags."""
     import noise_amd  # noqa: F401  (loads the library)
     from noise_amd import _lib
     from noise_amd import kernels as K
@@ -75,25 +99,12 @@ def probe_mlp(rows=512 * 2048, d=512, f=2048, reps=3):
     for _ in range(reps):
         dst.copy_(src)
     del src, dst
-    members, T = rows // 2048, 2048
-    nrows = members // 2
-    h = torch.randn(rows, d, device=dev, generator=g).bfloat16()
-    w_fc = (torch.randn(f, d, device=dev, generator=g) / d ** 0.5).bfloat16()
-    w_pr = (torch.randn(d, f, device=dev, generator=g) / f ** 0.5).bfloat16()
-    sign = torch.tensor([1e-3, -1e-3], device=dev).repeat(members // 2)
-    a_fc, b_pr = torch.randn(nrows, f, device=dev, generator=g), torch.randn(nrows, f, device=dev, generator=g)
-    a_pr = torch.randn(nrows, d, device=dev, generator=g)
-    u1 = torch.randn(rows, device=dev, generator=g)
-    hid = torch.empty(rows, f, device=dev, dtype=torch.bfloat16)
-    umlp = torch.empty(rows, f // 64, device=dev)
-    x = torch.randn(rows, d, device=dev, generator=g)
+    a = mlp_inputs()
     for _ in range(reps):
-        r1 = K.rank1(sign, T, [a_fc], [u1], 1, 1, 1)
-        K.lowrank_gemm(h, w_fc, r1, _lib.EPI_RELU2_BF16, hid, b_pr, umlp)
-        r1 = K.rank1(sign, T, [a_pr], [umlp], umlp.shape[1], umlp.shape[1], 1)
-        K.lowrank_gemm(hid, w_pr, r1, _lib.EPI_ADD_F32, x)
+        K.mlp_fused(a['x'], a['x'], a['T'], a['members'], a['w_fc'], a['w_pr'], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
+                    a['sign'], a['fc'], a['pr'])
     torch.cuda.synchronize()
-    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x MLP pair over {rows} rows', flush=True)
+    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused over {a["x"].shape[0]} rows', flush=True)
 
 
 def probe_attention(members=512, T=2048, reps=2):
@@ -407,12 +418,10 @@ def main():
     elapsed = time.perf_counter() - t0
     probe, es.engine.probe = es.engine.probe, None
 
-    fc_ms = sum(a.elapsed_time(b) for a, b, _, _ in probe) / len(probe)
-    mp_ms = sum(b.elapsed_time(c) for _, b, c, _ in probe) / len(probe)
-    rows = probe[0][3]
+    mlp_ms = sum(a.elapsed_time(b) for a, b, _ in probe) / len(probe)
+    rows = probe[0][2]
     flops = mlp_flops(rows)
-    pair_s = (fc_ms + mp_ms) / 1e3
-    achieved = flops / pair_s / 1e12
+    achieved = flops / (mlp_ms / 1e3) / 1e12
     members = 2 * pairs
     value = members * T * args.steps / elapsed
     out = {
@@ -433,9 +442,8 @@ def main():
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
                      'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(),
-                     'kernel': 'fused relu^2 MLP: lowrank_gemm<RELU2> (c_fc) + lowrank_gemm<ADD_F32,K=2048> (c_proj)',
-                     'flops_per_launch': flops, 'rows_per_launch': rows,
-                     'launch_ms': {'c_fc': fc_ms, 'c_proj': mp_ms}},
+                     'kernel': 'mlp_fused: norm + c_fc + rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip',
+                     'flops_per_launch': flops, 'rows_per_launch': rows, 'launch_ms': mlp_ms},
         'step_tflops': step_flops(members, T) / (elapsed / args.steps) / 1e12,
         'mean_loss': losses[-1],
     }

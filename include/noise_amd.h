@@ -65,6 +65,45 @@ int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_
                        void* C, int64_t ldc, const float* b_next, int64_t ld_bnext,
                        float* u_next, int64_t ld_unext, void* stream);
 
+/* ---- fused relu^2 MLP -------------------------------------------------------------------- */
+#define NOISE_MLP_NORM 1     /* h = bf16(norm(in)) (RMSNorm, no gain); else h = bf16(in) */
+#define NOISE_MLP_RESIDUAL 2 /* out = in + mlp(h); else out = mlp(h) */
+typedef struct {
+  const float* in;           /* fp32 [*, 512]: row t of member p at in + p*member_stride_in + t*ld_in */
+  int64_t ld_in, member_stride_in; /* member_stride_in 0: one set of rows shared by every member */
+  float* out;                /* fp32 [*, 512], indexed alike with ld_out / member_stride_out; may be in */
+  int64_t ld_out, member_stride_out;
+  int T, members, flags;
+  const uint16_t* w_fc;      /* mlp.c_fc.weight as packed by noise_mlp_pack */
+  const uint16_t* w_proj;    /* mlp.c_proj.weight as packed by noise_mlp_pack */
+  const float* sign;         /* [members] +-sigma; NULL = unperturbed */
+  int member_shift;          /* noise row of member p = p >> member_shift */
+  const float* a_fc;         /* [noise rows, 2048] (c_fc out) */
+  int64_t ld_a_fc;
+  const float* b_fc;         /* [noise rows, 512] (c_fc in) */
+  int64_t ld_b_fc;
+  const float* a_proj;       /* [noise rows, 512] (c_proj out) */
+  int64_t ld_a_proj;
+  const float* b_proj;       /* [noise rows, 2048] (c_proj in) */
+  int64_t ld_b_proj;
+} noise_mlp_t;
+
+/* out = [in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 in one launch, the [rows, 2048] hidden
+ * kept on chip: replaces `x + lowrank(c_proj, relu(lowrank(c_fc, norm(x)))^2)`
+ * (train/val/eggroll.py:93 with `lowrank` eggroll.py:56-58; utils/model.py:100-107). Cast points:
+ * h and the relu^2 hidden are rounded to bf16 (GEMM operands), the rank-1 dots use those rounded
+ * values with fp32 b, everything else is fp32. in, w_fc, w_proj and the noise rows must be
+ * 16-byte aligned (leading dimensions multiples of 4 floats). */
+int noise_mlp_fused(const noise_mlp_t* args, void* stream);
+
+/* Packs the MLP weights into the bf16 operand layouts noise_mlp_fused reads (each 2 MiB, 16-byte
+ * aligned; either pair of pointers may be NULL): mlp.c_fc.weight (fp32 [2048, ld_fc >= 512]) as
+ * [2048][512] and mlp.c_proj.weight (fp32 [512, ld_proj >= 2048]) as [64 chunks][512][32], both
+ * with every 16-deep k-step in the order the fused kernel's MFMA accumulators deliver it. No
+ * counterpart in the reference: the weight-copy step of the bf16 GEMMs (autocast, eggroll.py:144). */
+int noise_mlp_pack(const float* w_fc, int64_t ld_fc, const float* w_proj, int64_t ld_proj,
+                   uint16_t* fc_packed, uint16_t* proj_packed, void* stream);
+
 /* ---- embedding ------------------------------------------------------------------------ */
 /* x0[p*T + t] = norm(W[i] + sign[p] a_p[i] b_p) with i = idx[p*idx_stride + t] (idx_stride 0:
  * one sequence shared by every member), fp32 [members*T, d]; x (if not NULL) receives a copy.

@@ -11,6 +11,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libnoise_amd.so'
 
 NOISE_OK, NOISE_EINVAL, NOISE_EHIP, NOISE_ENONFINITE = 0, 1, 2, 3
 EPI_BF16, EPI_F32, EPI_ADD_F32, EPI_RELU2_BF16 = 0, 1, 2, 3
+MLP_NORM, MLP_RESIDUAL = 1, 2
 
 P = C.c_void_p
 I64 = C.c_int64
@@ -36,6 +37,13 @@ class Rope(C.Structure):
     _fields_ = [('qkv', P), ('out', P), ('M', INT), ('T', INT), ('member_shift', INT), ('cos', P),
                 ('sin', P), ('gate', P), ('ve_table', P), ('idx', P), ('idx_stride', I64), ('vocab', INT), ('sign', P),
                 ('ve_a', P), ('ve_b', P), ('ld_ve_a', I64), ('ld_ve_b', I64)]
+
+
+class Mlp(C.Structure):
+    _fields_ = [('in_', P), ('ld_in', I64), ('member_stride_in', I64), ('out', P), ('ld_out', I64),
+                ('member_stride_out', I64), ('T', INT), ('members', INT), ('flags', INT), ('w_fc', P),
+                ('w_proj', P), ('sign', P), ('member_shift', INT), ('a_fc', P), ('ld_a_fc', I64), ('b_fc', P),
+                ('ld_b_fc', I64), ('a_proj', P), ('ld_a_proj', I64), ('b_proj', P), ('ld_b_proj', I64)]
 
 
 class Attention(C.Structure):
@@ -88,6 +96,8 @@ class ChainHead(C.Structure):
 SIGNATURES = {
     'noise_abi_version': [],
     'noise_lowrank_gemm': [P, I64, P, I64, INT, INT, INT, C.POINTER(Rank1), INT, P, I64, P, I64, P, I64, P],
+    'noise_mlp_fused': [C.POINTER(Mlp), P],
+    'noise_mlp_pack': [P, I64, P, I64, P, P, P],
     'noise_embed_norm': [P, I64, INT, INT, P, I64, INT, INT, P, P, I64, P, I64, INT, P, P, P],
     'noise_mix_norm': [C.POINTER(MixNorm), P],
     'noise_rope_norm_ve': [C.POINTER(Rope), P],

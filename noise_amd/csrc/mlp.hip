@@ -1,0 +1,501 @@
+// Fused MLP block of the population forward, one launch per layer:
+//   out = [in +] c_proj(relu(c_fc(norm in) + rank-1)^2) + rank-1
+// Reference: train/val/eggroll.py:93 (x + lowrank(c_proj, relu(lowrank(c_fc, norm(x)))^2)),
+// utils/model.py:100-107 (relu^2 MLP), `lowrank` eggroll.py:56-58 (x W^T + sign (x . b) a^T).
+//
+// The [rows, 2048] relu^2 hidden never leaves the chip. A workgroup owns 128 rows of one member
+// (four waves, one per SIMD, 32 rows each) and all 512 output columns; the 2048 hidden features
+// stream through in chunks of 32:
+//   * the wave's rows arrive in one coalesced pass straight into the c_proj accumulators (where
+//     they also start the residual sum); the row norms come from cross-lane sums, and h = bf16 of
+//     the normalised rows is transposed into the c_fc operand layout by MFMAs against a permuted
+//     identity (exact), ending in 128 VGPRs;
+//   * c_fc is computed transposed, hid^T[32 features, 32 rows] = W_fc[chunk] h^T, with h as the B
+//     operand of v_mfma_f32_32x32x16_bf16. The accumulator of that product gives lane l the hidden
+//     values of row l % 32 -- exactly the row the A operand of the c_proj MFMA wants in lane l --
+//     for the features 8 (j / 4) + 4 (l / 32) + j % 4 (j = 0..15). Both packed weight copies
+//     (noise_mlp_pack) store their K dimension in that order, so the rank-1 term, relu^2 and the
+//     bf16 rounding run on the accumulators in registers and their result is the next MFMA's
+//     operand;
+//   * c_proj accumulates out[32 rows, 512] per wave in 256 registers (16 32x32 blocks);
+//   * the weights stream through two LDS stages of one chunk each (c_fc rows padded to 1040 bytes
+//     so the fragment reads hit 16 distinct bank groups; the c_proj chunk pre-swizzled in HBM),
+//     fetched one chunk ahead by direct global -> LDS loads. Step i runs the 32 c_fc MFMAs of
+//     chunk i interleaved with the 32 c_proj MFMAs of chunk i - 1, whose hidden values come out of
+//     the other c_fc accumulator set: the epilogue of one chunk overlaps the MFMAs of the next.
+// Per row the kernel moves 2 KB in and 2 KB out (fp32), against 18 KB through HBM for the separate
+// norm, c_fc and c_proj launches.
+#include "mma_tile.h"
+
+namespace {
+
+constexpr int D = 512, F = 2048, FC = 32, NCH = F / FC;
+constexpr int ROWS = 128;                        // rows per workgroup
+constexpr int WFC_ROW = 1040;                    // bytes per c_fc row in LDS (1 KB + 16 pad)
+constexpr int WFC_PART = FC * WFC_ROW;           // 33280
+constexpr int WMP_PART = D * FC * 2;             // 32768: [512 rows][32 k] bf16, swizzled
+constexpr int STAGE = WFC_PART + WMP_PART;       // 66048
+constexpr int NOISE_OFS = 2 * STAGE;             // a_fc [2048] | b_proj [2048] | a_proj [512] | b_fc [512]
+constexpr int LDS_BYTES = NOISE_OFS + (2 * F + 2 * D) * 4;  // 152576
+constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (F.rms_norm default)
+#ifndef MLP_AHEAD
+#define MLP_AHEAD 3  // MFMA pairs of fragment-read lookahead
+#endif
+
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+
+// Position q (0..15) of a 16-deep k-step of the packed c_proj copy holds hidden feature
+// perm16(q) of that step: lanes 0-31 supply k-slots 0-7 from accumulators j = 0..7 of the c_fc
+// block (features 0-3, 8-11), lanes 32-63 slots 8-15 (features 4-7, 12-15).
+__host__ __device__ constexpr int perm16(int q) { return 8 * ((q & 7) >> 2) + 4 * (q >> 3) + (q & 3); }
+
+// Stage `buf` <- c_fc rows of the cf-th chunk (if cf >= 0) and the packed c_proj cm-th chunk (if
+// cm >= 0) of the workgroup's chunk order.
+// Each wave issues 8 + 8 direct loads of 1 KB (lane l's 16 bytes land at the base + 16 l).
+NOISE_DEV void load_stage(const noise_mlp_t& g, unsigned char* lds, int wave, int lane, int buf, int cf, int cm,
+                          int c0) {
+  unsigned char* st = lds + buf * STAGE;
+  if (cf >= 0) cf = (cf + c0) & (NCH - 1);  // the workgroup's chunk order starts at chunk c0
+  if (cm >= 0) cm = (cm + c0) & (NCH - 1);
+  if (cf >= 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int row = wave * 8 + k;
+      __builtin_amdgcn_global_load_lds((const void*)(g.w_fc + (int64_t)(cf * FC + row) * D + lane * 8),
+                                       (void*)(st + row * WFC_ROW), 16, 0, 0);
+    }
+  }
+  if (cm >= 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int blk = wave * 8 + k;
+      __builtin_amdgcn_global_load_lds((const void*)(g.w_proj + (int64_t)cm * (D * FC) + blk * 512 + lane * 8),
+                                       (void*)(st + WFC_PART + blk * 1024), 16, 0, 0);
+    }
+  }
+}
+
+// A copy of an accumulator register the compiler cannot reuse: without it the prologue kept VGPR
+// copies of all 256 input values alive between its two passes over them and spilled.
+NOISE_DEV float agpr_read(float a) {
+  float v;
+  __asm__ volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
+// The next stage's loads of one wave: 8 c_fc rows and 8 1-KB blocks of the packed c_proj chunk.
+// mlp_step issues them one per MFMA pair through the first half of a step: issued back to back
+// at the start of the step they stalled the wave's MFMA stream behind the memory pipeline
+// (measured at the bench shape: 5.2 -> see DESIGN for the current figure).
+struct StageLoads {
+  const uint16_t* fc_src;  // row wave * 8 of the c_fc chunk, this lane's 16 bytes
+  const uint16_t* mp_src;  // block wave * 8 of the c_proj chunk, this lane's 16 bytes
+  unsigned char* fc_dst;   // LDS: c_fc row wave * 8 of the stage
+  unsigned char* mp_dst;   // LDS: c_proj block wave * 8 of the stage
+};
+
+NOISE_DEV StageLoads stage_loads(const noise_mlp_t& g, unsigned char* lds, int wave, int lane, int buf, int cf,
+                                 int cm, int c0) {
+  cf = (cf + c0) & (NCH - 1);
+  cm = (cm + c0) & (NCH - 1);
+  unsigned char* st = lds + buf * STAGE;
+  return StageLoads{g.w_fc + (int64_t)(cf * FC + wave * 8) * D + lane * 8,
+                    g.w_proj + (int64_t)cm * (D * FC) + wave * 8 * 512 + lane * 8, st + wave * 8 * WFC_ROW,
+                    st + WFC_PART + wave * 8 * 1024};
+}
+
+NOISE_DEV bf16x8 as_bf16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  return __builtin_bit_cast(bf16x8, (u32x4){w0, w1, w2, w3});
+}
+
+// ds_read_b128 at a byte address + immediate offset, invisible to the compiler's wait counting
+// (every read is waited for explicitly with lgkm_wait).
+#define MLP_DSREAD(DST, ADDR, OFS) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(DST) : "v"(ADDR), "n"(OFS))
+#define MLP_LGKM(N) __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N))
+
+// One step of the chunk pipeline. FCP: run the c_fc MFMAs of chunk `cf` into fc[FB]; PRJ: first
+// turn fc[1 - FB] (chunk cf - 1) into the c_proj operand (rank-1, relu^2, bf16, u_proj dots) and
+// run its 32 c_proj MFMAs. Stage buffer `buf` holds c_fc rows of chunk cf and c_proj chunk cf - 1.
+template <bool FCP, bool PRJ, int FB, bool LFC, bool LMP>
+NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&acc)[16], float& up,
+                        uint32_t fcb, uint32_t mpb0, uint32_t mpb1, const float* s_afc, const float* s_bmp,
+                        int chunk_prev, int half, float su, int c0, const StageLoads& ld) {
+  bf16x8 hid[2];
+  if (PRJ) {
+    // hidden of chunk cf - 1: lane's row r = l % 32, features base + 8 g + 4 half + q.
+    const int cp = (chunk_prev + c0) & (NCH - 1);
+    const float* pa = s_afc + cp * FC + 4 * half;
+    const float* pb = s_bmp + cp * FC + 4 * half;
+    float hv[16];
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const float4 av = *reinterpret_cast<const float4*>(pa + 8 * gi);
+      const float4 bv = *reinterpret_cast<const float4*>(pb + 8 * gi);
+      const float a4[4] = {av.x, av.y, av.z, av.w}, b4[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = fc[1 - FB][4 * gi + q] + su * a4[q];
+        v = v > 0.f ? v * v : 0.f;
+        v = bf2f(f2bf(v));
+        hv[4 * gi + q] = v;
+        up += v * b4[q];
+      }
+    }
+    hid[0] = as_bf16x8(pack_bf2(hv[0], hv[1]), pack_bf2(hv[2], hv[3]), pack_bf2(hv[4], hv[5]), pack_bf2(hv[6], hv[7]));
+    hid[1] = as_bf16x8(pack_bf2(hv[8], hv[9]), pack_bf2(hv[10], hv[11]), pack_bf2(hv[12], hv[13]),
+                       pack_bf2(hv[14], hv[15]));
+  }
+  // 32 MFMA pairs: c_fc k-step t of chunk cf and c_proj block (t & 15), k-step t >> 4 of chunk
+  // cf - 1. Fragments are read MLP_AHEAD pairs ahead through MLP_AHEAD + 1 register sets: with one
+  // wave per SIMD nothing else hides the LDS latency.
+  bf16x8 fa[MLP_AHEAD + 1], fb[MLP_AHEAD + 1];
+  constexpr int NR = (FCP ? 1 : 0) + (PRJ ? 1 : 0);  // LDS reads per pair
+#define MLP_READ(T_, SET_)                                                      \
+  {                                                                             \
+    if (FCP) MLP_DSREAD(fa[SET_], fcb, 32 * (T_));                              \
+    if (PRJ) {                                                                  \
+      if ((T_) < 16) MLP_DSREAD(fb[SET_], mpb0, 2048 * ((T_) & 15));            \
+      else MLP_DSREAD(fb[SET_], mpb1, 2048 * ((T_) & 15));                      \
+    }                                                                           \
+  }
+#pragma unroll
+  for (int t = 0; t < MLP_AHEAD; ++t) MLP_READ(t, t)
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const int set = t % (MLP_AHEAD + 1);
+    if (LFC && t < 8)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.fc_src + t * D), (void*)(ld.fc_dst + t * WFC_ROW), 16, 0, 0);
+    if (LMP && t >= 8 && t < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (t - 8) * 512), (void*)(ld.mp_dst + (t - 8) * 1024),
+                                       16, 0, 0);
+    if (t + MLP_AHEAD < 32) MLP_READ(t + MLP_AHEAD, (t + MLP_AHEAD) % (MLP_AHEAD + 1))
+    // Pair t's reads are done once at most the later pairs' reads are in flight.
+    MLP_LGKM(NR * (31 - t < MLP_AHEAD ? 31 - t : MLP_AHEAD));
+    if (FCP) {
+      // Inline asm pins the c_fc accumulators to VGPRs (the AGPRs hold the 256 c_proj
+      // accumulators). Chained MFMAs whose srcC is exactly the previous vDst need no wait states;
+      // the last one of the chunk is followed by s_nops covering the VALU read of its result
+      // (the compiler cannot see that the asm is an MFMA).
+      if (t == 0)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
+      else if (t < 31)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
+      else
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
+    }
+    if (PRJ) {
+      // Inline asm keeps the accumulators in AGPRs. The hidden operand was written by VALU this
+      // step (2 wait states before an MFMA reads it: s_nop 1 ahead of its first use); after the
+      // chunk's last MFMA the epilogue may read the accumulators (s_nops as for c_fc).
+      if (t == 0 || t == 16)
+        __asm__ volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                         : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
+      else if (t < 31)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
+      else
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
+    }
+  }
+#undef MLP_READ
+}
+
+template <bool NORM, bool RESID>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+mlp_fused_kernel(const noise_mlp_t g) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, half = lane >> 5;
+  // Workgroup -> (member p, row block b). Workgroups go to the XCDs round-robin; numbering the
+  // blocks of groups of 8 members so that XCD x runs b = 0, 1, 2, ... in turn lets each XCD walk
+  // the feature chunks from bpm different starting points (c0 below) instead of every CU asking
+  // L2 for the same weight lines at the same moment (measured on MI355X: 5.8 -> 5.2 ms at the
+  // bench shape). c0 depends only on b, so a member's result does not depend on which other
+  // members share the launch.
+  const int bpm = (g.T + ROWS - 1) / ROWS;
+  int p, b;
+  {
+    const int i = blockIdx.x, full = (g.members & ~7) * bpm;
+    if (i < full) {
+      const int q = i >> 3;
+      b = q % bpm;
+      p = (q / bpm) * 8 + (i & 7);
+    } else {
+      const int j = i - full;
+      p = (g.members & ~7) + j / bpm;
+      b = j % bpm;
+    }
+  }
+  const int c0 = (b * (bpm >= NCH ? 1 : NCH / bpm)) & (NCH - 1);
+  const int tb = b * ROWS + wave * 32;  // first row of this wave
+  const bool pert = g.sign != nullptr;
+  const int64_t pn = (int64_t)(p >> g.member_shift);
+  const float s = pert ? g.sign[p] : 0.f;
+  float* s_afc = reinterpret_cast<float*>(lds + NOISE_OFS);
+  float* s_bmp = s_afc + F;
+  float* s_amp = s_bmp + F;
+  float* s_bfc = s_amp + D;
+
+  // The first c_fc chunk starts streaming into stage 0 while the rows are normalised.
+  load_stage(g, lds, wave, lane, 0, 0, -1, c0);
+
+  // ---- prologue, one pass over the input: the wave's 32 rows land in the c_proj accumulator
+  // layout (lane l holds column 32 nb + l % 32 of rows 8 (j / 4) + 4 (l / 32) + j % 4), where they
+  // also start the residual sum.
+  // The 256 loads go straight into the accumulator AGPRs by inline asm, three rows of 16 ahead of
+  // their use (left to itself the compiler waited for each load before issuing the next). Vector
+  // loads complete in issue order, so once at most the later rows' loads are in flight a row has
+  // landed; the wait is tied to that row's registers.
+  floatx16 acc[16];
+  const float* xrow = g.in + (int64_t)p * g.member_stride_in + r;
+#define MLP_XLOAD(J_)                                                                                      \
+  {                                                                                                      \
+    const int rj_ = tb + 8 * ((J_) >> 2) + 4 * half + ((J_) & 3);                                         \
+    const float* src_ = xrow + (int64_t)(rj_ < g.T ? rj_ : g.T - 1) * g.ld_in;                            \
+    _Pragma("unroll") for (int nb = 0; nb < 16; ++nb)                                                     \
+      __asm__ volatile("global_load_dword %0, %1, off offset:%2" : "=a"(acc[nb][J_]) : "v"(src_), "n"(nb * 128)); \
+  }
+#define MLP_XWAIT(J_, N_)                                                                                 \
+  __asm__ volatile("s_waitcnt vmcnt(%16)"                                                                \
+                   : "+a"(acc[0][J_]), "+a"(acc[1][J_]), "+a"(acc[2][J_]), "+a"(acc[3][J_]),               \
+                     "+a"(acc[4][J_]), "+a"(acc[5][J_]), "+a"(acc[6][J_]), "+a"(acc[7][J_]),               \
+                     "+a"(acc[8][J_]), "+a"(acc[9][J_]), "+a"(acc[10][J_]), "+a"(acc[11][J_]),             \
+                     "+a"(acc[12][J_]), "+a"(acc[13][J_]), "+a"(acc[14][J_]), "+a"(acc[15][J_])            \
+                   : "n"(N_))
+  MLP_XLOAD(0)
+  MLP_XLOAD(1)
+  MLP_XLOAD(2)
+  float ps[16];  // per-lane sums of squares of each accumulator row
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j + 3 < 16) MLP_XLOAD(j + 3)
+    MLP_XWAIT(j, 16 * (15 - j < 3 ? 15 - j : 3));
+    ps[j] = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) {
+      const float v = agpr_read(acc[nb][j]);
+      ps[j] += v * v;
+    }
+  }
+#undef MLP_XWAIT
+#undef MLP_XLOAD
+
+  // The member's perturbation rows, 5120 floats (20 per thread); zeros when unperturbed, so the
+  // rank-1 terms vanish without a branch in the main loop.
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const int e = (k * 256 + tid) * 4;  // 0 .. 5116
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (pert) {
+      const float* src = e < F ? g.a_fc + pn * g.ld_a_fc + e
+                       : e < 2 * F ? g.b_proj + pn * g.ld_b_proj + (e - F)
+                       : e < 2 * F + D ? g.a_proj + pn * g.ld_a_proj + (e - 2 * F)
+                                       : g.b_fc + pn * g.ld_b_fc + (e - 2 * F - D);
+      v = *reinterpret_cast<const float4*>(src);
+    }
+    *reinterpret_cast<float4*>(s_afc + e) = v;
+  }
+
+  // Row norms: per-lane partial sums over the 16 column blocks, then across the half-wave
+  // (lane q of a half ends with row value (q >> 1) & 15), broadcast back per accumulator row.
+  float rrj[16];
+  if (NORM) {
+    const float rr = rsqrtf(noise::halfwave_transpose_sum16(ps, lane) * (1.0f / D) + RMS_EPS);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rrj[j] = __shfl(rr, (lane & 32) + 2 * j, 64);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rrj[j] = 1.f;
+  }
+  __syncthreads();  // the perturbation rows are in LDS
+
+  // h = bf16(row * rr), turned into the c_fc B operand (lane l: row l % 32) by MFMAs against a
+  // permuted identity: with A = h block nb (lane: column 32 nb + l % 32, k-slots = the lane's
+  // accumulator rows 16 s + 8 (q / 4) + 4 (l / 32) + q % 4) and B[k][j] = 1 where row(k) = j, the
+  // product is h^T exactly (every sum has one non-zero term), and its accumulators hold row l % 32
+  // at the columns 32 nb + 8 (v / 4) + 4 (l / 32) + v % 4 -- the perm16 order in which the packed
+  // c_fc copy stores its K dimension.
+  bf16x8 ident[2];
+#pragma unroll
+  for (int sx = 0; sx < 2; ++sx) {
+    const bool mine = (r >> 4) == sx && ((r >> 2) & 1) == half;
+    const int q = 4 * ((r >> 3) & 1) + (r & 3);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = (mine && (q >> 1) == k) ? (0x3F80u << (16 * (q & 1))) : 0u;
+    ident[sx] = as_bf16x8(w[0], w[1], w[2], w[3]);
+  }
+  bf16x8 hB[32];
+#pragma unroll
+  for (int nb = 0; nb < 16; ++nb) {
+    uint32_t hw[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      hw[k] = pack_bf2(agpr_read(acc[nb][2 * k]) * rrj[2 * k], agpr_read(acc[nb][2 * k + 1]) * rrj[2 * k + 1]);
+    floatx16 tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(hw[0], hw[1], hw[2], hw[3]), ident[0],
+                                                           (floatx16){}, 0, 0, 0);
+    tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(hw[4], hw[5], hw[6], hw[7]), ident[1], tr, 0, 0, 0);
+    hB[2 * nb] = as_bf16x8(pack_bf2(tr[0], tr[1]), pack_bf2(tr[2], tr[3]), pack_bf2(tr[4], tr[5]),
+                           pack_bf2(tr[6], tr[7]));
+    hB[2 * nb + 1] = as_bf16x8(pack_bf2(tr[8], tr[9]), pack_bf2(tr[10], tr[11]), pack_bf2(tr[12], tr[13]),
+                               pack_bf2(tr[14], tr[15]));
+  }
+  // u_fc = bf16(h) . b_fc of row l % 32: this lane's 256 columns (k-step ks, slot q: column
+  // 16 ks + 8 (q / 4) + 4 (l / 32) + q % 4), then the other half-row from lane l ^ 32.
+  float uf = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 32; ++ks) {
+    const float4 b0 = *reinterpret_cast<const float4*>(s_bfc + 16 * ks + 4 * half);
+    const float4 b1 = *reinterpret_cast<const float4*>(s_bfc + 16 * ks + 8 + 4 * half);
+    const u32x4 w = __builtin_bit_cast(u32x4, hB[ks]);
+    uf += bf_lo(w[0]) * b0.x + bf_hi(w[0]) * b0.y + bf_lo(w[1]) * b0.z + bf_hi(w[1]) * b0.w;
+    uf += bf_lo(w[2]) * b1.x + bf_hi(w[2]) * b1.y + bf_lo(w[3]) * b1.z + bf_hi(w[3]) * b1.w;
+  }
+  uf += __shfl_xor(uf, 32, 64);
+  const float su = s * uf;
+  if (!RESID) {
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[nb][j] = 0.f;
+  }
+
+  // LDS byte addresses of this lane's fragment rows: c_fc row r (k-step ks at + 32 ks), c_proj
+  // row 32 nb + r of k-step kk at chunk (2 kk + half) ^ ((r >> 2) & 3) (+ 2048 nb).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  const uint32_t fcb[2] = {lds0 + r * WFC_ROW + 16 * half, lds0 + STAGE + r * WFC_ROW + 16 * half};
+  const int sw = (r >> 2) & 3;
+  const uint32_t mpr = lds0 + WFC_PART + r * 64;
+  const uint32_t mpb[2][2] = {{mpr + 16 * ((0 + half) ^ sw), mpr + 16 * ((2 + half) ^ sw)},
+                              {mpr + STAGE + 16 * ((0 + half) ^ sw), mpr + STAGE + 16 * ((2 + half) ^ sw)}};
+
+  floatx16 fc[2];
+  float up = 0.f;  // bf16(hidden) . b_proj over this lane's features
+
+  // Step i: stage i % 2 holds c_fc chunk i and c_proj chunk i - 1; stage (i + 1) % 2 is refilled.
+#define MLP_BARRIER() __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory")
+  MLP_BARRIER();
+  mlp_step<true, false, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, 0, half, su, c0,
+                                       stage_loads(g, lds, wave, lane, 1, 1, 0, c0));
+#pragma unroll 1
+  for (int i = 1; i < NCH - 1; i += 2) {
+    MLP_BARRIER();
+    mlp_step<true, true, 1, true, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], s_afc, s_bmp, i - 1, half, su,
+                                        c0, stage_loads(g, lds, wave, lane, 0, i + 1, i, c0));
+    MLP_BARRIER();
+    mlp_step<true, true, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, i, half, su, c0,
+                                        stage_loads(g, lds, wave, lane, 1, i + 2, i + 1, c0));
+  }
+  // i = NCH - 1 (odd): stage 1 holds c_fc chunk 63 and c_proj chunk 62; stage 0 receives c_proj 63.
+  MLP_BARRIER();
+  mlp_step<true, true, 1, false, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], s_afc, s_bmp, NCH - 2, half,
+                                       su, c0, stage_loads(g, lds, wave, lane, 0, 0, NCH - 1, c0));
+  MLP_BARRIER();
+  mlp_step<false, true, 0, false, false>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, NCH - 1, half,
+                                         su, c0, stage_loads(g, lds, wave, lane, 1, 0, 0, c0));
+#undef MLP_BARRIER
+
+  // ---- epilogue: rank-1 term of c_proj, sign (hidden . b_proj) a_proj, and the store.
+  up += __shfl_xor(up, 32, 64);  // lane l: row l % 32
+  const float sup = s * up;
+  float am[16];
+#pragma unroll
+  for (int nb = 0; nb < 16; ++nb) am[nb] = s_amp[nb * 32 + r];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int rl = 8 * (j >> 2) + 4 * half + (j & 3);
+    const float sr = __shfl(sup, rl, 64);
+    const int rj = tb + rl;
+    if (rj < g.T) {
+      float* dst = g.out + (int64_t)p * g.member_stride_out + (int64_t)rj * g.ld_out + r;
+#pragma unroll
+      for (int nb = 0; nb < 16; ++nb) dst[nb * 32] = acc[nb][j] + sr * am[nb];
+    }
+  }
+}
+
+// One thread per 16-byte piece of the packed copies. c_fc: row f, piece c holds K positions
+// 8 c .. 8 c + 7 with position 16 g + q reading column 16 g + perm16(q). c_proj: chunk c, row n,
+// physical piece phi holds logical piece phi ^ ((n >> 2) & 3) of the chunk's 32 positions, position
+// 16 g + q reading feature 32 c + 16 g + perm16(q).
+__global__ void __launch_bounds__(256) mlp_pack_kernel(const float* __restrict__ w_fc, int64_t ld_fc,
+                                                       const float* __restrict__ w_proj, int64_t ld_proj,
+                                                       uint16_t* __restrict__ fc_packed,
+                                                       uint16_t* __restrict__ proj_packed) {
+  const int id = blockIdx.x * 256 + threadIdx.x;  // < 2 * 131072
+  uint32_t out[4];
+  if (id < F * D / 8) {
+    if (!fc_packed) return;
+    const int f = id >> 6, c = id & 63;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const int q0 = 8 * c + e, q1 = q0 + 1;
+      const int k0 = 16 * (q0 >> 4) + perm16(q0 & 15), k1 = 16 * (q1 >> 4) + perm16(q1 & 15);
+      out[e / 2] = pack_bf2(w_fc[(int64_t)f * ld_fc + k0], w_fc[(int64_t)f * ld_fc + k1]);
+    }
+    *reinterpret_cast<u32x4*>(fc_packed + (int64_t)id * 8) = (u32x4){out[0], out[1], out[2], out[3]};
+    return;
+  }
+  if (!proj_packed) return;
+  const int jd = id - F * D / 8;
+  const int phi = jd & 3, n = (jd >> 2) & (D - 1), c = jd >> 11;
+  const int kc = phi ^ ((n >> 2) & 3);  // logical piece: positions 8 kc .. 8 kc + 7
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const int q0 = 8 * kc + e, q1 = q0 + 1;
+    const int f0 = c * FC + 16 * (q0 >> 4) + perm16(q0 & 15), f1 = c * FC + 16 * (q1 >> 4) + perm16(q1 & 15);
+    out[e / 2] = pack_bf2(w_proj[(int64_t)n * ld_proj + f0], w_proj[(int64_t)n * ld_proj + f1]);
+  }
+  *reinterpret_cast<u32x4*>(proj_packed + (int64_t)jd * 8) = (u32x4){out[0], out[1], out[2], out[3]};
+}
+
+}  // namespace
+
+extern "C" int noise_mlp_pack(const float* w_fc, int64_t ld_fc, const float* w_proj, int64_t ld_proj,
+                              uint16_t* fc_packed, uint16_t* proj_packed, void* stream) {
+  NOISE_REQUIRE(!fc_packed || (w_fc && ld_fc >= D), "mlp_pack: c_fc needs w_fc with ld_fc >= 512");
+  NOISE_REQUIRE(!proj_packed || (w_proj && ld_proj >= F), "mlp_pack: c_proj needs w_proj with ld_proj >= 2048");
+  NOISE_REQUIRE(((uintptr_t)fc_packed % 16) == 0 && ((uintptr_t)proj_packed % 16) == 0,
+                "mlp_pack: packed copies must be 16-byte aligned");
+  if (!fc_packed && !proj_packed) return NOISE_OK;
+  mlp_pack_kernel<<<2 * F * D / 8 / 256, 256, 0, (hipStream_t)stream>>>(w_fc, ld_fc, w_proj, ld_proj, fc_packed,
+                                                                       proj_packed);
+  return noise::check_launch("mlp_pack");
+}
+
+extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
+  NOISE_REQUIRE(args, "mlp_fused: null arguments");
+  const noise_mlp_t& g = *args;
+  NOISE_REQUIRE(g.in && g.out && g.w_fc && g.w_proj, "mlp_fused: null in, out or weights");
+  NOISE_REQUIRE(g.T > 0 && g.members >= 0, "mlp_fused: T=%d members=%d", g.T, g.members);
+  NOISE_REQUIRE((g.flags & ~(NOISE_MLP_NORM | NOISE_MLP_RESIDUAL)) == 0, "mlp_fused: unknown flags %d", g.flags);
+  NOISE_REQUIRE(g.ld_in >= D && g.ld_out >= D && g.ld_in % 4 == 0 && g.member_stride_in % 4 == 0 &&
+                    g.member_stride_in >= 0 && g.member_stride_out >= 0,
+                "mlp_fused: rows need ld >= 512 with ld_in and member_stride_in multiples of 4");
+  NOISE_REQUIRE(((uintptr_t)g.in % 16) == 0 && ((uintptr_t)g.w_fc % 16) == 0 && ((uintptr_t)g.w_proj % 16) == 0,
+                "mlp_fused: in, w_fc and w_proj must be 16-byte aligned");
+  if (g.sign) {
+    NOISE_REQUIRE(g.a_fc && g.b_fc && g.a_proj && g.b_proj, "mlp_fused: perturbation needs a/b of both matrices");
+    NOISE_REQUIRE(g.member_shift >= 0 && g.member_shift < 31, "mlp_fused: bad member_shift");
+    NOISE_REQUIRE(g.ld_a_fc >= F && g.ld_b_proj >= F && g.ld_a_proj >= D && g.ld_b_fc >= D &&
+                      g.ld_a_fc % 4 == 0 && g.ld_b_proj % 4 == 0 && g.ld_a_proj % 4 == 0 && g.ld_b_fc % 4 == 0,
+                  "mlp_fused: noise rows need lda >= out, ldb >= in, multiples of 4");
+    NOISE_REQUIRE(((uintptr_t)g.a_fc % 16) == 0 && ((uintptr_t)g.b_fc % 16) == 0 &&
+                      ((uintptr_t)g.a_proj % 16) == 0 && ((uintptr_t)g.b_proj % 16) == 0,
+                  "mlp_fused: noise rows must be 16-byte aligned");
+  }
+  const int64_t blocks = (int64_t)g.members * ((g.T + ROWS - 1) / ROWS);
+  NOISE_REQUIRE(blocks < (1ll << 31), "mlp_fused: too many rows");
+  if (blocks == 0) return NOISE_OK;
+  const dim3 grid((unsigned)blocks);
+  hipStream_t st = (hipStream_t)stream;
+  switch (g.flags) {
+    case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL: mlp_fused_kernel<true, true><<<grid, 256, 0, st>>>(g); break;
+    case NOISE_MLP_NORM: mlp_fused_kernel<true, false><<<grid, 256, 0, st>>>(g); break;
+    case NOISE_MLP_RESIDUAL: mlp_fused_kernel<false, true><<<grid, 256, 0, st>>>(g); break;
+    default: mlp_fused_kernel<false, false><<<grid, 256, 0, st>>>(g); break;
+  }
+  return noise::check_launch("mlp_fused");
+}

@@ -8,7 +8,7 @@ import ctypes as C
 import torch
 
 from . import _lib
-from ._lib import Attention, Head, MixNorm, Rank1, Rope
+from ._lib import Attention, Head, MixNorm, Mlp, Rank1, Rope
 
 
 def _ptr(t):
@@ -85,6 +85,64 @@ def lowrank_gemm(A, W, r1, mode, C_out, b_next=None, u_next=None):
     _lib.call('noise_lowrank_gemm', _ptr(A), lda, _ptr(W), ldw, M, N, K,
               C.byref(r1) if r1 is not None else None, mode, _ptr(C_out), ldc,
               _ptr(b_next), ldb, _ptr(u_next), ldun, _stream())
+
+
+MLP_PACKED_ELEMS = 2048 * 512  # bf16 elements of each packed MLP weight copy
+
+
+def mlp_pack(w_fc=None, fc_packed=None, w_proj=None, proj_packed=None):
+    """Packed bf16 copies of c_fc (fp32 [2048, 512]) and/or c_proj (fp32 [512, 2048]) weights in the
+    operand layouts of mlp_fused."""
+    for w, out, shape, name in ((w_fc, fc_packed, (2048, 512), 'c_fc'), (w_proj, proj_packed, (512, 2048), 'c_proj')):
+        if out is None:
+            continue
+        _on_gpu(w, out)
+        _need(w.dtype == torch.float32 and tuple(w.shape) == shape and w.stride(1) == 1,
+              f'mlp_pack: {name} weight must be fp32 {list(shape)} with contiguous rows')
+        _need(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == MLP_PACKED_ELEMS,
+              f'mlp_pack: packed {name} must be a contiguous bf16 tensor of 2048 * 512 elements')
+    _lib.call('noise_mlp_pack', _ptr(w_fc if fc_packed is not None else None),
+              w_fc.stride(0) if fc_packed is not None else 0,
+              _ptr(w_proj if proj_packed is not None else None), w_proj.stride(0) if proj_packed is not None else 0,
+              _ptr(fc_packed), _ptr(proj_packed), _stream())
+
+
+def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=None, fc=None, proj=None,
+              member_stride_in=None, member_stride_out=None):
+    """x_out = [x_in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 with h = bf16(norm x_in) under
+    MLP_NORM (else bf16(x_in)), in one launch. x_in / x_out: fp32 rows of 512; member p's rows
+    start at p * member_stride (default T rows). fc / proj: NoiseRows of c_fc and c_proj."""
+    _on_gpu(x_in, x_out, w_fc_packed, w_proj_packed, sign)
+    ld_in = _rows(x_in, 512, torch.float32, 'x_in')
+    ld_out = _rows(x_out, 512, torch.float32, 'x_out')
+    for w in (w_fc_packed, w_proj_packed):
+        _need(w.dtype == torch.bfloat16 and w.numel() == MLP_PACKED_ELEMS and w.is_contiguous(),
+              'mlp_fused: the weights must be packed bf16 copies (mlp_pack)')
+    g = Mlp()
+    g.in_, g.ld_in = x_in.data_ptr(), ld_in
+    g.member_stride_in = T * ld_in if member_stride_in is None else member_stride_in
+    g.out, g.ld_out = x_out.data_ptr(), ld_out
+    g.member_stride_out = T * ld_out if member_stride_out is None else member_stride_out
+    span_in = (members - 1) * g.member_stride_in + (T - 1) * ld_in + 512 if members else 0
+    span_out = (members - 1) * g.member_stride_out + (T - 1) * ld_out + 512 if members else 0
+    _need(span_in <= x_in.numel() and span_out <= x_out.numel(), 'mlp_fused: x_in / x_out have too few rows')
+    g.T, g.members, g.flags = T, members, flags
+    g.w_fc, g.w_proj = w_fc_packed.data_ptr(), w_proj_packed.data_ptr()
+    if sign is not None:
+        _need(sign.dtype == torch.float32 and sign.numel() >= members, 'mlp_fused: sign [members] fp32')
+        need = ((members - 1) >> fc.shift) + 1 if members else 0
+        for t, width, name in ((fc.a, 2048, 'c_fc a'), (fc.b, 512, 'c_fc b'), (proj.a, 512, 'c_proj a'),
+                               (proj.b, 2048, 'c_proj b')):
+            _on_gpu(t)
+            _rows(t, width, torch.float32, name)
+            _need(t.shape[0] >= need, f'mlp_fused: {name} has {t.shape[0]} noise rows, {need} needed')
+        _need(proj.shift == fc.shift, 'mlp_fused: c_fc and c_proj noise rows must share member_shift')
+        g.sign, g.member_shift = sign.data_ptr(), fc.shift
+        g.a_fc, g.ld_a_fc = fc.a.data_ptr(), fc.a.stride(0)
+        g.b_fc, g.ld_b_fc = fc.b.data_ptr(), fc.b.stride(0)
+        g.a_proj, g.ld_a_proj = proj.a.data_ptr(), proj.a.stride(0)
+        g.b_proj, g.ld_b_proj = proj.b.data_ptr(), proj.b.stride(0)
+    _lib.call('noise_mlp_fused', C.byref(g), _stream())
 
 
 def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0):

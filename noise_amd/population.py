@@ -12,9 +12,8 @@ Per layer the engine runs (one launch each, all on the current stream):
                 q, k = bf16(norm(rot(.))); v = bf16(v + gate ve)
   attention     y = bf16(softmax_window(q k^T / 8) v); u_o = y.b_o per head
   lowrank_gemm  x += y Wo^T + s u_o a_o^T
-  mix_norm      h = bf16(norm x); u_fc = h.b_fc
-  lowrank_gemm  hid = bf16(relu(h Wfc^T + s u a^T)^2); u_mp = hid.b_mp per 64 columns
-  lowrank_gemm  x += hid Wmp^T + s u_mp a_mp^T
+  mlp_fused     x += bf16(relu(h Wfc^T + s u_fc a_fc^T)^2) Wmp^T + s u_mp a_mp^T with
+                h = bf16(norm x), u_fc = h.b_fc, u_mp = hid.b_mp: the hidden stays on chip
 then mix_norm (final norm + u_head), head_ce (fp32-accurate head, soft-cap, CE) and member_mean.
 """
 import math
@@ -54,6 +53,8 @@ class PreparedWeights:
         self.o = [torch.empty(d, d, **bf) for _ in range(L)]
         self.fc = [torch.empty(f, d, **bf) for _ in range(L)]
         self.mp = [torch.empty(d, f, **bf) for _ in range(L)]
+        self.fc_packed = [torch.empty(K.MLP_PACKED_ELEMS, **bf) for _ in range(L)]
+        self.mp_packed = [torch.empty(K.MLP_PACKED_ELEMS, **bf) for _ in range(L)]
         v = cfg.padded_vocab
         self.head_hi = torch.empty(v, d, **bf)
         self.head_lo = torch.empty(v, d, **bf)
@@ -69,6 +70,8 @@ class PreparedWeights:
             K.cast_bf16(p[pre + 'attn.c_proj.weight'].contiguous(), self.o[i])
             K.cast_bf16(p[pre + 'mlp.c_fc.weight'].contiguous(), self.fc[i])
             K.cast_bf16(p[pre + 'mlp.c_proj.weight'].contiguous(), self.mp[i])
+            K.mlp_pack(p[pre + 'mlp.c_fc.weight'].contiguous(), self.fc_packed[i],
+                       p[pre + 'mlp.c_proj.weight'].contiguous(), self.mp_packed[i])
         K.cast_bf16(p['lm_head.weight'].contiguous(), self.head_hi, self.head_lo)
 
     def gate(self, i):
@@ -95,7 +98,7 @@ class Workspace:
         self.qkv16 = torch.empty(rows, 3 * d, **bf)
         self.y = torch.empty(rows, d, **bf)
         self.uproj = torch.empty(rows, cfg.n_head, **f32)
-        self.hid = torch.empty(rows, f, **bf)
+        self.hid = None  # the unfused MLP's [rows, 2048] hidden, allocated only when used
         self.umlp = torch.empty(rows, f // 64, **f32)
         self.ce = torch.empty(rows, **f32)
 
@@ -108,9 +111,12 @@ class Engine:
         self.cfg = cfg
         self.ws = None
         self._rot = {}
-        # When a list, every fused-MLP GEMM pair is bracketed by timing events on the launch
-        # stream: (before c_fc, between, after c_proj, rows) is appended per layer and chunk.
+        # When a list, every MLP launch is bracketed by timing events on the launch stream:
+        # (before, after, rows) is appended per layer and chunk.
         self.probe = None
+        # False runs the MLP as mix_norm + two lowrank_gemm launches through an HBM hidden
+        # (kept to compare the two on the same inputs).
+        self.fused_mlp = True
 
     def _mark(self):
         if self.probe is None:
@@ -141,7 +147,10 @@ class Engine:
         ws = self.workspace(M)
         x, x0, h, u3, u1 = ws.x[:M], ws.x0[:M], ws.h[:M], ws.u3[:M], ws.u1[:M]
         gate, qkv16, y = ws.gate[:M], ws.qkv16[:M], ws.y[:M]
-        uproj, hid, umlp, ce = ws.uproj[:M], ws.hid[:M], ws.umlp[:M], ws.ce[:M]
+        uproj, umlp, ce = ws.uproj[:M], ws.umlp[:M], ws.ce[:M]
+        if not self.fused_mlp and (ws.hid is None or ws.hid.shape[0] < M):
+            ws.hid = torch.empty(ws.rows, cfg.mlp_dim, dtype=torch.bfloat16, device=self.device)
+        hid = None if self.fused_mlp else ws.hid[:M]
         cos, sin = self.rotary(T)
         pert = sign is not None
         g = (lambda name: nz[name]) if pert else (lambda name: None)
@@ -170,16 +179,19 @@ class Engine:
                                uproj if pert else None)
             r1 = K.rank1(sign, T, [o.a], [uproj], cfg.n_head, cfg.n_head, shift) if pert else None
             K.lowrank_gemm(y, W.o[i], r1, _lib.EPI_ADD_F32, x)
-            K.mix_norm(x, h, T, sign, shift=shift, bs=(fc.b,) if pert else (), u=u1)
-            r1 = K.rank1(sign, T, [fc.a], [u1], 1, 1, shift) if pert else None
             ev = self._mark()
-            K.lowrank_gemm(h, W.fc[i], r1, _lib.EPI_RELU2_BF16, hid, mp.b if pert else None,
-                           umlp if pert else None)
-            r1 = K.rank1(sign, T, [mp.a], [umlp], umlp.shape[1], umlp.shape[1], shift) if pert else None
-            ev_mid = self._mark()
-            K.lowrank_gemm(hid, W.mp[i], r1, _lib.EPI_ADD_F32, x)
+            if self.fused_mlp:
+                K.mlp_fused(x, x, T, members, W.fc_packed[i], W.mp_packed[i], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
+                            sign, fc, mp)
+            else:
+                K.mix_norm(x, h, T, sign, shift=shift, bs=(fc.b,) if pert else (), u=u1)
+                r1 = K.rank1(sign, T, [fc.a], [u1], 1, 1, shift) if pert else None
+                K.lowrank_gemm(h, W.fc[i], r1, _lib.EPI_RELU2_BF16, hid, mp.b if pert else None,
+                               umlp if pert else None)
+                r1 = K.rank1(sign, T, [mp.a], [umlp], umlp.shape[1], umlp.shape[1], shift) if pert else None
+                K.lowrank_gemm(hid, W.mp[i], r1, _lib.EPI_ADD_F32, x)
             if ev is not None:
-                self.probe.append((ev, ev_mid, self._mark(), M))
+                self.probe.append((ev, self._mark(), M))
         hd = g('lm_head.weight')
         K.mix_norm(x, h, T, sign, shift=shift, bs=(hd.b,) if pert else (), u=u1)
         out_ce = ce if ce_out is None else ce_out
@@ -202,7 +214,8 @@ def _noise_rows(noise, names, lo, hi, shift=0):
 
 
 def _f32rows(t):
-    if t.dtype != torch.float32 or t.stride(-1) != 1 or (t.dim() == 2 and t.stride(0) % 4):
+    if (t.dtype != torch.float32 or t.stride(-1) != 1 or (t.dim() == 2 and t.stride(0) % 4)
+            or t.data_ptr() % 16):
         t = t.to(torch.float32).contiguous()
     return t
 

@@ -1,0 +1,192 @@
+"""The fused relu^2 MLP (noise_mlp_fused) against float64 on the same inputs, through the C ABI.
+
+Reference semantics: train/val/eggroll.py:93, `x + lowrank(c_proj, relu(lowrank(c_fc, norm(x)))^2)`
+with `lowrank` eggroll.py:56-58 and the relu^2 MLP of utils/model.py:100-107. The float64
+reference keeps the kernel's cast points (h and the hidden rounded to bf16, bf16 weight copies,
+the rank-1 dots over the rounded operands) so what is left is fp32 accumulation order, plus the odd
+bf16 rounding that lands on the other side of a boundary. Bars: the north star's 1e-2 relative on
+bf16-level activations for the largest element, and 1e-3 on the RMS of the whole output.
+"""
+import math
+
+import pytest
+import torch
+
+from noise_amd import _lib
+from noise_amd import kernels as K
+from noise_amd.kernels import NoiseRows
+
+pytestmark = pytest.mark.gpu
+
+EPS = torch.finfo(torch.float32).eps
+D, F = 512, 2048
+
+
+def _weights(g):
+    w1 = torch.randn(F, D, generator=g) / math.sqrt(D)
+    w2 = torch.randn(D, F, generator=g) / math.sqrt(F)
+    return w1, w2
+
+
+def _packed(w1, w2, device):
+    p1 = torch.empty(K.MLP_PACKED_ELEMS, dtype=torch.bfloat16, device=device)
+    p2 = torch.empty(K.MLP_PACKED_ELEMS, dtype=torch.bfloat16, device=device)
+    K.mlp_pack(w1.to(device), p1, w2.to(device), p2)
+    return p1, p2
+
+
+def mlp_ref(x, w1, w2, s=0.0, a_fc=None, b_fc=None, a_pr=None, b_pr=None, norm=True, resid=True):
+    """float64 with the kernel's cast points; x [T, 512] float32 (CPU)."""
+    if norm:  # the norm itself in float32, as the kernel forms it
+        h = x * torch.rsqrt(x.square().mean(-1, keepdim=True) + EPS)
+    else:
+        h = x
+    h = h.to(torch.bfloat16).double()
+    pre = h @ w1.to(torch.bfloat16).double().t()
+    if s:
+        pre = pre + s * (h @ b_fc.double())[:, None] * a_fc.double()[None, :]
+    hid = torch.relu(pre).square().to(torch.bfloat16).double()
+    y = hid @ w2.to(torch.bfloat16).double().t()
+    if s:
+        y = y + s * (hid @ b_pr.double())[:, None] * a_pr.double()[None, :]
+    return x.double() + y if resid else y
+
+
+def _close(got, ref, what):
+    err = (got.double() - ref).abs()
+    scale = float(ref.abs().max())
+    rms = float(err.square().mean().sqrt()) / max(float(ref.square().mean().sqrt()), 1e-30)
+    print(f'{what}: max |err| {float(err.max()):.3e} (max |ref| {scale:.3e}), relative rms {rms:.3e}')
+    assert float(err.max()) <= 1e-2 * scale, what
+    assert rms <= 1e-3, what
+
+
+@pytest.mark.parametrize('T,members,shift,pert,flags', [
+    (256, 4, 1, True, _lib.MLP_NORM | _lib.MLP_RESIDUAL),
+    (100, 3, 0, True, _lib.MLP_NORM | _lib.MLP_RESIDUAL),      # ragged: partial row blocks
+    (37, 5, 0, False, _lib.MLP_NORM | _lib.MLP_RESIDUAL),      # T < 128, unperturbed
+    (2048, 2, 1, True, _lib.MLP_NORM | _lib.MLP_RESIDUAL),     # 16 row blocks per member
+    (160, 2, 0, True, _lib.MLP_NORM),
+    (160, 2, 0, True, _lib.MLP_RESIDUAL),
+    (160, 2, 1, True, 0),
+])
+def test_mlp_fused_matches_float64(device, T, members, shift, pert, flags):
+    g = torch.Generator().manual_seed(1000 + T + members + flags)
+    w1, w2 = _weights(g)
+    x = torch.randn(members * T, D, generator=g) * 1.5
+    rows = members >> shift if shift else members
+    rows = max(rows, 1) + (members & 1)
+    sign = torch.tensor([0.02 if j % 2 == 0 else -0.02 for j in range(members)])
+    fc = NoiseRows(a=torch.randn(rows, F, generator=g), b=torch.randn(rows, D, generator=g), shift=shift)
+    pr = NoiseRows(a=torch.randn(rows, D, generator=g), b=torch.randn(rows, F, generator=g), shift=shift)
+    dev = lambda n: NoiseRows(a=n.a.to(device), b=n.b.to(device), shift=n.shift)
+    w1p, w2p = _packed(w1, w2, device)
+    xin = x.to(device)
+    xout = torch.full_like(xin, float('nan'))
+    K.mlp_fused(xin, xout, T, members, w1p, w2p, flags,
+                sign.to(device) if pert else None, dev(fc), dev(pr))
+    got = xout.cpu()
+    norm, resid = bool(flags & _lib.MLP_NORM), bool(flags & _lib.MLP_RESIDUAL)
+    for p in range(members):
+        n = p >> shift
+        s = float(sign[p]) if pert else 0.0
+        ref = mlp_ref(x[p * T:(p + 1) * T], w1, w2, s, fc.a[n], fc.b[n], pr.a[n], pr.b[n], norm, resid)
+        _close(got[p * T:(p + 1) * T], ref, f'T={T} member {p} flags {flags}')
+
+
+def test_mlp_fused_in_place_equals_out_of_place(device):
+    """The step runs the kernel in place on the residual stream: same bits as a separate output."""
+    g = torch.Generator().manual_seed(7)
+    w1, w2 = _weights(g)
+    T, members = 384, 4
+    x = torch.randn(members * T, D, generator=g).to(device)
+    sign = torch.tensor([1e-3, -1e-3] * 2, device=device)
+    fc = NoiseRows(a=torch.randn(2, F, generator=g).to(device), b=torch.randn(2, D, generator=g).to(device), shift=1)
+    pr = NoiseRows(a=torch.randn(2, D, generator=g).to(device), b=torch.randn(2, F, generator=g).to(device), shift=1)
+    w1p, w2p = _packed(w1, w2, device)
+    flags = _lib.MLP_NORM | _lib.MLP_RESIDUAL
+    out = torch.empty_like(x)
+    K.mlp_fused(x, out, T, members, w1p, w2p, flags, sign, fc, pr)
+    xi = x.clone()
+    K.mlp_fused(xi, xi, T, members, w1p, w2p, flags, sign, fc, pr)
+    assert torch.equal(out, xi)
+
+
+PERM16 = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+
+
+def test_mlp_pack_layouts(device):
+    """The packed copies hold bf16(W) once for every element. c_fc [2048, 512]: row f, K position
+    16 g + q holds column 16 g + perm16(q). c_proj: chunk c of 32 features is a [512, 32] block whose
+    16-byte pieces are swizzled within the row (piece phi holds logical piece phi ^ ((n >> 2) & 3))
+    and whose position 16 g + q holds feature 32 c + 16 g + perm16(q). perm16 is the order in which
+    the fused kernel's MFMA accumulators deliver a 16-deep k-step."""
+    w1 = torch.arange(F * D, dtype=torch.float32).view(F, D) % 251 - 125  # exact in bf16
+    w2 = torch.arange(D * F, dtype=torch.float32).view(D, F) % 241 - 120
+    p1, p2 = _packed(w1, w2, device)
+    fc = p1.cpu().float().view(F, D)
+    cols = [16 * (k // 16) + PERM16[k % 16] for k in range(D)]
+    assert torch.equal(fc, w1[:, cols])
+    blk = p2.cpu().float().view(F // 32, D, 4, 8)  # chunk, row n, physical piece, element
+    for c in (0, 1, 37, 63):
+        for n in (0, 1, 4, 5, 13, 200, 511):
+            for phi in range(4):
+                kc = phi ^ ((n >> 2) & 3)
+                feats = [c * 32 + 16 * ((8 * kc + e) // 16) + PERM16[(8 * kc + e) % 16] for e in range(8)]
+                assert blk[c, n, phi].tolist() == w2[n, feats].tolist()
+
+
+def test_config1_mlp_full_size(device):
+    """Config 1 at full size: P = 256 members, T = 2048 shared bf16 rows x ~ N(0, 1), W1 [512->2048]
+    ~ N(0, 1/512), W2 [2048->512] ~ N(0, 1/2048), rank-1 pairs (a1 in R^512, b1 in R^2048, a2 in
+    R^2048, b2 in R^512) ~ N(0, 1), sigma = 1e-3 antithetic: y_p = relu^2(x (W1 + s b1 a1^T)^T)
+    (W2 + s b2 a2^T)^T, one launch (the shared x read through a member stride of 0). Sampled members
+    and rows against float64 (north-star naming: a multiplies the input, b is the output direction)."""
+    g = torch.Generator().manual_seed(41)
+    T, P = 2048, 256
+    x = torch.randn(T, D, generator=g).to(torch.bfloat16).float()
+    w1, w2 = _weights(g)
+    a1, b1 = torch.randn(P // 2, D, generator=g), torch.randn(P // 2, F, generator=g)
+    a2, b2 = torch.randn(P // 2, F, generator=g), torch.randn(P // 2, D, generator=g)
+    sign = torch.tensor([1e-3, -1e-3] * (P // 2))
+    w1p, w2p = _packed(w1, w2, device)
+    y = torch.empty(P * T, D, device=device)
+    fc = NoiseRows(a=b1.to(device), b=a1.to(device), shift=1)
+    pr = NoiseRows(a=b2.to(device), b=a2.to(device), shift=1)
+    K.mlp_fused(x.to(device), y, T, P, w1p, w2p, 0, sign.to(device), fc, pr,
+                member_stride_in=0)
+    torch.cuda.synchronize()
+    rows = torch.randperm(T, generator=g)[:96]
+    for p in (0, 1, 2, 77, 128, 254, 255):
+        ref = mlp_ref(x[rows], w1, w2, float(sign[p]), b1[p // 2], a1[p // 2], b2[p // 2], a2[p // 2],
+                      norm=False, resid=False)
+        _close(y[p * T + rows.to(device)].cpu(), ref, f'config 1 member {p}')
+    assert bool(torch.isfinite(y).all())
+
+
+def test_fused_and_unfused_population_paths_agree(device, init_params):
+    """The population forward with the fused MLP and with the separate norm + c_fc + c_proj
+    launches (the HBM hidden) both hold the 1e-4 loss bar against the oracle's build policy on the
+    same inputs; they differ from each other by bf16 roundings that fall the other way (~2e-5)."""
+    from oracle import model_ref as R
+    import noise_amd
+    from noise_amd.population import engine_for
+    from noise_amd.synthetic import antithetic, pair_noise, sequence
+    idx, targets = sequence(256, seed=61)
+    noise, sign = antithetic(pair_noise(4, seed=62), 1e-3)
+    p = {k: v.to(device) for k, v in init_params.items()}
+    nz = {k: tuple(x.to(device) for x in v) if isinstance(v, tuple) else v.to(device) for k, v in noise.items()}
+    eng = engine_for(device)
+    args = (None, p, nz, sign.to(device), idx.to(device), targets.to(device))
+    fused = noise_amd.population_loss(*args)
+    eng.fused_mlp = False
+    try:
+        unfused = noise_amd.population_loss(*args)
+    finally:
+        eng.fused_mlp = True
+    oracle = R.population_loss(init_params, noise, sign, idx, targets, policy='build').float()
+    print('fused - unfused', (fused - unfused).abs().max().item(), 'fused - oracle',
+          (fused.cpu() - oracle).abs().max().item(), 'unfused - oracle', (unfused.cpu() - oracle).abs().max().item())
+    assert float((fused.cpu() - oracle).abs().max()) <= 1e-4
+    assert float((unfused.cpu() - oracle).abs().max()) <= 1e-4
+    assert float((fused - unfused).abs().max()) <= 1e-4

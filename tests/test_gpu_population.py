@@ -3,7 +3,7 @@ CPU oracle (same weights, tokens and host-supplied perturbations), and size-inde
 properties at the full 2048-token shape.
 
 Bar: <= 1e-4 absolute on every per-member fp32 loss against the oracle's 'build' policy (the
-GPU's cast points); the reference's own fp32 goldens are met within 2e-4."""
+GPU's cast points) and against the reference's own fp32 goldens of config 0."""
 import math
 
 import pytest
@@ -41,7 +41,8 @@ def test_config0_population_loss(device, init_params, golden, golden_json):
     oracle = R.population_loss(init_params, noise, sign, idx, targets, policy='build').float()
     print('config0 gpu', got.tolist(), 'max |gpu - oracle|', float((got - oracle).abs().max()))
     assert float((got - oracle).abs().max()) <= 1e-4
-    assert float((got - t(golden['config0/losses'])).abs().max()) <= 2e-4
+    print('max |gpu - reference golden|', float((got - t(golden['config0/losses'])).abs().max()))
+    assert float((got - t(golden['config0/losses'])).abs().max()) <= 1e-4
 
 
 def test_sensitive_population_loss(device, init_params, golden, golden_json):
@@ -122,6 +123,39 @@ def test_full_length_properties(device, init_params):
     neg = noise_amd.population_loss(None, p, _to(noise, device), (-sign).to(device), idx.to(device), targets.to(device))
     assert torch.equal(pos.view(4, 2).flip(1).reshape(-1), neg)
     assert float((pos - zero).abs().max()) < 0.5
+
+
+def test_bench_chunk_shape(device, init_params):
+    """The launch shape bench.py times: one forward of 512 members x T = 2048 (2^20 rows per
+    kernel launch). sigma = 0 makes every member bit-equal and equal to the clean forward; the sign
+    flip swaps every pair bit-exactly; two pairs recomputed in a 4-member chunk are bit-identical to
+    their values inside the 512-member chunk; one pair is held to 1e-4 against the oracle's build
+    policy at T = 2048 (train/val/eggroll.py:139-146)."""
+    T, pairs = 2048, 256
+    idx, targets = sequence(T, seed=71)
+    p = _params(init_params, device)
+    base = pair_noise(pairs, seed=72)
+    noise, sign = antithetic(base, 1e-3)
+    nz = _to(noise, device)
+    del noise
+    di, dt, ds = idx.to(device), targets.to(device), sign.to(device)
+    full = noise_amd.population_loss(None, p, nz, ds, di, dt, chunk=512)
+    neg = noise_amd.population_loss(None, p, nz, -ds, di, dt, chunk=512)
+    assert torch.equal(full.view(pairs, 2).flip(1).reshape(-1), neg)
+    sel = torch.tensor([6, 7, 400, 401], device=device)
+    sub = {k: tuple(x[sel] for x in v) if isinstance(v, tuple) else v[sel] for k, v in nz.items()}
+    small = noise_amd.population_loss(None, p, sub, ds[sel], di, dt, chunk=4)
+    assert torch.equal(small, full[sel])
+    zero = noise_amd.population_loss(None, p, nz, ds * 0, di, dt, chunk=512)
+    assert torch.equal(zero, zero[:1].expand(2 * pairs))
+    clean = noise_amd.clean_loss(p, di[None], dt[None]).double().mean()
+    assert abs(float(zero[0]) - float(clean)) <= 1e-5
+    one = {k: tuple(x[[3]] for x in v) if isinstance(v, tuple) else v[[3]] for k, v in base.items()}
+    n2, s2 = antithetic(one, 1e-3)
+    oracle = R.population_loss(init_params, n2, s2, idx, targets, policy='build').float()
+    err = float((full[6:8].cpu() - oracle).abs().max())
+    print('bench shape: pair 3 vs oracle', full[6:8].tolist(), oracle.tolist(), err)
+    assert err <= 1e-4
 
 
 def test_config1_mlp_block(device):
