@@ -19,7 +19,7 @@ LIB = PKG / 'libnoise_amd.so'
 ARCH = 'gfx950'
 
 FLAGS = [
-    f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-Wall', '-Wno-unused-function',
+    f'--offload-arch={ARCH}', '-O3', '-std=c++20', '-fPIC', '-Wall', '-Wno-unused-function',
     f'-I{ROOT / "include"}', f'-I{CSRC}',
     # Packed fp32 VALU forms are kept out of the generated code on purpose.
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',

@@ -25,6 +25,8 @@
 //     the other c_fc accumulator set: the epilogue of one chunk overlaps the MFMAs of the next.
 // Per row the kernel moves 2 KB in and 2 KB out (fp32), against 18 KB through HBM for the separate
 // norm, c_fc and c_proj launches.
+#include <utility>
+
 #include "mma_tile.h"
 
 namespace {
@@ -86,7 +88,7 @@ NOISE_DEV float agpr_read(float a) {
 // The next stage's loads of one wave: 8 c_fc rows and 8 1-KB blocks of the packed c_proj chunk.
 // mlp_step issues them one per MFMA pair through the first half of a step: issued back to back
 // at the start of the step they stalled the wave's MFMA stream behind the memory pipeline
-// (measured at the bench shape: 5.2 -> see DESIGN for the current figure).
+// (measured at the bench shape: 5.1 -> 4.7 ms per launch).
 struct StageLoads {
   const uint16_t* fc_src;  // row wave * 8 of the c_fc chunk, this lane's 16 bytes
   const uint16_t* mp_src;  // block wave * 8 of the c_proj chunk, this lane's 16 bytes
@@ -113,92 +115,121 @@ NOISE_DEV bf16x8 as_bf16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
 #define MLP_DSREAD(DST, ADDR, OFS) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(DST) : "v"(ADDR), "n"(OFS))
 #define MLP_LGKM(N) __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N))
 
-// One step of the chunk pipeline. FCP: run the c_fc MFMAs of chunk `cf` into fc[FB]; PRJ: first
-// turn fc[1 - FB] (chunk cf - 1) into the c_proj operand (rank-1, relu^2, bf16, u_proj dots) and
-// run its 32 c_proj MFMAs. Stage buffer `buf` holds c_fc rows of chunk cf and c_proj chunk cf - 1.
+// The MFMA order of one step. With both halves: F0..F3 (c_fc k-steps 0-3) while the epilogue of
+// the previous chunk produces the c_proj operand, then P0 F4 P1 F5 ... P27 F31, then P28..P31 (P t:
+// c_proj block t & 15, k-step t >> 4). With one half, its 32 MFMAs in order.
+template <bool FCP, bool PRJ>
+struct StepOps {
+  static constexpr int N = (FCP ? 32 : 0) + (PRJ ? 32 : 0);
+  static constexpr bool is_fc(int s) {
+    return !PRJ ? true : !FCP ? false : s < 4 ? true : (s - 4 >= 56 ? false : ((s - 4) & 1) != 0);
+  }
+  static constexpr int idx(int s) {
+    return (!PRJ || !FCP || s < 4) ? s : (s - 4 >= 56 ? 28 + (s - 60) : (((s - 4) & 1) ? 4 + ((s - 4) >> 1) : (s - 4) >> 1));
+  }
+};
+
+// One step of the chunk pipeline. FCP: the c_fc MFMAs of chunk `cf` into fc[FB]; PRJ: turn
+// fc[1 - FB] (chunk cf - 1) into the c_proj operand (rank-1 term, relu^2, bf16, u_proj dots) and
+// run its 32 c_proj MFMAs. Stage buffer `buf` holds c_fc rows of chunk cf and c_proj chunk cf - 1;
+// the loads of the next stage (LFC, LMP) are issued one per MFMA during the first 16. Every MFMA is
+// inline asm so that the c_fc accumulators stay in VGPRs and the c_proj ones in AGPRs; the hazards
+// the compiler then cannot see are covered explicitly: 2 wait states between the VALU writing the
+// c_proj operand and its first MFMA, and 24 after a chunk's last MFMA before VALU reads its result.
+// Fragments are read MLP_AHEAD MFMAs ahead; the epilogue's perturbation values are read before
+// all of them, so the wait for the first fragment covers them too.
 template <bool FCP, bool PRJ, int FB, bool LFC, bool LMP>
 NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&acc)[16], float& up,
-                        uint32_t fcb, uint32_t mpb0, uint32_t mpb1, const float* s_afc, const float* s_bmp,
-                        int chunk_prev, int half, float su, int c0, const StageLoads& ld) {
-  bf16x8 hid[2];
+                        uint32_t fcb, uint32_t mpb0, uint32_t mpb1, uint32_t ab_base, int chunk_prev, float su,
+                        int c0, const StageLoads& ld) {
+  using O = StepOps<FCP, PRJ>;
+  constexpr int NA = MLP_AHEAD + 1;
+  floatx4 av[4], bv[4];
   if (PRJ) {
-    // hidden of chunk cf - 1: lane's row r = l % 32, features base + 8 g + 4 half + q.
-    const int cp = (chunk_prev + c0) & (NCH - 1);
-    const float* pa = s_afc + cp * FC + 4 * half;
-    const float* pb = s_bmp + cp * FC + 4 * half;
-    float hv[16];
+    // Perturbation values of the previous chunk: this lane's features base + 8 g + 4 half + q.
+    const uint32_t ab = ab_base + (uint32_t)(((chunk_prev + c0) & (NCH - 1)) * FC * 4);
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const float4 av = *reinterpret_cast<const float4*>(pa + 8 * gi);
-      const float4 bv = *reinterpret_cast<const float4*>(pb + 8 * gi);
-      const float a4[4] = {av.x, av.y, av.z, av.w}, b4[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float v = fc[1 - FB][4 * gi + q] + su * a4[q];
-        v = v > 0.f ? v * v : 0.f;
-        v = bf2f(f2bf(v));
-        hv[4 * gi + q] = v;
-        up += v * b4[q];
-      }
+      MLP_DSREAD(av[gi], ab, 32 * gi);
+      MLP_DSREAD(bv[gi], ab, 4 * F + 32 * gi);
     }
-    hid[0] = as_bf16x8(pack_bf2(hv[0], hv[1]), pack_bf2(hv[2], hv[3]), pack_bf2(hv[4], hv[5]), pack_bf2(hv[6], hv[7]));
-    hid[1] = as_bf16x8(pack_bf2(hv[8], hv[9]), pack_bf2(hv[10], hv[11]), pack_bf2(hv[12], hv[13]),
-                       pack_bf2(hv[14], hv[15]));
   }
-  // 32 MFMA pairs: c_fc k-step t of chunk cf and c_proj block (t & 15), k-step t >> 4 of chunk
-  // cf - 1. Fragments are read MLP_AHEAD pairs ahead through MLP_AHEAD + 1 register sets: with one
-  // wave per SIMD nothing else hides the LDS latency.
-  bf16x8 fa[MLP_AHEAD + 1], fb[MLP_AHEAD + 1];
-  constexpr int NR = (FCP ? 1 : 0) + (PRJ ? 1 : 0);  // LDS reads per pair
-#define MLP_READ(T_, SET_)                                                      \
-  {                                                                             \
-    if (FCP) MLP_DSREAD(fa[SET_], fcb, 32 * (T_));                              \
-    if (PRJ) {                                                                  \
-      if ((T_) < 16) MLP_DSREAD(fb[SET_], mpb0, 2048 * ((T_) & 15));            \
-      else MLP_DSREAD(fb[SET_], mpb1, 2048 * ((T_) & 15));                      \
-    }                                                                           \
+  bf16x8 fr[NA];
+  // Fragment read for op S (S a compile-time constant, so the offsets are immediates).
+  auto read = [&, fcb, mpb0, mpb1]<int S>() __attribute__((always_inline)) {
+    constexpr int i = O::idx(S);
+    if constexpr (O::is_fc(S)) MLP_DSREAD(fr[S % NA], fcb, 32 * i);
+    else if constexpr (i < 16) MLP_DSREAD(fr[S % NA], mpb0, 2048 * (i & 15));
+    else MLP_DSREAD(fr[S % NA], mpb1, 2048 * (i & 15));
+  };
+  [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
+    (read.template operator()<S>(), ...);
+  }(std::make_integer_sequence<int, MLP_AHEAD>{});
+  uint32_t hw[8];
+  bf16x8 hid[2];
+  // Epilogue piece e (0..7): values 2 e, 2 e + 1 of the previous chunk's accumulators; pieces 0-3
+  // make the operand of the first 16 c_proj MFMAs, pieces 4-7 that of the last 16.
+  auto epi = [&]<int E>() __attribute__((always_inline)) {
+    constexpr int gi = E >> 1, q = 2 * (E & 1);
+    const float v0 = fmaxf(fc[1 - FB][2 * E] + su * av[gi][q], 0.f);
+    const float v1 = fmaxf(fc[1 - FB][2 * E + 1] + su * av[gi][q + 1], 0.f);
+    const uint32_t w = pack_bf2(v0 * v0, v1 * v1);
+    hw[E] = w;
+    up += bf_lo(w) * bv[gi][q] + bf_hi(w) * bv[gi][q + 1];
+    if constexpr (E == 3) hid[0] = as_bf16x8(hw[0], hw[1], hw[2], hw[3]);
+    if constexpr (E == 7) hid[1] = as_bf16x8(hw[4], hw[5], hw[6], hw[7]);
+  };
+  if constexpr (PRJ && !FCP) {  // last step: the epilogue runs first
+    MLP_LGKM(MLP_AHEAD);
+    __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]),
+                     "+v"(bv[3]));
+    [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
+      (epi.template operator()<E>(), ...);
+    }(std::make_integer_sequence<int, 8>{});
   }
-#pragma unroll
-  for (int t = 0; t < MLP_AHEAD; ++t) MLP_READ(t, t)
-#pragma unroll
-  for (int t = 0; t < 32; ++t) {
-    const int set = t % (MLP_AHEAD + 1);
-    if (LFC && t < 8)
-      __builtin_amdgcn_global_load_lds((const void*)(ld.fc_src + t * D), (void*)(ld.fc_dst + t * WFC_ROW), 16, 0, 0);
-    if (LMP && t >= 8 && t < 16)
-      __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (t - 8) * 512), (void*)(ld.mp_dst + (t - 8) * 1024),
+  auto op = [&]<int SX>() __attribute__((always_inline)) {
+    if constexpr (LFC && SX < 8)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.fc_src + SX * D), (void*)(ld.fc_dst + SX * WFC_ROW), 16, 0, 0);
+    if constexpr (LMP && SX >= 8 && SX < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (SX - 8) * 512), (void*)(ld.mp_dst + (SX - 8) * 1024),
                                        16, 0, 0);
-    if (t + MLP_AHEAD < 32) MLP_READ(t + MLP_AHEAD, (t + MLP_AHEAD) % (MLP_AHEAD + 1))
-    // Pair t's reads are done once at most the later pairs' reads are in flight.
-    MLP_LGKM(NR * (31 - t < MLP_AHEAD ? 31 - t : MLP_AHEAD));
-    if (FCP) {
-      // Inline asm pins the c_fc accumulators to VGPRs (the AGPRs hold the 256 c_proj
-      // accumulators). Chained MFMAs whose srcC is exactly the previous vDst need no wait states;
-      // the last one of the chunk is followed by s_nops covering the VALU read of its result
-      // (the compiler cannot see that the asm is an MFMA).
-      if (t == 0)
-        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
-      else if (t < 31)
-        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
+    if constexpr (SX + MLP_AHEAD < O::N) read.template operator()<SX + MLP_AHEAD>();
+    MLP_LGKM(O::N - 1 - SX < MLP_AHEAD ? O::N - 1 - SX : MLP_AHEAD);
+    const bf16x8 f = fr[SX % NA];
+    constexpr int i = O::idx(SX);
+    if constexpr (O::is_fc(SX)) {
+      if constexpr (i == 0)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(fc[FB]) : "v"(f), "v"(hB[i]));
+      else if constexpr (i < 31)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(fc[FB]) : "v"(f), "v"(hB[i]));
       else
         __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                         : "+v"(fc[FB]) : "v"(fa[set]), "v"(hB[t]));
-    }
-    if (PRJ) {
-      // Inline asm keeps the accumulators in AGPRs. The hidden operand was written by VALU this
-      // step (2 wait states before an MFMA reads it: s_nop 1 ahead of its first use); after the
-      // chunk's last MFMA the epilogue may read the accumulators (s_nops as for c_fc).
-      if (t == 0 || t == 16)
+                         : "+v"(fc[FB]) : "v"(f), "v"(hB[i]));
+      if constexpr (PRJ && i < 8) {
+        // Epilogue piece i after c_fc MFMA i (held there by the scheduling barriers): pieces 0-3
+        // before the first c_proj MFMA, 4-7 among the first ones; the perturbation values are in
+        // once the first fragment is.
+        if constexpr (i == 0)
+          __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]), "+v"(bv[1]),
+                           "+v"(bv[2]), "+v"(bv[3]));
+        __builtin_amdgcn_sched_barrier(0);
+        epi.template operator()<i>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      if constexpr (i == 0 || i == 16)
         __asm__ volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
-                         : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
-      else if (t < 31)
-        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
+                         : "+a"(acc[i & 15]) : "v"(hid[i >> 4]), "v"(f));
+      else if constexpr (i < 31 || FCP)
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc[i & 15]) : "v"(hid[i >> 4]), "v"(f));
       else
         __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                         : "+a"(acc[t & 15]) : "v"(hid[t >> 4]), "v"(fb[set]));
+                         : "+a"(acc[i & 15]) : "v"(hid[i >> 4]), "v"(f));
     }
-  }
-#undef MLP_READ
+  };
+  [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
+    (op.template operator()<S>(), ...);
+  }(std::make_integer_sequence<int, O::N>{});
 }
 
 template <bool NORM, bool RESID>
@@ -365,6 +396,7 @@ mlp_fused_kernel(const noise_mlp_t g) {
   // LDS byte addresses of this lane's fragment rows: c_fc row r (k-step ks at + 32 ks), c_proj
   // row 32 nb + r of k-step kk at chunk (2 kk + half) ^ ((r >> 2) & 3) (+ 2048 nb).
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+  const uint32_t ab_base = lds0 + NOISE_OFS + 16 * half;  // a_fc at + 0, b_proj at + 4 F floats
   const uint32_t fcb[2] = {lds0 + r * WFC_ROW + 16 * half, lds0 + STAGE + r * WFC_ROW + 16 * half};
   const int sw = (r >> 2) & 3;
   const uint32_t mpr = lds0 + WFC_PART + r * 64;
@@ -377,24 +409,24 @@ mlp_fused_kernel(const noise_mlp_t g) {
   // Step i: stage i % 2 holds c_fc chunk i and c_proj chunk i - 1; stage (i + 1) % 2 is refilled.
 #define MLP_BARRIER() __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory")
   MLP_BARRIER();
-  mlp_step<true, false, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, 0, half, su, c0,
+  mlp_step<true, false, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], ab_base, 0, su, c0,
                                        stage_loads(g, lds, wave, lane, 1, 1, 0, c0));
 #pragma unroll 1
   for (int i = 1; i < NCH - 1; i += 2) {
     MLP_BARRIER();
-    mlp_step<true, true, 1, true, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], s_afc, s_bmp, i - 1, half, su,
-                                        c0, stage_loads(g, lds, wave, lane, 0, i + 1, i, c0));
+    mlp_step<true, true, 1, true, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], ab_base, i - 1, su, c0,
+                                        stage_loads(g, lds, wave, lane, 0, i + 1, i, c0));
     MLP_BARRIER();
-    mlp_step<true, true, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, i, half, su, c0,
+    mlp_step<true, true, 0, true, true>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], ab_base, i, su, c0,
                                         stage_loads(g, lds, wave, lane, 1, i + 2, i + 1, c0));
   }
   // i = NCH - 1 (odd): stage 1 holds c_fc chunk 63 and c_proj chunk 62; stage 0 receives c_proj 63.
   MLP_BARRIER();
-  mlp_step<true, true, 1, false, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], s_afc, s_bmp, NCH - 2, half,
-                                       su, c0, stage_loads(g, lds, wave, lane, 0, 0, NCH - 1, c0));
+  mlp_step<true, true, 1, false, true>(hB, fc, acc, up, fcb[1], mpb[1][0], mpb[1][1], ab_base, NCH - 2, su, c0,
+                                       stage_loads(g, lds, wave, lane, 0, 0, NCH - 1, c0));
   MLP_BARRIER();
-  mlp_step<false, true, 0, false, false>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], s_afc, s_bmp, NCH - 1, half,
-                                         su, c0, stage_loads(g, lds, wave, lane, 1, 0, 0, c0));
+  mlp_step<false, true, 0, false, false>(hB, fc, acc, up, fcb[0], mpb[0][0], mpb[0][1], ab_base, NCH - 1, su, c0,
+                                         stage_loads(g, lds, wave, lane, 1, 0, 0, c0));
 #undef MLP_BARRIER
 
   // ---- epilogue: rank-1 term of c_proj, sign (hidden . b_proj) a_proj, and the store.
