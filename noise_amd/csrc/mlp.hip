@@ -41,7 +41,13 @@ constexpr int NOISE_OFS = 2 * STAGE;             // a_fc [2048] | b_proj [2048] 
 constexpr int LDS_BYTES = NOISE_OFS + (2 * F + 2 * D) * 4;  // 152576
 constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (F.rms_norm default)
 #ifndef MLP_AHEAD
-#define MLP_AHEAD 3  // MFMA pairs of fragment-read lookahead
+#define MLP_AHEAD 3  // MFMAs of fragment-read lookahead
+#endif
+#ifndef MLP_NTSTORE
+#define MLP_NTSTORE 0  // output rows stored past L2 (non-temporal)
+#endif
+#ifndef MLP_LSTRIDE
+#define MLP_LSTRIDE 1  // MFMAs between two loads of the next stage
 #endif
 
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
@@ -188,10 +194,14 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
     }(std::make_integer_sequence<int, 8>{});
   }
   auto op = [&]<int SX>() __attribute__((always_inline)) {
-    if constexpr (LFC && SX < 8)
-      __builtin_amdgcn_global_load_lds((const void*)(ld.fc_src + SX * D), (void*)(ld.fc_dst + SX * WFC_ROW), 16, 0, 0);
-    if constexpr (LMP && SX >= 8 && SX < 16)
-      __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (SX - 8) * 512), (void*)(ld.mp_dst + (SX - 8) * 1024),
+    // Load k of the next stage goes out with MFMA LS * k (all 16 within the step's MFMAs).
+    constexpr int LS = O::N >= 16 * MLP_LSTRIDE ? MLP_LSTRIDE : O::N / 16;
+    constexpr int LK = SX / LS;
+    static_assert(16 * LS <= O::N, "every load of the next stage must be issued");
+    if constexpr (SX % LS == 0 && LFC && LK < 8)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.fc_src + LK * D), (void*)(ld.fc_dst + LK * WFC_ROW), 16, 0, 0);
+    if constexpr (SX % LS == 0 && LMP && LK >= 8 && LK < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (LK - 8) * 512), (void*)(ld.mp_dst + (LK - 8) * 1024),
                                        16, 0, 0);
     if constexpr (SX + MLP_AHEAD < O::N) read.template operator()<SX + MLP_AHEAD>();
     MLP_LGKM(O::N - 1 - SX < MLP_AHEAD ? O::N - 1 - SX : MLP_AHEAD);
@@ -443,7 +453,13 @@ mlp_fused_kernel(const noise_mlp_t g) {
     if (rj < g.T) {
       float* dst = g.out + (int64_t)p * g.member_stride_out + (int64_t)rj * g.ld_out + r;
 #pragma unroll
-      for (int nb = 0; nb < 16; ++nb) dst[nb * 32] = acc[nb][j] + sr * am[nb];
+      for (int nb = 0; nb < 16; ++nb) {
+#if MLP_NTSTORE
+        __builtin_nontemporal_store(acc[nb][j] + sr * am[nb], dst + nb * 32);
+#else
+        dst[nb * 32] = acc[nb][j] + sr * am[nb];
+#endif
+      }
     }
   }
 }
