@@ -237,6 +237,20 @@ int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t*
  * it makes one pass over every pair. No counterpart in the reference: workspace sizing. */
 int64_t noise_es_gradient_work(int n, int out, int in);
 
+/* noise_es_gradient for callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc); no counterpart in the reference. The split pair sum keeps its
+ * partial tiles in a fixed array the library holds on each device until the process ends
+ * (noise_es_gradient_noalloc_capacity() floats, 32 MiB: enough for 1536 pairs of a [4096, 512]
+ * gradient); a call that would need more returns NOISE_EINVAL. Same kernels, split and result as
+ * noise_es_gradient with a large enough workspace. No allocation and no HIP call besides the
+ * launches (the first call on a device looks the array's address up once). Calls on one device
+ * share the array: calls that overlap in time on one GPU (different streams) race. The calling
+ * thread's current device must be the stream's device. */
+int noise_es_gradient_noalloc(const float* w, int n, const float* a_base, const int64_t* a_off,
+                              const float* b_base, const int64_t* b_off, int out, int in, float scale,
+                              int accumulate, float* G, void* stream);
+int64_t noise_es_gradient_noalloc_capacity(void);
+
 /* AdamW over a flat fp32 buffer (torch.optim.AdamW semantics, eggroll.py:164-167, 205):
  * param *= 1 - lr wd; m = lerp(m, g, 1 - b1); v = b2 v + (1 - b2) g^2;
  * param -= lr / (1 - b1^t) * m / (sqrt(v) / sqrt(1 - b2^t) + eps). */

@@ -108,6 +108,8 @@ SIGNATURES = {
     'noise_fitness': [P, INT, INT, P, P, P],
     'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P, I64, P],
     'noise_es_gradient_work': [INT, INT, INT],
+    'noise_es_gradient_noalloc': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
+    'noise_es_gradient_noalloc_capacity': [],
     'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],
     'noise_cast_bf16': [P, I64, P, P, P],
     'noise_coordinate_differences': [P, INT, I64, P, INT, INT, F32, P, I64, P],
@@ -138,6 +140,7 @@ def load():
     lib.noise_last_error.argtypes = []
     lib.noise_last_error.restype = C.c_char_p
     lib.noise_es_gradient_work.restype = I64  # a size, not a status
+    lib.noise_es_gradient_noalloc_capacity.restype = I64
     _lib = lib
     return lib
 

@@ -8,6 +8,8 @@
 //   the same kernel reads materialised [pairs, out] noise or slices of one shared noise buffer.
 // * adamw (eggroll.py:164-167 with the torch.optim.AdamW of eggroll.py:205): one pass over a flat
 //   fp32 parameter buffer.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -214,6 +216,58 @@ extern "C" int noise_es_gradient(const float* w, int n, const float* a_base, con
   es_gradient_reduce_kernel<<<(unsigned)((elems + 255) / 256), 256, 0, st>>>(work, split, elems, scale, accumulate,
                                                                              G);
   return noise::check_launch("es_gradient");
+}
+
+// ---- allocation-free variant of noise_es_gradient -------------------------------------------
+// The split pair sum keeps its partial tiles in `scratch`, a file-scope device array each GPU holds
+// for the life of the process. Host code never passes the array's name to a kernel (on the host it
+// is only a stand-in for the symbol): the device address comes from hipGetSymbolAddress, once per
+// device, with that device current, and is kept per device.
+namespace {
+constexpr int64_t ES_SCRATCH_FLOATS = int64_t(8) << 20;  // 32 MiB: the 1536-pair split of a [4096, 512] gradient
+constexpr int ES_MAX_DEVICES = 64;
+__device__ __align__(256) float scratch[ES_SCRATCH_FLOATS];
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[ES_MAX_DEVICES] = {};
+
+int device_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return noise::set_error(NOISE_EHIP, "es_gradient_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= ES_MAX_DEVICES)
+    return noise::set_error(NOISE_EINVAL, "es_gradient_noalloc: device %d beyond the %d supported", dev, ES_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return noise::set_error(NOISE_EHIP, "es_gradient_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                              hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return NOISE_OK;
+}
+}  // namespace
+
+extern "C" int64_t noise_es_gradient_noalloc_capacity(void) { return ES_SCRATCH_FLOATS; }
+
+extern "C" int noise_es_gradient_noalloc(const float* w, int n, const float* a_base, const int64_t* a_off,
+                                         const float* b_base, const int64_t* b_off, int out, int in, float scale,
+                                         int accumulate, float* G, void* stream) {
+  NOISE_REQUIRE(out > 0 && in > 0 && n >= 0, "es_gradient_noalloc: bad arguments");
+  const int split = es_splits(n, out, in);
+  const int64_t need = split > 1 ? (int64_t)split * out * in : 0;
+  NOISE_REQUIRE(need <= ES_SCRATCH_FLOATS,
+                "es_gradient_noalloc: %d pairs over a [%d, %d] gradient need %lld scratch floats, beyond the fixed "
+                "%lld (use noise_es_gradient with a workspace)",
+                n, out, in, (long long)need, (long long)ES_SCRATCH_FLOATS);
+  float* work = nullptr;
+  if (need > 0)
+    if (int rc = device_scratch(&work)) return rc;
+  // The same kernels and split as noise_es_gradient with a workspace of `need` floats: every partial
+  // tile the reduction reads is written by this call first, so the array needs no clearing.
+  return noise_es_gradient(w, n, a_base, a_off, b_base, b_off, out, in, scale, accumulate, G, work, need, stream);
 }
 
 extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
