@@ -225,6 +225,14 @@ int noise_member_mean(const float* ce, int members, int T, float* out, void* str
 int noise_fitness(const float* losses, int n_losses, int pairs, float* weight,
                   int* status_out, void* stream);
 
+/* The rank-normalised variant of noise_fitness: f_j = L[2j+1] - L[2j] replaced by its centred rank
+ * ranked[j] = rank(f_j) / (n - 1) - 0.5 (n = n_losses / 2; rank = position in a stable ascending sort:
+ * ties keep index order, NaN after every number, as torch.argsort(stable=True)), then
+ * weight[i] = sum over j = i mod pairs of ranked[j] in ascending j. Extends the z-score of
+ * train/val/eggroll.py:151-154 (config 4's "rank-normalised fitness"). ranked: [n] fp32 output. */
+int noise_fitness_ranks(const float* losses, int n_losses, int pairs, float* weight, float* ranked,
+                        int* status_out, void* stream);
+
 /* G[o, i] (+)= scale * sum_j w[j] a_j[o] b_j[i], with a_j = a_base + a_off[j],
  * b_j = b_base + b_off[j] (train/val/eggroll.py:155-163 with scale = -1/n; a vector
  * parameter is out = L, in = 1 with b_j = 1 when b_base is NULL). */

@@ -106,6 +106,7 @@ SIGNATURES = {
     'noise_head_ce': [C.POINTER(Head), P],
     'noise_member_mean': [P, INT, INT, P, P],
     'noise_fitness': [P, INT, INT, P, P, P],
+    'noise_fitness_ranks': [P, INT, INT, P, P, P, P],
     'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P, I64, P],
     'noise_es_gradient_work': [INT, INT, INT],
     'noise_es_gradient_noalloc': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],

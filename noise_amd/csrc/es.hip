@@ -2,7 +2,8 @@
 //
 // * fitness (train/val/eggroll.py:151-154): f_j = L[2j+1] - L[2j], f /= unbiased std(f) + 1e-8,
 //   weight[i] = sum over j with j % pairs == i of f_j. One workgroup, fixed reduction order, so
-//   every process that holds the same losses computes bit-identical weights.
+//   every process that holds the same losses computes bit-identical weights. fitness_ranks: the
+//   centred-rank variant of the same differences.
 // * es_gradient (eggroll.py:155-163): G = scale * sum_j w_j a_j b_j^T, an fp32 GEMM whose
 //   reduction dimension is the pair index; a_j and b_j are addressed through per-pair offsets, so
 //   the same kernel reads materialised [pairs, out] noise or slices of one shared noise buffer.
@@ -51,6 +52,49 @@ __global__ __launch_bounds__(FT) void fitness_kernel(const float* __restrict__ l
   for (int i = tid; i < pairs; i += FT) {
     float acc = 0.f;
     for (int j = i; j < n; j += pairs) acc += (losses[2 * j + 1] - losses[2 * j]) * inv;
+    weight[i] = acc;
+  }
+  if (tid == 0 && status) *status = nbad > 0.f ? NOISE_ENONFINITE : NOISE_OK;
+}
+
+// Centred-rank fitness: the same antithetic differences f_j = L[2j+1] - L[2j], replaced by
+// rank(f_j) / (n - 1) - 0.5 with the rank of a stable ascending sort (ties keep index order, NaN
+// sorts after every number), then summed into the pair slots like the z-score. The rank is the
+// count #{k : f_k < f_j} + #{k < j : f_k == f_j}, so it equals torch.argsort(stable=True) without
+// sorting; the differences stream through LDS in tiles of FT. One workgroup; fixed order.
+NOISE_DEV bool rank_before(float a, int ia, float b, int ib) {  // a sorts before b
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return !na ? true : (!nb ? false : ia < ib);
+  return a < b || (a == b && ia < ib);
+}
+
+__global__ __launch_bounds__(FT) void fitness_ranks_kernel(const float* __restrict__ losses, int n, int pairs,
+                                                           float* __restrict__ weight, float* __restrict__ ranked,
+                                                           int* status) {
+  __shared__ float tile[FT];
+  __shared__ float red[FT];
+  const int tid = threadIdx.x;
+  float bad = 0.f;
+  const float denom = (float)(n > 1 ? n - 1 : 1);
+  for (int j0 = 0; j0 < n; j0 += FT) {  // the differences this pass ranks: j0 + tid
+    const int j = j0 + tid;
+    const float fj = j < n ? losses[2 * j + 1] - losses[2 * j] : 0.f;
+    if (j < n && (!isfinite(losses[2 * j]) || !isfinite(losses[2 * j + 1]))) bad = 1.f;
+    int rank = 0;
+    for (int k0 = 0; k0 < n; k0 += FT) {
+      __syncthreads();
+      const int k = k0 + tid;
+      tile[tid] = k < n ? losses[2 * k + 1] - losses[2 * k] : 0.f;
+      __syncthreads();
+      const int kn = n - k0 < FT ? n - k0 : FT;
+      for (int t = 0; t < kn; ++t) rank += rank_before(tile[t], k0 + t, fj, j) ? 1 : 0;
+    }
+    if (j < n) ranked[j] = (float)rank / denom - 0.5f;
+  }
+  const float nbad = block_sum(bad, red);  // its barriers also order the `ranked` writes
+  for (int i = tid; i < pairs; i += FT) {
+    float acc = 0.f;
+    for (int j = i; j < n; j += pairs) acc += ranked[j];
     weight[i] = acc;
   }
   if (tid == 0 && status) *status = nbad > 0.f ? NOISE_ENONFINITE : NOISE_OK;
@@ -186,6 +230,14 @@ extern "C" int noise_fitness(const float* losses, int n_losses, int pairs, float
   NOISE_REQUIRE(n_losses >= 2 && n_losses % 2 == 0, "fitness: n_losses=%d must be even and >= 2", n_losses);
   fitness_kernel<<<1, FT, 0, (hipStream_t)stream>>>(losses, n_losses / 2, pairs, weight, status_out);
   return noise::check_launch("fitness");
+}
+
+extern "C" int noise_fitness_ranks(const float* losses, int n_losses, int pairs, float* weight, float* ranked,
+                                   int* status_out, void* stream) {
+  NOISE_REQUIRE(losses && weight && ranked && pairs > 0, "fitness_ranks: bad arguments");
+  NOISE_REQUIRE(n_losses >= 2 && n_losses % 2 == 0, "fitness_ranks: n_losses=%d must be even and >= 2", n_losses);
+  fitness_ranks_kernel<<<1, FT, 0, (hipStream_t)stream>>>(losses, n_losses / 2, pairs, weight, ranked, status_out);
+  return noise::check_launch("fitness_ranks");
 }
 
 extern "C" int64_t noise_es_gradient_work(int n, int out, int in) {

@@ -10,7 +10,9 @@ reference's interface and bookkeeping:
 * members [rank * per_rank, (rank + 1) * per_rank) in chunks of 2 * CHUNK, member 2j / 2j+1 of a
   chunk being pair (start + 2j) % (2 pairs) // 2 at +sigma / -sigma (eggroll.py:137-146);
 * all_gather of the losses across ranks (eggroll.py:147-150), then the fitness, the rank-1
-  gradient rebuild and `optimizer.step()` (eggroll.py:151-167); returns the mean loss.
+  gradient rebuild and `optimizer.step()` (eggroll.py:151-167); returns the mean loss. The fitness
+  is the reference's z-score of the antithetic differences; `fitness='ranks'` replaces it by their
+  centred ranks (rank / (n - 1) - 0.5, stable ascending order).
 
 What changes is where the work runs: the forward is the fused kernels of noise_amd.population
 (pairs are passed once, each kernel maps member p to pair row p >> 1 instead of repeating the
@@ -31,7 +33,11 @@ NOISE = 2 ** 28
 
 
 class Eggroll:
-    def __init__(self, model, pairs, rank=0, world=1, sigma=SIGMA, chunk=CHUNK, noise_size=NOISE, seed=SEED):
+    def __init__(self, model, pairs, rank=0, world=1, sigma=SIGMA, chunk=CHUNK, noise_size=NOISE, seed=SEED,
+                 fitness='zscore'):
+        if fitness not in ('zscore', 'ranks'):
+            raise ValueError(f"fitness must be 'zscore' (the reference's) or 'ranks', not {fitness!r}")
+        self.fitness = fitness
         self.model, self.pairs, self.rank, self.world = model, pairs, rank, world
         self.sigma, self.chunk, self.noise_size, self.seed = sigma, chunk, noise_size, seed
         self.device = next(model.parameters()).device
@@ -125,7 +131,8 @@ class Eggroll:
             losses = torch.cat(gathered)
         n = losses.numel() // 2
         weight = torch.empty(pairs, device=self.device)
-        K.fitness(losses, pairs, weight, self.status)
+        ranked = torch.empty(n, device=self.device) if self.fitness == 'ranks' else None
+        K.fitness(losses, pairs, weight, self.status, self.fitness, ranked)
         need = max(K.es_gradient_work(pairs, s[0], s[1] if len(s) == 2 else 1) for s in self.shapes.values())
         if self.grad_work is None or self.grad_work.numel() < need:
             self.grad_work = torch.empty(max(need, 1), device=self.device)
@@ -137,10 +144,13 @@ class Eggroll:
             else:
                 K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name],
                               work=self.grad_work)
-        if int(self.status.item()) != 0:  # checked before the weights move
+        # One host sync per step: the status and the mean loss come back together, before the
+        # weights move (the reference reads only the mean, eggroll.py:168).
+        status, mean = torch.stack([self.status[0].to(torch.float32), losses.mean()]).tolist()
+        if status != 0:
             raise FloatingPointError('non-finite member loss in the population step')
         optimizer.zero_grad(set_to_none=True)
         for name, p in self.params.items():
             p.grad = self.grads[name]
         optimizer.step()
-        return losses.mean().item()
+        return mean

@@ -254,10 +254,21 @@ def cast_bf16(x, hi, lo=None):
     _lib.call('noise_cast_bf16', _ptr(x), x.numel(), _ptr(hi), _ptr(lo), _stream())
 
 
-def fitness(losses, pairs, weight, status):
-    _on_gpu(losses, weight, status)
+def fitness(losses, pairs, weight, status, mode='zscore', ranked=None):
+    """weight [pairs] from antithetic losses: the reference z-score (mode 'zscore') or centred ranks
+    ('ranks'; `ranked` [len(losses) / 2] receives the per-pair values)."""
+    _on_gpu(losses, weight, status, ranked)
     _need(losses.dtype == torch.float32 and losses.is_contiguous(), 'fitness: fp32 losses')
-    _lib.call('noise_fitness', _ptr(losses), losses.numel(), pairs, _ptr(weight), _ptr(status), _stream())
+    _need(weight.dtype == torch.float32 and weight.is_contiguous() and weight.numel() >= pairs, 'fitness: weight')
+    if mode == 'zscore':
+        _lib.call('noise_fitness', _ptr(losses), losses.numel(), pairs, _ptr(weight), _ptr(status), _stream())
+    elif mode == 'ranks':
+        _need(ranked is not None and ranked.dtype == torch.float32 and ranked.is_contiguous() and
+              ranked.numel() >= losses.numel() // 2, 'fitness: ranks mode needs ranked [len(losses) / 2] fp32')
+        _lib.call('noise_fitness_ranks', _ptr(losses), losses.numel(), pairs, _ptr(weight), _ptr(ranked),
+                  _ptr(status), _stream())
+    else:
+        raise ValueError(f"fitness mode must be 'zscore' or 'ranks', not {mode!r}")
 
 
 def es_gradient_work(n, out, inn):

@@ -1,9 +1,12 @@
 """AdamW on the libnoise_amd kernel (torch.optim.AdamW semantics, as train/val/eggroll.py:205 builds it).
 
-When the parameters are views that exactly tile one flat fp32 buffer (a `noise_amd.model.GPT`
-and its gradients from `Eggroll`), the whole update is one launch; otherwise one launch per
-parameter. `lr` may be changed between steps through `param_groups` like any torch optimizer
-(the reference's warmdown writes `group['lr']`, eggroll.py:208-212).
+The per-parameter state has torch.optim.AdamW's own keys and layout -- 'step' (a 0-dim float
+tensor), 'exp_avg', 'exp_avg_sq' -- so `state_dict()` / `load_state_dict()` round-trip it like
+torch's. When the parameters (and their gradients) are views that exactly tile one flat fp32
+buffer (a `noise_amd.model.GPT` and the gradients `Eggroll` sets), every state tensor is a view of
+one flat moment buffer laid out the same way and the whole update is one launch; otherwise one
+launch per parameter on the same state. `lr` may be changed between steps through `param_groups`
+like any torch optimizer (the reference's warmdown writes `group['lr']`, eggroll.py:208-212).
 """
 import torch
 
@@ -18,7 +21,8 @@ def _flat_base(tensors):
     storage = base.untyped_storage().data_ptr()
     off = base.storage_offset()
     for t in tensors:
-        if (t.untyped_storage().data_ptr() != storage or t.storage_offset() != off or not t.is_contiguous()):
+        if (t.untyped_storage().data_ptr() != storage or t.storage_offset() != off or not t.is_contiguous()
+                or t.dtype != base.dtype or t.device != base.device):
             return None
         off += t.numel()
     total = off - tensors[0].storage_offset()
@@ -27,9 +31,35 @@ def _flat_base(tensors):
 
 
 class AdamW(torch.optim.Optimizer):
-    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0):
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2):
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay))
-        self._flat = {}  # group index -> moments of a flat group
+
+    def _state(self, p):
+        st = self.state[p]
+        if not st:
+            st['step'] = torch.tensor(0.0)
+            st['exp_avg'] = torch.zeros_like(p)
+            st['exp_avg_sq'] = torch.zeros_like(p)
+        return st
+
+    def _flat_moments(self, params, pflat):
+        """(exp_avg, exp_avg_sq) flat buffers laid out like pflat whose views are the params'
+        state tensors; states that are not such views yet (new, or loaded from a state dict) are
+        gathered into fresh buffers first. None if the params are at different steps."""
+        states = [self._state(p) for p in params]
+        if len({float(st['step']) for st in states}) != 1:
+            return None
+        flats = []
+        for key in ('exp_avg', 'exp_avg_sq'):
+            flat = _flat_base([st[key] for st in states])
+            if flat is None or flat.numel() != pflat.numel() or flat.device != pflat.device:
+                flat = torch.cat([st[key].reshape(-1).to(pflat.device, torch.float32) for st in states])
+                off = 0
+                for p, st in zip(params, states):
+                    st[key] = flat[off:off + p.numel()].view_as(p)
+                    off += p.numel()
+            flats.append(flat)
+        return flats
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -37,30 +67,25 @@ class AdamW(torch.optim.Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        for gi, group in enumerate(self.param_groups):
+        for group in self.param_groups:
             params = [p for p in group['params'] if p.grad is not None]
             if not params:
                 continue
             beta1, beta2 = group['betas']
-            state = self._flat.setdefault(gi, {})
+            args = (group['lr'], beta1, beta2, group['eps'], group['weight_decay'])
             pflat = _flat_base(params)
             gflat = _flat_base([p.grad for p in params])
-            if pflat is not None and gflat is not None:
-                if 'exp_avg' not in state or state['exp_avg'].numel() != pflat.numel():
-                    state['exp_avg'] = torch.zeros_like(pflat)
-                    state['exp_avg_sq'] = torch.zeros_like(pflat)
-                    state['step'] = 0
-                state['step'] += 1
-                K.adamw(pflat, gflat, state['exp_avg'], state['exp_avg_sq'], group['lr'], beta1, beta2,
-                        group['eps'], group['weight_decay'], state['step'])
+            flats = self._flat_moments(params, pflat) if pflat is not None and gflat is not None else None
+            if flats is not None:
+                for p in params:
+                    self.state[p]['step'] += 1
+                K.adamw(pflat, gflat, flats[0], flats[1], *args, int(self.state[params[0]]['step']))
                 continue
             for p in params:
-                st = self.state[p]
-                if not st:
-                    st['exp_avg'] = torch.zeros_like(p)
-                    st['exp_avg_sq'] = torch.zeros_like(p)
-                    st['step'] = 0
+                st = self._state(p)
                 st['step'] += 1
-                K.adamw(p, p.grad.contiguous(), st['exp_avg'], st['exp_avg_sq'], group['lr'], beta1, beta2,
-                        group['eps'], group['weight_decay'], st['step'])
+                for key in ('exp_avg', 'exp_avg_sq'):
+                    if not st[key].is_contiguous():
+                        st[key] = st[key].contiguous()
+                K.adamw(p, p.grad.contiguous(), st['exp_avg'], st['exp_avg_sq'], *args, int(st['step']))
         return loss

@@ -29,6 +29,15 @@ def centred_ranks(f):
     return ranks.to(f.dtype) / max(n - 1, 1) - 0.5
 
 
+def fitness_ranks(losses, pairs):
+    """The rank-normalised variant of `fitness`: centred ranks of the same antithetic differences,
+    index_add into the pair slots (the mode of this build named by config 4; the reference's own
+    fitness is the z-score of eggroll.py:151-152). Returns (weight, ranked, n)."""
+    f = losses[1::2] - losses[0::2]
+    r = centred_ranks(f)
+    return torch.zeros(pairs, dtype=f.dtype).index_add_(0, torch.arange(len(f)) % pairs, r), r, len(f)
+
+
 def gradient(weight, pair_noise, n):
     """name -> gradient for the weights w [pairs] of the pair noise (a, b) / eps."""
     out = {}

@@ -22,6 +22,13 @@ def golden():
 
 
 @pytest.fixture(scope='session')
+def golden_autocast():
+    """The reference's population losses under bf16 autocast (tests/golden/make_golden.py --autocast)."""
+    with np.load(GOLDEN / 'golden_autocast.npz', allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope='session')
 def golden_json():
     import json
     return json.loads((GOLDEN / 'golden.json').read_text())

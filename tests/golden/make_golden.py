@@ -123,5 +123,33 @@ def main(ref_root):
     print(json.dumps({k: summary[k] for k in ('config0', 'sensitive', 'window_sizes')}, indent=1))
 
 
+def autocast_losses(ref_root):
+    """golden_autocast.npz: the reference's population_loss on the config-0 and sensitive inputs
+    again, under torch.autocast('cpu', dtype=torch.bfloat16) -- the bf16 arithmetic its trainer
+    runs the population forward in (train/val/eggroll.py:144-145 wraps the call in bf16 autocast,
+    there on the GPU). The distance between these and the fp32 losses of golden.npz is the
+    envelope of a correct bf16 evaluation of the reference's own forward."""
+    sys.path.insert(0, str(ref_root))
+    from train.val.eggroll import make_model, population_loss
+
+    torch.set_grad_enabled(False)
+    model = make_model(torch.device('cpu'), 0)
+    params = dict(model.named_parameters())
+    arrays = {}
+    for tag, cfg, p in (('config0', CONFIG0, params),
+                        ('sensitive', SENSITIVE, sensitive_weights(params, SENSITIVE['weight_seed']))):
+        idx, targets = sequence(cfg['length'], seed=cfg['token_seed'])
+        noise, sign = antithetic(pair_noise(cfg['pairs'], seed=cfg['noise_seed']), cfg['sigma'])
+        with torch.autocast('cpu', dtype=torch.bfloat16):
+            losses = population_loss(model, p, noise, sign, idx, targets)
+        arrays[tag + '/losses_autocast'] = losses.float().numpy()
+    np.savez_compressed(HERE / 'golden_autocast.npz', **arrays)
+    print(json.dumps({k: [float(x) for x in v] for k, v in arrays.items()}, indent=1))
+
+
 if __name__ == '__main__':
-    main(Path(sys.argv[1] if len(sys.argv) > 1 else '/root/reference'))
+    root = Path(sys.argv[1] if len(sys.argv) > 1 else '/root/reference')
+    if '--autocast' in sys.argv:
+        autocast_losses(root)
+    else:
+        main(root)

@@ -327,6 +327,103 @@ def test_fitness_gradient_adamw(device):
     torch.testing.assert_close(dp.cpu(), refp.detach(), rtol=0, atol=1e-6)
 
 
+def test_adamw_state_dict_round_trip(device):
+    """noise_amd.AdamW keeps torch.optim.AdamW's state format: after two one-launch steps on a GPT
+    whose parameters and gradients tile flat buffers, state_dict() holds every moment and the step;
+    an optimizer restored from it takes the same next step bit for bit, torch.optim.AdamW loads the
+    same state dict and takes the same step, and the per-parameter path (gradients that do not
+    tile) continues from the same moments."""
+    import copy
+    import noise_amd
+    from noise_amd.optim import AdamW
+    g = _gen(13)
+
+    def model_with_grads():
+        m = noise_amd.make_model(device, 0)
+        ps = list(m.parameters())
+        flat = torch.empty(sum(p.numel() for p in ps), device=device)
+        off = 0
+        for p in ps:
+            p.grad = flat[off:off + p.numel()].view_as(p)
+            off += p.numel()
+        return m, ps, flat
+
+    hyper = dict(lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.01)
+    m1, ps1, g1 = model_with_grads()
+    opt1 = AdamW(m1.parameters(), **hyper)
+    grads = [torch.randn(g1.numel(), generator=g).to(device) * 1e-3 for _ in range(4)]
+    for k in range(2):
+        g1.copy_(grads[k])
+        opt1.step()
+    sd = copy.deepcopy(opt1.state_dict())
+    assert len(sd['state']) == len(ps1)
+    assert all(float(st['step']) == 2 and st['exp_avg'].shape == ps1[i].shape and bool(st['exp_avg_sq'].any())
+               for i, st in sd['state'].items())
+
+    m2, ps2, g2 = model_with_grads()
+    with torch.no_grad():
+        for a, b in zip(ps2, ps1):
+            a.copy_(b)
+    opt2 = AdamW(m2.parameters(), **hyper)
+    opt2.load_state_dict(sd)
+    ref = [p.detach().clone().requires_grad_(True) for p in ps1]
+    opt_t = torch.optim.AdamW(ref, **hyper)
+    opt_t.load_state_dict(copy.deepcopy(sd))
+    g1.copy_(grads[2])
+    g2.copy_(grads[2])
+    opt1.step()
+    opt2.step()
+    off = 0
+    for r in ref:
+        r.grad = grads[2][off:off + r.numel()].view_as(r).clone()
+        off += r.numel()
+    opt_t.step()
+    for a, b, r in zip(ps1, ps2, ref):
+        assert torch.equal(a, b)
+        torch.testing.assert_close(a, r.detach(), rtol=0, atol=1e-6)
+
+    # The per-parameter path (separate gradient tensors) on optimizer 2 follows optimizer 1's flat step.
+    for p, gg in zip(ps2, torch.split(grads[3], [p.numel() for p in ps2])):
+        p.grad = gg.view_as(p).clone()
+    g1.copy_(grads[3])
+    opt1.step()
+    opt2.step()
+    for a, b in zip(ps1, ps2):
+        torch.testing.assert_close(a, b, rtol=0, atol=1e-7)
+
+
+def test_fitness_ranks_bit_exact(device):
+    """Centred-rank fitness on 3072 losses (1536 pairs) with planted ties -- equal differences,
+    +0.0 / -0.0, duplicated blocks -- bit-exact to the oracle's stable-argsort ranks, including the
+    wrap into fewer pair slots and the non-finite status."""
+    from oracle import es_ref
+    g = _gen(12)
+    pairs = 1536
+    losses = torch.randn(2 * pairs, generator=g) * 0.01 + 8
+    losses[2 * 100 + 1] = losses[2 * 100]                  # f = +0
+    losses[2 * 101 + 1], losses[2 * 101] = 8.0, 8.0        # f = 0 again
+    losses[2 * 102 + 1], losses[2 * 102] = -0.0, 0.0       # f = -0.0
+    losses[2 * 300:2 * 340] = losses[2 * 500:2 * 540]      # 40 duplicated differences
+    q = (torch.randint(0, 9, (pairs,), generator=g) * 2 ** -10).float()  # coarse grid: many ties
+    losses[1:2 * 900:2][:600] = losses[0:2 * 900:2][:600] + q[:600]
+    for slots in (pairs, 1000):
+        w_ref, r_ref, n = es_ref.fitness_ranks(losses, slots)
+        w = torch.empty(slots, device=device)
+        ranked = torch.empty(n, device=device)
+        status = torch.full((1,), 7, dtype=torch.int32, device=device)
+        nk.fitness(losses.to(device), slots, w, status, mode='ranks', ranked=ranked)
+        assert torch.equal(ranked.cpu(), r_ref)
+        assert torch.equal(w.cpu(), w_ref)
+        assert int(status.item()) == 0
+    bad = losses.clone()
+    bad[5] = float('nan')
+    w = torch.empty(pairs, device=device)
+    nk.fitness(bad.to(device), pairs, w, status, mode='ranks', ranked=ranked)
+    assert int(status.item()) == _lib.NOISE_ENONFINITE
+    _, r_nan, _ = es_ref.fitness_ranks(bad, pairs)
+    assert torch.equal(ranked.cpu(), r_nan)  # NaN sorts last, as torch.argsort does
+
+
 @pytest.mark.parametrize('out,inn', [(512, 512), (70, 90), (300, 1)])
 def test_es_gradient_split_pairs(device, out, inn):
     """The gradient with the pair sum split over more workgroups (1536 pairs, as the population

@@ -32,7 +32,7 @@ def _sensitive(init_params):
     return sensitive_params(init_params)
 
 
-def test_config0_population_loss(device, init_params, golden, golden_json):
+def test_config0_population_loss(device, init_params, golden, golden_json, golden_autocast):
     c = golden_json['config0']
     idx, targets = t(golden['config0/idx']), t(golden['config0/targets'])
     noise, sign = antithetic(pair_noise(c['pairs'], seed=c['noise_seed']), c['sigma'])
@@ -43,9 +43,11 @@ def test_config0_population_loss(device, init_params, golden, golden_json):
     assert float((got - oracle).abs().max()) <= 1e-4
     print('max |gpu - reference golden|', float((got - t(golden['config0/losses'])).abs().max()))
     assert float((got - t(golden['config0/losses'])).abs().max()) <= 1e-4
+    # and the reference's own bf16-autocast losses (its trainer's arithmetic, eggroll.py:144-145)
+    assert float((got - t(golden_autocast['config0/losses_autocast'])).abs().max()) <= 1e-4
 
 
-def test_sensitive_population_loss(device, init_params, golden, golden_json):
+def test_sensitive_population_loss(device, init_params, golden, golden_json, golden_autocast):
     c = golden_json['sensitive']
     p = _sensitive(init_params)
     idx, targets = t(golden['sensitive/idx']), t(golden['sensitive/targets'])
@@ -62,9 +64,16 @@ def test_sensitive_population_loss(device, init_params, golden, golden_json):
     err = float((got.double() - oracle).abs().max())
     print('sensitive gpu', got.tolist(), 'max |gpu - oracle|', err, 'envelope', envelope)
     assert err <= 1e-4 + 4 * envelope
-    # The bf16 cast points alone put the oracle's build policy ~2e-3 from the reference's fp32
-    # losses on these weights; the GPU path must stay within 5e-3 of them.
-    assert float((got - t(golden['sensitive/losses'])).abs().max()) <= 5e-3
+    # Against the reference itself: its own bf16-autocast losses (the arithmetic its trainer runs,
+    # eggroll.py:144-145) lie 2.5e-3 from its fp32 losses on these weights. A correct bf16
+    # evaluation is held to that envelope (and to the plain 1e-4 where the envelope is smaller),
+    # from both fixtures.
+    ref32, ref16 = t(golden['sensitive/losses']), t(golden_autocast['sensitive/losses_autocast'])
+    bar = max(1e-4, float((ref16 - ref32).abs().max()))
+    print('sensitive: |gpu - ref fp32|', float((got - ref32).abs().max()), '|gpu - ref autocast|',
+          float((got - ref16).abs().max()), 'bar', bar)
+    assert float((got - ref32).abs().max()) <= bar
+    assert float((got - ref16).abs().max()) <= bar
 
 
 def test_clean_forward_matches_reference(device, init_params, golden):
@@ -219,6 +228,52 @@ def test_eggroll_step_matches_oracle(device, init_params):
     for name, p in model.named_parameters():
         g = es.grads[name].cpu().double()
         torch.testing.assert_close(g, grads[name], rtol=1e-4, atol=1e-6 * float(grads[name].abs().max()))
+        ref = before[name].clone()
+        es_ref.adamw_step(ref, es.grads[name].cpu(), torch.zeros_like(ref), torch.zeros_like(ref), 1, 1e-3, (0.5, 0.95))
+        torch.testing.assert_close(p.detach().cpu(), ref, rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize('mode', ['zscore', 'ranks'])
+def test_eggroll_step_multi_sequence(device, init_params, mode):
+    """Eggroll.step with 3 sequences and 2 pairs (train/val/eggroll.py:133-167): members = 2 x 3,
+    each sequence gets one antithetic pair, sequence 2 reuses pair 0 (the j % pairs wrap of the
+    fitness), one pair per forward chunk. Member losses, fitness weights, gradients and the AdamW
+    update against the oracle, in the reference's z-score mode and the centred-rank mode."""
+    model = noise_amd.make_model(device, 0)
+    es = noise_amd.Eggroll(model, pairs=2, chunk=1, noise_size=1 << 22, fitness=mode)
+    opt = noise_amd.AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    T, B = 128, 3
+    seqs = [sequence(T, seed=60 + k) for k in range(B)]
+    x = torch.stack([a for a, _ in seqs]).to(device)
+    y = torch.stack([b for _, b in seqs]).to(device)
+    offsets = es.offsets(1)
+    before = {k: v.detach().cpu().clone() for k, v in model.named_parameters()}
+    gpu_losses = es.population_losses(x, y, offsets).cpu()
+    assert gpu_losses.shape == (2 * B,)
+    pair_of_seq = [0, 1, 0]
+    want = []
+    for k in range(B):
+        one = {n: tuple(v.cpu() for v in nz) if isinstance(nz, tuple) else nz.cpu()
+               for n, nz in es.noise(offsets, torch.tensor([pair_of_seq[k]], device=device)).items()}
+        noise, sign = antithetic(one, es.sigma)
+        want.append(R.population_loss(before, noise, sign, seqs[k][0], seqs[k][1], policy='build').float())
+    want = torch.cat(want)
+    assert float((gpu_losses - want).abs().max()) <= 1e-4
+
+    mean = es.step(x, y, opt, 1)
+    assert abs(mean - float(gpu_losses.mean())) <= 1e-6
+    if mode == 'zscore':
+        w, n = es_ref.fitness(gpu_losses.double(), 2)
+    else:
+        w, _, n = es_ref.fitness_ranks(gpu_losses, 2)
+        w = w.double()
+    assert n == 3
+    pair = {k: tuple(v.cpu() for v in nz) if isinstance(nz, tuple) else nz.cpu()
+            for k, nz in es.noise(offsets, torch.arange(2, device=device)).items()}
+    grads = es_ref.gradient(w, pair, n)
+    for name, p in model.named_parameters():
+        g = es.grads[name].cpu().double()
+        torch.testing.assert_close(g, grads[name], rtol=1e-4, atol=1e-6 * float(grads[name].abs().max()) + 1e-12)
         ref = before[name].clone()
         es_ref.adamw_step(ref, es.grads[name].cpu(), torch.zeros_like(ref), torch.zeros_like(ref), 1, 1e-3, (0.5, 0.95))
         torch.testing.assert_close(p.detach().cpu(), ref, rtol=0, atol=2e-6)

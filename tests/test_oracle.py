@@ -42,6 +42,27 @@ def test_init_matches_reference(init_params, golden, golden_json):
             assert torch.equal(init_params[key[5:]][:8, :16], t(golden[key])), key
 
 
+def test_product_make_model_matches_reference(golden, golden_json):
+    """noise_amd.make_model (the shipped init, train/val/eggroll.py:38-53 over utils/model.py:149-175)
+    on the CPU reproduces the reference's seed-0 parameters: the golden heads, sums and 8 x 16
+    corners written by the reference itself, in named_parameters() order (the draw order is the
+    seed-parity contract), and bit-equal to the oracle's restatement."""
+    import noise_amd
+    from oracle.model_ref import init_params
+    model = noise_amd.make_model('cpu', 0)
+    params = dict(model.named_parameters())
+    assert [n for n in params] == [n for n, _ in golden_json['named_parameters']]
+    for name, p in params.items():
+        ref = golden_json['init'][name]
+        assert [float(v) for v in p.detach().flatten()[:4]] == ref['head'], name
+        assert abs(float(p.double().sum()) - ref['sum']) <= 1e-9 * max(1.0, abs(ref['sum'])) + 1e-6, name
+    for key in golden:
+        if key.startswith('init/'):
+            assert torch.equal(params[key[5:]].detach()[:8, :16], t(golden[key])), key
+    oracle = init_params(0)
+    assert all(torch.equal(params[n].detach(), oracle[n]) for n in oracle)
+
+
 def test_rotary_tables_bit_exact(golden):
     cos, sin = R.rotary_tables(2048)
     bits = lambda x: x.bfloat16().view(torch.int16).numpy().view(np.uint16)
@@ -108,6 +129,27 @@ def test_population_loss_matches_reference_sensitive(init_params, golden, golden
     torch.testing.assert_close(losses, t(golden['sensitive/losses']), rtol=0, atol=2e-5)
     clean = R.clean_loss(p, idx[None], targets[None], policy='fp32')[0]
     torch.testing.assert_close(clean, t(golden['sensitive/clean']), rtol=0, atol=5e-5)
+
+
+def test_build_policy_within_reference_autocast_envelope(init_params, golden, golden_json, golden_autocast):
+    """The oracle's bf16 build policy against the reference's own bf16-autocast losses
+    (eggroll.py:144-145 wraps population_loss in torch.autocast): on both fixtures it stays
+    within max(1e-4, |ref_autocast - ref_fp32|), the spread the reference's own two arithmetics
+    show, of each of them."""
+    for tag in ('config0', 'sensitive'):
+        c = golden_json[tag]
+        p = init_params if tag == 'config0' else sensitive_params(init_params, c['weight_seed'])
+        idx, targets, noise, sign = _config_inputs(golden, tag, c['pairs'], c['sigma'], c['noise_seed'])
+        build = R.population_loss(p, noise, sign, idx, targets, policy='build').float()
+        ref32, ref16 = t(golden[f'{tag}/losses']), t(golden_autocast[f'{tag}/losses_autocast'])
+        bar = max(1e-4, float((ref16 - ref32).abs().max()))
+        assert float((build - ref32).abs().max()) <= bar, tag
+        assert float((build - ref16).abs().max()) <= bar, tag
+        if tag == 'sensitive':
+            assert 1e-3 < bar < 5e-3   # the envelope is the bf16 casts', not a loose guess
+        # the antithetic differences, what the fitness reads, keep their signs under both arithmetics
+        d = lambda v: v[0::2] - v[1::2]
+        assert torch.equal(torch.sign(d(build)), torch.sign(d(ref16))), tag
 
 
 def test_clean_forward_matches_reference(init_params, golden):
@@ -242,6 +284,31 @@ def test_fitness_matches_brute_force():
     w2, n2 = es_ref.fitness(losses, 4)
     full = torch.tensor([x / (std + 1e-8) for x in f], dtype=torch.float64)
     torch.testing.assert_close(w2, torch.stack([full[0] + full[4], full[1] + full[5], full[2], full[3]]))
+
+
+def test_centred_ranks_pinned():
+    """es_ref.centred_ranks against scipy's ordinal ranking (ties in order of appearance, the order a
+    stable ascending sort leaves them in), a hand-worked case with ties and a signed zero, and the
+    defining properties: a permutation of 0..n-1 scaled into [-0.5, 0.5], monotone in f."""
+    from scipy.stats import rankdata
+    f = torch.tensor([3.0, 1.0, 2.0, 1.0, -0.0, 0.0])
+    # sorted: -0.0 (idx 4) = 0.0 (idx 5) < 1 (idx 1) = 1 (idx 3) < 2 < 3 -> ranks 5, 2, 4, 3, 0, 1
+    want = torch.tensor([5, 2, 4, 3, 0, 1], dtype=torch.float32) / 5 - 0.5
+    assert torch.equal(es_ref.centred_ranks(f), want)
+    g = torch.Generator().manual_seed(11)
+    for n in (1, 2, 7, 500):
+        x = torch.randint(-20, 20, (n,), generator=g).float() / 4  # many ties
+        r = es_ref.centred_ranks(x)
+        ordinal = torch.from_numpy(rankdata(x.numpy(), method='ordinal')).float() - 1
+        assert torch.equal(r, ordinal / max(n - 1, 1) - 0.5)
+        assert torch.round((r.double() + 0.5) * max(n - 1, 1)).sort()[0].tolist() == [float(k) for k in range(n)]
+        i, j = torch.triu_indices(n, n, 1)
+        assert bool(((x[i] < x[j]) <= (r[i] < r[j])).all())
+    # rank-mode fitness: more differences than pairs wrap around like the z-score's index_add
+    losses = torch.tensor([0.0, 3.0, 0.0, 1.0, 0.0, 2.0, 5.0, 6.0])  # f = 3, 1, 2, 1
+    w, r, n = es_ref.fitness_ranks(losses, 3)
+    assert n == 4 and torch.equal(r, torch.tensor([3, 0, 2, 1], dtype=torch.float32) / 3 - 0.5)
+    assert torch.equal(w, torch.stack([r[0] + r[3], r[1], r[2]]))
 
 
 def test_gradient_matches_brute_force():
