@@ -209,10 +209,16 @@ typedef struct {
   const int64_t* targets; /* target of row p*T + t: targets[p * targets_stride + t] */
   int64_t targets_stride;
   float* ce;             /* out [M] per-token cross-entropy */
+  int64_t ignore_index;  /* a row whose target equals this gets ce = 0 (F.cross_entropy's
+                            ignore_index: -100 by default, -1 in GPT.forward); any other target
+                            outside [0, V) gives ce = NaN */
+  float* logits;         /* NULL, or out [M, ld_logits] fp32: the capped logits 15 tanh(z / 15) */
+  int64_t ld_logits;     /* >= V */
 } noise_head_t;
 
 /* logits = h (W + s a b^T)^T in fp32 accuracy, 15 tanh(logits / 15), cross-entropy against
- * the target (train/val/eggroll.py:94-102; utils/model.py:203-209). V % 256 == 0. */
+ * the target (train/val/eggroll.py:94-102; utils/model.py:203-209), and, when `logits` is set,
+ * the capped logits themselves (utils/model.py:203-204, 210). V % 256 == 0. */
 int noise_head_ce(const noise_head_t* args, void* stream);
 
 /* out[p] = mean over t of ce[p*T + t] (eggroll.py:102). */

@@ -55,7 +55,7 @@ class Attention(C.Structure):
 class Head(C.Structure):
     _fields_ = [('h', P), ('w_hi', P), ('w_lo', P), ('M', INT), ('V', INT), ('T', INT),
                 ('member_shift', INT), ('sign', P), ('a', P), ('lda', I64), ('u', P), ('targets', P),
-                ('targets_stride', I64), ('ce', P)]
+                ('targets_stride', I64), ('ce', P), ('ignore_index', I64), ('logits', P), ('ld_logits', I64)]
 
 
 class Probe(C.Structure):

@@ -1,8 +1,9 @@
-// Perturbed fp32-accurate head + soft-cap + cross-entropy, logits never leave the chip.
+// Perturbed fp32-accurate head + soft-cap + cross-entropy; the logits leave the chip only when the
+// caller asks for them (the scoring forward without targets).
 //
 // Reference semantics (train/val/eggroll.py:94-102; utils/model.py:203-209): for every member
 // row r, z = h_r (W + s a b^T)^T over the whole vocabulary, z' = 15 tanh(z / 15), and
-// ce_r = logsumexp(z') - z'[target]. The reference materialises [32, T, V] fp32 logits per slice;
+// ce_r = logsumexp(z') - z'[target], or 0 when the target is the ignore_index. The reference materialises [32, T, V] fp32 logits per slice;
 // here a workgroup (8 waves) owns 256 rows and sweeps the vocabulary in 256-column tiles of
 // mma_tile<256> (measured 5% faster than two 4-wave workgroups on 128-column tiles), keeping only
 // per-row running sums of exp(z') (the soft-cap bounds z' to [-15, 15], so no running max is
@@ -22,7 +23,11 @@ constexpr int HT = HCfg::THREADS;
 
 // ALIGNED: every 256-row tile lies inside one member (T % 256 == 0), so the rank-1 vector a is one
 // row per tile; the general instantiation reads a per row (and is only used for ragged T).
-template <bool ALIGNED>
+// LOGITS: also store every capped logit (the scoring forward without targets); the loss-only
+// instantiation keeps no trace of the store.
+constexpr int TGT_IGNORED = -2, TGT_INVALID = -1;
+
+template <bool ALIGNED, bool LOGITS>
 __global__ void __attribute__((amdgpu_flat_work_group_size(HT, HT), amdgpu_waves_per_eu(2, 2)))
 head_ce_kernel(const noise_head_t g) {
   // One LDS object (per-row data first, where every access is an immediate offset, then the tile
@@ -45,11 +50,11 @@ head_ce_kernel(const noise_head_t g) {
   if (tid < 256) {
     const int row = m0 + tid;
     float su = 0.f;
-    int tg = -1;
+    int tg = TGT_INVALID;
     if (row < g.M) {
       if (perturbed) su = g.sign[row / T] * g.u[row];
       const int64_t t = g.targets[(int64_t)(row / T) * g.targets_stride + row % T];
-      tg = (t >= 0 && t < g.V) ? (int)t : -1;
+      tg = (t >= 0 && t < g.V) ? (int)t : (t == g.ignore_index ? TGT_IGNORED : TGT_INVALID);
     }
     su_s[tid] = su;
     tgt_s[tid] = tg;
@@ -82,6 +87,7 @@ head_ce_kernel(const noise_head_t g) {
     const float c = __builtin_fmaf(-30.0f, __builtin_amdgcn_rcpf(t + 1.0f), 15.0f);          \
     e += __builtin_amdgcn_exp2f(c * 1.4426950408889634f);                                    \
     if (colbase + ni * 32 == tg) tz_s[rl] = c;                                               \
+    if (LOGITS && m0 + rl < g.M) g.logits[(int64_t)(m0 + rl) * g.ld_logits + colbase + ni * 32] = c; \
   }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
@@ -127,7 +133,7 @@ head_ce_kernel(const noise_head_t g) {
     float tot = 0.f;
 #pragma unroll
     for (int c = 0; c < HWN; ++c) tot += sum_s[c][tid];
-    if (row < g.M) g.ce[row] = logf(tot) - tz_s[tid];
+    if (row < g.M) g.ce[row] = tgt_s[tid] == TGT_IGNORED ? 0.f : logf(tot) - tz_s[tid];
   }
 }
 
@@ -141,10 +147,19 @@ extern "C" int noise_head_ce(const noise_head_t* args, void* stream) {
   NOISE_REQUIRE(!g.sign || (g.a && g.u && g.lda >= g.V), "head_ce: perturbation needs a [*, V] and u");
   NOISE_REQUIRE(((uintptr_t)g.h % 16) == 0 && ((uintptr_t)g.w_hi % 16) == 0 && ((uintptr_t)g.w_lo % 16) == 0,
                 "head_ce: h and weights must be 16-byte aligned");
+  NOISE_REQUIRE(!g.logits || g.ld_logits >= g.V, "head_ce: ld_logits=%lld < V=%d", (long long)g.ld_logits, g.V);
+  NOISE_REQUIRE(g.ignore_index < 0 || g.ignore_index >= g.V,
+                "head_ce: ignore_index=%lld is a class index; only out-of-range values can be ignored",
+                (long long)g.ignore_index);
   if (g.M == 0) return NOISE_OK;
-  if (g.T % 256 == 0)
-    head_ce_kernel<true><<<(g.M + 255) / 256, HT, 0, (hipStream_t)stream>>>(g);
-  else
-    head_ce_kernel<false><<<(g.M + 255) / 256, HT, 0, (hipStream_t)stream>>>(g);
+  const dim3 grid((g.M + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  if (g.T % 256 == 0) {
+    if (g.logits) head_ce_kernel<true, true><<<grid, HT, 0, s>>>(g);
+    else head_ce_kernel<true, false><<<grid, HT, 0, s>>>(g);
+  } else {
+    if (g.logits) head_ce_kernel<false, true><<<grid, HT, 0, s>>>(g);
+    else head_ce_kernel<false, false><<<grid, HT, 0, s>>>(g);
+  }
   return noise::check_launch("head_ce");
 }

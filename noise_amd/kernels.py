@@ -233,7 +233,10 @@ def window_attention(qkv16, y, members, T, window, b_proj=None, shift=0, u_proj=
     _lib.call('noise_window_attention', C.byref(g), _stream())
 
 
-def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_stride=0):
+def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_stride=0, ignore_index=-100,
+            logits=None):
+    """ce [M] (0 where the target is `ignore_index`); with `logits` [M, >= V] fp32 also the capped
+    logits."""
     g = Head()
     g.h, g.w_hi, g.w_lo = h.data_ptr(), w_hi.data_ptr(), w_lo.data_ptr()
     g.M, g.V, g.T = h.shape[0], w_hi.shape[0], T
@@ -241,6 +244,12 @@ def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_s
         g.sign, g.a, g.lda, g.u, g.member_shift = (sign.data_ptr(), nz.a.data_ptr(), nz.a.stride(0),
                                                    u.data_ptr(), nz.shift)
     g.targets, g.targets_stride, g.ce = targets.data_ptr(), targets_stride, ce.data_ptr()
+    g.ignore_index = ignore_index
+    if logits is not None:
+        _on_gpu(logits)
+        _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1 and
+              logits.shape[0] >= g.M and logits.shape[1] >= g.V, 'head_ce: logits must be fp32 [M, >= V] rows')
+        g.logits, g.ld_logits = logits.data_ptr(), logits.stride(0)
     _lib.call('noise_head_ce', C.byref(g), _stream())
 
 

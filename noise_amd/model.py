@@ -10,13 +10,16 @@ keys and shapes and round-trips through `load_state_dict(strict=True)` of the fi
   (train/val/eggroll.py:50-52).
 
 `forward(idx, targets)` is the sigma = 0 scoring forward (utils/model.py:193-210) on the same
-kernels as the population, returning the per-token losses reduced as `loss_reduction` says.
+kernels as the population, returning the per-token losses reduced as `loss_reduction` says, or,
+without targets, the capped logits.
 """
 import torch
 from torch import nn
 
 from .config import GPTConfig, VE_GATE_CHANNELS, has_ve, param_shapes, window_sizes
 from .population import clean_loss, rotary_tables
+
+IGNORE = -1  # GPT.forward's ignore_index (utils/model.py:208)
 
 
 class CausalSelfAttention(nn.Module):
@@ -107,16 +110,23 @@ class GPT(nn.Module):
                 torch.nn.init.zeros_(block.attn.ve_gate.weight)
 
     def forward(self, idx, targets=None, loss_reduction='mean'):
+        """utils/model.py:193-210. Without targets: the soft-capped logits [B, T, vocab] fp32.
+        With targets: their cross-entropy with ignore_index=-1 (a -1 target scores 0 and, under
+        'mean', is left out of the count), reduced as loss_reduction says."""
+        if loss_reduction not in ('mean', 'sum', 'none'):
+            raise ValueError(f'unknown loss_reduction {loss_reduction!r}')
+        params = dict(self.named_parameters())
+        B, T = idx.shape
         if targets is None:
-            raise NotImplementedError('only the loss forward runs on the fused head; pass targets')
-        ce = clean_loss(dict(self.named_parameters()), idx, targets, self.config)
+            logits = torch.empty(B, T, self.config.padded_vocab, dtype=torch.float32, device=idx.device)
+            clean_loss(params, idx, torch.full_like(idx, IGNORE), self.config, ignore_index=IGNORE, logits=logits)
+            return logits[..., :self.config.vocab_size]
+        ce = clean_loss(params, idx, targets, self.config, ignore_index=IGNORE)
         if loss_reduction == 'none':
             return ce.view(-1)
         if loss_reduction == 'sum':
             return ce.sum()
-        if loss_reduction == 'mean':
-            return ce.mean()
-        raise ValueError(f'unknown loss_reduction {loss_reduction!r}')
+        return ce.sum() / (targets != IGNORE).sum()
 
 
 def make_model(device, seed):

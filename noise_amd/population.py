@@ -137,11 +137,12 @@ class Engine:
         return self._rot[T]
 
     def forward(self, W, nz, sign, idx, targets, T, members, losses_out=None, ce_out=None,
-                idx_stride=0):
-        """Per-member mean CE into losses_out [members] (and per-token CE into ce_out).
+                idx_stride=0, ignore_index=-100, logits_out=None):
+        """Per-member mean CE into losses_out [members] (and per-token CE into ce_out, the capped
+        logits into logits_out [members * T, V] when given).
 
         nz: name -> NoiseRows for these members (None when sign is None). idx/targets: [T] shared
-        (idx_stride 0) or [members, T] (idx_stride T)."""
+        (idx_stride 0) or [members, T] (idx_stride T). A target equal to ignore_index scores 0."""
         cfg = self.cfg
         M = members * T
         ws = self.workspace(M)
@@ -195,7 +196,7 @@ class Engine:
         hd = g('lm_head.weight')
         K.mix_norm(x, h, T, sign, shift=shift, bs=(hd.b,) if pert else (), u=u1)
         out_ce = ce if ce_out is None else ce_out
-        K.head_ce(h, W.head_hi, W.head_lo, T, targets, out_ce, sign, hd, u1, idx_stride)
+        K.head_ce(h, W.head_hi, W.head_lo, T, targets, out_ce, sign, hd, u1, idx_stride, ignore_index, logits_out)
         if losses_out is not None:
             K.member_mean(out_ce, members, T, losses_out)
 
@@ -261,9 +262,13 @@ def population_loss(model, p, noise, sign, idx, targets, chunk=DEFAULT_CHUNK):
     return losses
 
 
-def clean_loss(model_params, idx, targets, cfg=GPTConfig(), batch_chunk=64):
-    """Per-token cross-entropy [B, T] of the unperturbed model on B sequences (utils/model.py:193-210)."""
+def clean_loss(model_params, idx, targets, cfg=GPTConfig(), batch_chunk=64, ignore_index=-100, logits=None):
+    """Per-token cross-entropy [B, T] of the unperturbed model on B sequences (utils/model.py:193-210):
+    0 where the target is `ignore_index`; `logits` [B, T, V] fp32, when given, receives the capped
+    logits."""
     device = model_params['transformer.wte.weight'].device
+    if device.type != 'cuda':
+        raise ValueError('clean_loss runs on the GPU; move the parameters to a HIP device')
     B, T = idx.shape
     W = PreparedWeights(model_params, cfg)
     eng = engine_for(device)
@@ -273,5 +278,6 @@ def clean_loss(model_params, idx, targets, cfg=GPTConfig(), batch_chunk=64):
     for lo in range(0, B, batch_chunk):
         hi = min(B, lo + batch_chunk)
         eng.forward(W, None, None, idx[lo:hi], targets[lo:hi], T, hi - lo, None, ce[lo:hi].view(-1),
-                    idx_stride=T)
+                    idx_stride=T, ignore_index=ignore_index,
+                    logits_out=None if logits is None else logits[lo:hi].view((hi - lo) * T, -1))
     return ce

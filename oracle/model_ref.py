@@ -28,7 +28,10 @@ Precision policies:
              weight stays fp32, the residual stream, norms, rank-1 terms, soft-cap and
              log-sum-exp stay full precision;
   'build32' -- the same cast points in float32 arithmetic. |build - build32| measures how far the
-             bf16 cast points alone let two correct implementations drift on given inputs.
+             bf16 cast points alone let two correct implementations drift on given inputs;
+  'score16' -- (clean_loss only) the reference's GPU scoring arithmetic, a bf16 residual stream
+             (`scoring_loss_bf16`), pinned against golden_scoring.npz: the reference's own
+             GPT.forward with bf16 embedding tables under CPU bf16 autocast.
 
 Pinning (tests/test_oracle.py): every function above against the reference's own outputs in
 golden.npz; the whole forward against the reference's population_loss and GPT.forward goldens;
@@ -164,7 +167,7 @@ def softcap_ce(logits, targets):
     return torch.logsumexp(z, -1) - z.gather(-1, targets.unsqueeze(-1)).squeeze(-1)
 
 
-def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTConfig()):
+def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTConfig(), capped_logits=False):
     """Per-token cross-entropy [m, T] of m perturbed models (or, with noise=None, of the clean
     model on the rows of idx [B, T]).
 
@@ -239,6 +242,8 @@ def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTC
         x = x + linear(pre + 'mlp.c_proj.weight', hid)
     hf = rb(rms_norm(x))
     logits = linear('lm_head.weight', hf, round_weight=False)[..., :cfg.vocab_size]
+    if capped_logits:  # GPT.forward without targets (utils/model.py:203-204, 210)
+        return SOFTCAP * torch.tanh(logits / SOFTCAP)
     tgt = targets.expand(m, length) if noise is not None else targets
     return softcap_ce(logits, tgt)
 
@@ -249,5 +254,61 @@ def population_loss(params, noise, sign, idx, targets, policy='fp32', cfg=GPTCon
 
 
 def clean_loss(params, idx, targets, policy='fp32', cfg=GPTConfig()):
-    """Per-token cross-entropy [B, T] of the unperturbed model (utils/model.py:193-210)."""
+    """Per-token cross-entropy [B, T] of the unperturbed model (utils/model.py:193-210).
+    policy 'score16' is the reference's GPU scoring arithmetic (`scoring_loss_bf16`)."""
+    if policy == 'score16':
+        return scoring_loss_bf16(params, idx, targets, cfg)
     return forward(params, idx, targets, None, None, policy, cfg)
+
+
+def clean_logits(params, idx, policy='fp32', cfg=GPTConfig()):
+    """Soft-capped logits [B, T, vocab] of the unperturbed model (GPT.forward without targets,
+    utils/model.py:193-210)."""
+    return forward(params, idx, None, None, None, policy, cfg, capped_logits=True)
+
+
+def scoring_loss_bf16(params, idx, targets, cfg=GPTConfig()):
+    """Per-token cross-entropy [B, T] in the arithmetic the reference scores with on a GPU
+    (utils/eval.py:24-45): the token and value embedding tables stored in bfloat16
+    (utils/model.py:171-175), the forward under bf16 autocast. There every nn.Linear takes bf16
+    operands, accumulates in fp32 and returns bf16 (autocast's lower-precision list), and every
+    other op -- rms_norm (on neither autocast list), the lambda mix, the residual adds, rotary,
+    the gate, relu^2 -- runs in its bf16 input dtype, i.e. computes in fp32 and rounds its output
+    to bf16. The 0-dim fp32 lambdas join a bf16 product as bf16 operands. Attention returns bf16
+    (exact softmax here). The logits leave lm_head in bf16 and are widened before the fp32
+    soft-cap and cross-entropy (utils/model.py:203-209). Each op below is one rounding r()."""
+    r = lambda t: t.to(torch.bfloat16).float()
+    p = {k: v.float() for k, v in params.items()}
+    heads, dim = cfg.n_head, cfg.head_dim
+    B, T = idx.shape
+    cos, sin = rotary_tables(T, cfg)
+
+    def lin(x, name):
+        return r(x @ r(p[name]).t())
+
+    def rot(x):
+        d = x.shape[-1] // 2
+        x1, x2 = x[..., :d], x[..., d:]
+        c, s = cos[:, None, :], sin[:, None, :]
+        return torch.cat([r(r(x1 * c) + r(x2 * s)), r(r(x1 * -s) + r(x2 * c))], -1)
+
+    x = x0 = r(rms_norm(r(p['transformer.wte.weight'])[idx]))
+    for i in range(cfg.n_layer):
+        pre = f'transformer.h.{i}.'
+        lr, l0 = r(p['resid_lambdas'][i]), r(p['x0_lambdas'][i])
+        x = r(r(lr * x) + r(l0 * x0))
+        h = r(rms_norm(x))
+        q = lin(h, pre + 'attn.c_q.weight').view(B, T, heads, dim)
+        k = lin(h, pre + 'attn.c_k.weight').view(B, T, heads, dim)
+        v = lin(h, pre + 'attn.c_v.weight').view(B, T, heads, dim)
+        if has_ve(i, cfg.n_layer):
+            ve = r(p[f'value_embeds.{i}.weight'])[idx].view(B, T, heads, dim)
+            gate = r(2 * r(torch.sigmoid(lin(h[..., :VE_GATE_CHANNELS], pre + 'attn.ve_gate.weight'))))
+            v = r(v + r(gate.unsqueeze(-1) * ve))
+        q, k = r(rms_norm(rot(q))), r(rms_norm(rot(k)))
+        y = r(window_attention(q, k, v, window_sizes(cfg)[i])).reshape(B, T, -1)
+        x = r(x + lin(y, pre + 'attn.c_proj.weight'))
+        hid = r(torch.relu(lin(r(rms_norm(x)), pre + 'mlp.c_fc.weight')).square())
+        x = r(x + lin(hid, pre + 'mlp.c_proj.weight'))
+    logits = lin(r(rms_norm(x)), 'lm_head.weight')[..., :cfg.vocab_size]
+    return softcap_ce(logits, targets)

@@ -29,6 +29,14 @@ def golden_autocast():
 
 
 @pytest.fixture(scope='session')
+def golden_scoring():
+    """The reference's GPT.forward per-token losses in its GPU scoring arithmetic
+    (tests/golden/make_golden.py --scoring)."""
+    with np.load(GOLDEN / 'golden_scoring.npz', allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope='session')
 def golden_json():
     import json
     return json.loads((GOLDEN / 'golden.json').read_text())

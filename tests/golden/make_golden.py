@@ -147,9 +147,38 @@ def autocast_losses(ref_root):
     print(json.dumps({k: [float(x) for x in v] for k, v in arrays.items()}, indent=1))
 
 
+def scoring_losses(ref_root):
+    """golden_scoring.npz: the reference's GPT.forward per-token losses on the config-0 and
+    sensitive sequences with its GPU storage and arithmetic restated on the CPU -- token and
+    value embeddings held in bfloat16 (utils/model.py:171-175 casts them when the model lives on
+    a GPU) and the forward under bf16 autocast, as utils/eval.py:43-45 scores. This pins the
+    oracle's 'score16' policy, the reference's scoring arithmetic."""
+    sys.path.insert(0, str(ref_root))
+    from train.val.eggroll import make_model
+
+    torch.set_grad_enabled(False)
+    arrays = {}
+    for tag, cfg in (('config0', CONFIG0), ('sensitive', SENSITIVE)):
+        model = make_model(torch.device('cpu'), 0)
+        if tag == 'sensitive':
+            p = sensitive_weights(dict(model.named_parameters()), SENSITIVE['weight_seed'])
+            model.load_state_dict(p, strict=True)
+        model.transformer.wte.to(dtype=torch.bfloat16)
+        for ve in model.value_embeds.values():
+            ve.to(dtype=torch.bfloat16)
+        idx, targets = sequence(cfg['length'], seed=cfg['token_seed'])
+        with torch.autocast('cpu', dtype=torch.bfloat16):
+            ce = model(idx[None], targets[None], loss_reduction='none')
+        arrays[tag + '/scoring_ce'] = ce.float().numpy()
+    np.savez_compressed(HERE / 'golden_scoring.npz', **arrays)
+    print(json.dumps({k: [float(v.mean()), float(v.min()), float(v.max())] for k, v in arrays.items()}))
+
+
 if __name__ == '__main__':
     root = Path(sys.argv[1] if len(sys.argv) > 1 else '/root/reference')
     if '--autocast' in sys.argv:
         autocast_losses(root)
+    elif '--scoring' in sys.argv:
+        scoring_losses(root)
     else:
         main(root)

@@ -274,6 +274,52 @@ def test_head_ce(device):
     torch.testing.assert_close(losses.cpu().double(), ce.cpu().double().view(m, T).mean(1), rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize('T', [256, 300])
+def test_head_ce_ignore_index_and_logits(device, T):
+    """F.cross_entropy's ignore_index in the fused head: a target equal to it scores 0, any other
+    target outside [0, V) scores NaN (torch raises there); the optional capped-logits output
+    matches 15 tanh(z / 15) of the fp64 product, and asking for it leaves ce unchanged. T = 300
+    takes the ragged-row kernel and a partial last tile."""
+    g = _gen(17)
+    m, V = 2, 4096
+    M = T * m
+    h = _bf(R.rms_norm(torch.randn(M, 512, generator=g)))
+    W = torch.randn(V, 512, generator=g) * 0.06
+    a = torch.randn(m, V, generator=g)
+    u = torch.randn(M, generator=g)
+    sign = torch.tensor([0.01, -0.01])
+    targets = torch.randint(0, V, (m, T), generator=g)
+    targets[0, 3], targets[1, 7], targets[0, T - 1] = -1, -1, -1
+    targets[1, 11], targets[0, 20] = -100, V + 5
+    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi)
+    nk.cast_bf16(W.to(device), hi, lo)
+    dh, dt, ds, du = h.to(device), targets.to(device), sign.to(device), u.to(device)
+    nz = NoiseRows(a=a.to(device), shift=0)
+    p = torch.arange(M) // T
+    z = h.double() @ W.double().t() + (sign[p] * u).double()[:, None] * a[p].double()
+    tf = targets.reshape(-1)
+    valid = (tf >= 0) & (tf < V)
+    ref = torch.zeros(M, dtype=torch.float64)
+    ref[valid] = R.softcap_ce(z[valid], tf[valid])
+    for ignore in (-1, -100):
+        ce = torch.empty(M, device=device)
+        nk.head_ce(dh, hi, lo, T, dt, ce, ds, nz, du, targets_stride=T, ignore_index=ignore)
+        c = ce.cpu().double()
+        torch.testing.assert_close(c[valid], ref[valid], rtol=0, atol=2e-5)
+        assert torch.all(c[tf == ignore] == 0)
+        assert torch.all(torch.isnan(c[~valid & (tf != ignore)]))
+        logits = torch.full((M, V + 64), 7.0, device=device)
+        ce2 = torch.empty(M, device=device)
+        nk.head_ce(dh, hi, lo, T, dt, ce2, ds, nz, du, targets_stride=T, ignore_index=ignore, logits=logits)
+        assert torch.equal(ce2.cpu()[valid], ce.cpu()[valid])
+        lg = logits.cpu().double()
+        torch.testing.assert_close(lg[:, :V], 15 * torch.tanh(z / 15), rtol=0, atol=2e-5)
+        assert torch.all(lg[:, V:] == 7.0)  # the row padding past V is never written
+    with pytest.raises(Exception, match='ignore_index'):
+        nk.head_ce(dh, hi, lo, T, dt, ce, ds, nz, du, targets_stride=T, ignore_index=5)
+
+
 def test_cast_bf16_round_to_nearest_even(device):
     g = _gen(8)
     x = torch.randn(100003, generator=g) * 10

@@ -134,7 +134,7 @@ def test_eval_rows_and_hash(tmp_path):
     """load_rows (utils/prepare_data.py:39-47): shape check, sha256 of the int32 bytes against the
     pinned digest for a file named in the table, int64 out."""
     from noise_amd import evaluate as E
-    x = torch.arange(3 * E.SEQ, dtype=torch.int64).view(3, E.SEQ) % 4096
+    x = torch.arange(3 * E.ROW_TOKENS, dtype=torch.int64).view(3, E.ROW_TOKENS) % 4096
     assert E.token_hash(x) == __import__('hashlib').sha256(x.to(torch.int32).numpy().tobytes()).hexdigest()
     torch.save(x.to(torch.int32), tmp_path / 'rows.pt')
     got = E.load_rows(tmp_path / 'rows.pt', 3)
@@ -142,6 +142,20 @@ def test_eval_rows_and_hash(tmp_path):
     with pytest.raises(ValueError, match='token tensor'):
         E.load_rows(tmp_path / 'rows.pt', 4)
     torch.save(x, tmp_path / 'val.pt')  # the pinned name, wrong tokens
-    with pytest.raises(ValueError, match='hash mismatch'):
+    with pytest.raises(ValueError, match='sha256 mismatch'):
         E.load_rows(tmp_path / 'val.pt', 3)
     assert torch.equal(E.load_rows(tmp_path / 'val.pt', 3, expected=None), x)
+    # contiguous per-rank shards cover every row exactly once, sizes within one
+    split = E.TokenSplit(tmp_path / 'val.pt', torch.arange(544 * 2).view(544, 2))
+    for world in (1, 3, 8, 7):
+        parts = [split.shard(r, world) for r in range(world)]
+        assert torch.equal(torch.cat(parts), split.tokens)
+        assert max(len(q) for q in parts) - min(len(q) for q in parts) <= 1
+
+
+def test_eval_cli_rejects_wrong_split(tmp_path):
+    """The CLI refuses a split whose sha256 differs from the pinned val.pt, before any GPU work."""
+    from noise_amd import evaluate as E
+    torch.save(torch.zeros(E.VAL_ROWS, E.ROW_TOKENS, dtype=torch.int32), tmp_path / 'val.pt')
+    with pytest.raises(ValueError, match='sha256 mismatch'):
+        E.TokenSplit.open(tmp_path / 'val.pt', E.VAL_ROWS)

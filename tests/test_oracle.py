@@ -152,6 +152,29 @@ def test_build_policy_within_reference_autocast_envelope(init_params, golden, go
         assert torch.equal(torch.sign(d(build)), torch.sign(d(ref16))), tag
 
 
+def test_scoring_policy_matches_reference_scoring(init_params, golden, golden_json, golden_scoring):
+    """The oracle's 'score16' policy (the reference's GPU scoring arithmetic: bf16 embedding
+    tables, a bf16 residual stream under autocast, utils/eval.py:43-45) against the reference's
+    GPT.forward run that way (golden_scoring.npz). Two bf16-stream forwards that sum in different
+    orders scatter per token (sd ~0.01 on the sensitive weights), so the bars are on the
+    per-token maximum and on the sequence mean; a dropped term does not fit them (checked below
+    with the x0 mix removed)."""
+    sc = golden_scoring
+    bars = {'config0': (2e-3, 1e-4), 'sensitive': (0.08, 3e-3)}
+    for tag, (tok_bar, mean_bar) in bars.items():
+        c = golden_json[tag]
+        p = init_params if tag == 'config0' else sensitive_params(init_params, c['weight_seed'])
+        idx, targets = t(golden[f'{tag}/idx']), t(golden[f'{tag}/targets'])
+        ref = torch.from_numpy(sc[f'{tag}/scoring_ce']).view(-1).double()
+        got = R.clean_loss(p, idx[None], targets[None], policy='score16')[0].double()
+        assert float((got - ref).abs().max()) <= tok_bar, tag
+        assert abs(float(got.mean() - ref.mean())) <= mean_bar, tag
+        if tag == 'sensitive':
+            broken = dict(p, x0_lambdas=torch.zeros_like(p['x0_lambdas']))
+            bad = R.clean_loss(broken, idx[None], targets[None], policy='score16')[0].double()
+            assert float((bad - ref).abs().max()) > tok_bar or abs(float(bad.mean() - ref.mean())) > mean_bar
+
+
 def test_clean_forward_matches_reference(init_params, golden):
     idx, targets = t(golden['config0/idx']), t(golden['config0/targets'])
     clean = R.clean_loss(init_params, idx[None], targets[None], policy='fp32')[0]
