@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
     python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the fused MLP
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
+    python bench.py --probe-step     # for rocprofv3 --pmc: a copy of known size, then one step at 512 members
     python bench.py --probe-cycle    # the readout probe kernels (cycle_derivatives), own JSON line
     python bench.py --probe-chain    # chain_chunk (attention held) at the Cut estimator's shape, own JSON line
     python bench.py --probe-chain --own routed   # the same with the routed own-query moves
@@ -11,7 +12,7 @@
 Workload (config 4 of the baseline): one GPU's share of the population -- 3072 members (1536
 antithetic pairs) of the 37.7M-parameter model, rank-1 perturbations on every matrix and
 embedding and eps on the mixing scalars, sigma = 1e-3, one 2048-token Zipf(1.1) sequence -- then
-the fitness, the rank-1 gradient rebuild and an AdamW update of all weights. A step is one
+the rank-normalised fitness, the rank-1 gradient rebuild and an AdamW update of all weights. A step is one
 `Eggroll.step`. Weights are the seeded initialisation; tokens are synthetic.
 
 Printed: one JSON line. `value` = members * tokens * steps / wall time of the timed steps (inputs
@@ -105,6 +106,28 @@ def probe_mlp(reps=3):
                     a['sign'], a['fc'], a['pr'])
     torch.cuda.synchronize()
     print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused over {a["x"].shape[0]} rows', flush=True)
+
+
+def probe_step(members=512, T=2048):
+    """Counter-collection workload for every kernel of the step: one copy of a 1 GiB fp32 buffer
+    (the scale reference for FETCH_SIZE / WRITE_SIZE), then one `Eggroll.step` with `members`
+    members (one batched forward of 512 members: every forward kernel once per layer), the rank
+    fitness, the gradient rebuild and AdamW -- the bench's step at one chunk."""
+    import noise_amd
+    from noise_amd.synthetic import sequence
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    src = torch.randn(1 << 28, device=dev, generator=g)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    del src, dst
+    model = noise_amd.make_model(dev, 0)
+    opt = noise_amd.AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    es = noise_amd.Eggroll(model, members // 2, sigma=1e-3, chunk=256, fitness='ranks')
+    idx, targets = sequence(T, seed=0)
+    loss = es.step(idx[None].to(dev), targets[None].to(dev), opt, 1)
+    torch.cuda.synchronize()
+    print(f'probe-step: copy 1 GiB, one step of {members} members x {T} tokens, mean loss {loss:.6f}', flush=True)
 
 
 def probe_attention(members=512, T=2048, reps=2):
@@ -370,6 +393,7 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--probe-mlp', action='store_true', help='run the MLP counter-collection workload only')
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
+    ap.add_argument('--probe-step', action='store_true', help='run the whole-step counter-collection workload only')
     ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
     ap.add_argument('--probe-chain', action='store_true', help='bench chain_chunk (own JSON line)')
     ap.add_argument('--own', choices=['none', 'routed', 'window'], default='none',
@@ -385,6 +409,9 @@ def main():
         return
     if args.probe_attention:
         probe_attention()
+        return
+    if args.probe_step:
+        probe_step()
         return
     if args.probe_cycle:
         bench_probe_cycle(max(args.steps, 5), args.warmup, args.no_cpu)
@@ -402,7 +429,7 @@ def main():
     T = args.tokens
     model = noise_amd.make_model(device, 0)
     opt = noise_amd.AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
-    es = noise_amd.Eggroll(model, pairs, sigma=1e-3, chunk=args.chunk)
+    es = noise_amd.Eggroll(model, pairs, sigma=1e-3, chunk=args.chunk, fitness='ranks')
     idx, targets = sequence(T, seed=0)
     x, y = idx[None].to(device), targets[None].to(device)
 
@@ -437,7 +464,8 @@ def main():
         'vs_baseline': None,
         'dtype': 'bf16',
         'data': 'synthetic (Zipf(1.1) tokens, seed-0 weights, N(0,1) noise buffer)',
-        'config': {'workload': 'config 4: full EGGROLL population step (forward + fitness + rank-1 gradient + AdamW)',
+        'config': {'workload': 'config 4: full EGGROLL population step (forward + rank-normalised fitness + '
+                               'rank-1 gradient + AdamW)',
                    'members': members, 'pairs': pairs, 'seq_len': T, 'sigma': 1e-3, 'model': '37.7M (8x512, V=4096)',
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
