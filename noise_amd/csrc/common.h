@@ -83,6 +83,9 @@ NOISE_DEV void halfwave_transpose_sum(float (&v)[64], int lane) {
 namespace noise {
 int set_error(int status, const char* fmt, ...);
 int check_launch(const char* what);
+// The row-resident q|k|v projection (proj.hip): launched and true when the shapes allow it.
+bool proj_qkv_launch(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M, int K,
+                     const noise_rank1_t& r1, const noise_rope_t& rope, hipStream_t stream);
 }  // namespace noise
 
 #define NOISE_REQUIRE(cond, ...)                                      \

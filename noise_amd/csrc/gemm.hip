@@ -398,6 +398,8 @@ extern "C" int noise_qkv_rope_gemm(const uint16_t* A, int64_t lda, const uint16_
   if (rc) return rc;
   g.rope = rp;
   if (M == 0) return NOISE_OK;
+  if (noise::proj_qkv_launch(A, lda, W, ldw, M, K, g.r1, rp, (hipStream_t)stream))
+    return noise::check_launch("qkv_rope_gemm (row-resident)");
   const dim3 grid((unsigned)((int64_t)((M + BM - 1) / BM) * (1536 / 256)));
   lowrank_gemm_kernel<EPI_QKV_ROPE, 256, false><<<grid, 512, 0, (hipStream_t)stream>>>(g);
   return noise::check_launch("qkv_rope_gemm");

@@ -1,0 +1,95 @@
+"""Static checks of the gfx950 assembly of this library's own kernels (test infrastructure).
+
+Several kernels issue MFMAs and vector loads as inline asm, which the compiler schedules around
+without seeing inside. Two properties then rest on the code the compiler happens to emit, and
+are checked here on the assembly it does emit:
+
+* `mfma_hazards`: no MFMA reads a register (A, B or C operand) that a VALU instruction wrote
+  fewer than 2 wait states earlier (the compiler inserts these nops for its own MFMAs only);
+* `async_load_touches`: no instruction reads or writes the destination registers of a vector
+  load before an `s_waitcnt vmcnt(N)` that covers the load (an inline-asm load's destination is
+  written when the data lands, not when the asm statement ends; a register the compiler reuses
+  or copies in between is overwritten or read early).
+"""
+import re
+import subprocess
+
+from noise_amd import build as B
+
+
+def device_asm(src, tmp_path, defines=()):
+    out = tmp_path / (src.stem + '.s')
+    cmd = [B.hipcc(), *B.FLAGS, *defines, '--cuda-device-only', '-S', '-x', 'hip', str(src), '-o', str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f'hipcc -S failed for {src.name}:\n{res.stderr}')
+    return out.read_text()
+
+
+def _regs(tok):
+    tok = tok.strip()
+    m = re.match(r'([va])\[(\d+):(\d+)\]$', tok)
+    if m:
+        return {f'{m.group(1)}{i}' for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r'([va])(\d+)$', tok)
+    return {tok} if m else set()
+
+
+def _operands(line):
+    parts = line.split(None, 1)
+    return [o.strip() for o in re.split(r',(?![^\[]*\])', parts[1])] if len(parts) > 1 else []
+
+
+def _instructions(asm):
+    out = []
+    for line in asm.splitlines():
+        line = line.split(';')[0].strip()
+        if line and not line.startswith('.') and not re.match(r'^\S+:$', line):
+            out.append(line)
+    return out
+
+
+def mfma_hazards(asm, need=2):
+    ins = _instructions(asm)
+    bad = []
+    for i, line in enumerate(ins):
+        if not line.startswith('v_mfma'):
+            continue
+        srcs = set().union(*(_regs(o) for o in _operands(line)[1:4]))
+        waits = 0
+        for j in range(i - 1, max(i - 2 * need - 4, -1), -1):
+            prev = ins[j]
+            if prev.startswith('v_') and not prev.startswith('v_mfma'):
+                ops = _operands(prev)
+                if ops and _regs(ops[0]) & srcs and waits < need:
+                    bad.append((prev, line))
+                    break
+            waits += int(prev.split()[1]) + 1 if prev.startswith('s_nop') else 1
+            if waits >= need:
+                break
+    return bad
+
+
+def async_load_touches(asm):
+    ins = _instructions(asm)
+    bad = []
+    for i, line in enumerate(ins):
+        if not re.match(r'global_load_(dword|dwordx2|dwordx3|dwordx4)\b', line):
+            continue
+        dst = _regs(_operands(line)[0])
+        if not dst:
+            continue
+        later = 0  # vector memory operations issued after this load
+        for nxt in ins[i + 1:]:
+            m = re.match(r's_waitcnt\s.*vmcnt\((\d+)\)', nxt)
+            if m and int(m.group(1)) <= later:
+                break
+            if nxt.startswith(('s_endpgm', 's_branch', 's_setpc')):
+                break  # conditional branches are scanned through (their fall-through code)
+            ops = _operands(nxt)
+            if ops and set().union(*(_regs(o) for o in ops)) & dst:
+                bad.append((line, nxt))
+                break
+            if re.match(r'(global_|buffer_|flat_|scratch_)(load|store|atomic)', nxt):
+                later += 1
+    return bad

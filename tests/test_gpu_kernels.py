@@ -39,6 +39,8 @@ GEMM_CASES = [
     (256, 512, 2048, 128, 1, 16, 1),
     (300, 128, 128, 64, 1, 1, 0),        # one column tile, row tail
     (300, 384, 128, 64, 3, 2, 1),        # 128-column segments
+    (512, 512, 512, 256, 1, 8, 1),       # K = 512, 128-row aligned members (the step's attention c_proj shape)
+    (1024, 1536, 512, 128, 1, 2, 0),     # N = 1536 with one rank-1 segment
 ]
 
 
