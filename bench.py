@@ -358,28 +358,53 @@ def cpu_baseline_probe(n, P, V, tokens=768):
             'sample': f'oracle cycle_derivatives in numpy float32 on CPU, {tokens} tokens x {P} directions x V={V}'}
 
 
+def _cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def _median_time(fn, seconds_budget, max_reps=5):
+    t0 = time.perf_counter()
+    fn()  # warmup
+    first = time.perf_counter() - t0
+    reps = max(1, min(max_reps, int(seconds_budget / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], reps
+
+
 def cpu_baseline(seconds_budget=20.0):
+    """The CPU oracle's fp32 population_loss on the host cores: the bench's own workload at
+    T = 2048 (one antithetic pair, a bounded sample of the 3072 members) and config 0 of the
+    baseline (8 members, T = 256, Zipf(1.1) tokens, seed-0 weights, sigma 1e-3)."""
     from noise_amd.synthetic import antithetic, pair_noise, sequence
     from oracle import model_ref as R
-    threads = os.cpu_count() or 1
+    threads = int(os.environ.get('OMP_NUM_THREADS') or 0) or (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     params = R.init_params(0)
     idx, targets = sequence(2048, seed=0)
     noise, sign = antithetic(pair_noise(1, seed=1), 1e-3)
-    t0 = time.perf_counter()
-    R.population_loss(params, noise, sign, idx, targets, policy='fp32')  # warmup
-    first = time.perf_counter() - t0
-    reps = max(1, min(5, int(seconds_budget / max(first, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        R.population_loss(params, noise, sign, idx, targets, policy='fp32')
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, reps = _median_time(lambda: R.population_loss(params, noise, sign, idx, targets, policy='fp32'),
+                             seconds_budget)
+    idx0, tg0 = sequence(256, seed=0)
+    noise0, sign0 = antithetic(pair_noise(4, seed=1), 1e-3)
+    med0, reps0 = _median_time(lambda: R.population_loss(params, noise0, sign0, idx0, tg0, policy='fp32'),
+                               seconds_budget / 4)
     return {'value': 2 * 2048 / med, 'unit': 'member-tokens/s', 'cores': threads, 'kind': 'port',
             'sample': f'oracle population_loss fp32 on CPU, 2 members (1 antithetic pair) x 2048 tokens, '
-                      f'median of {reps} after 1 warmup'}
+                      f'median of {reps} after 1 warmup',
+            'cpu_model': _cpu_model(),
+            'config0': {'value': 8 * 256 / med0, 'unit': 'member-tokens/s',
+                        'sample': f'config 0: 8 members (4 pairs) x 256 tokens, median of {reps0} after 1 warmup'}}
 
 
 def main():
