@@ -124,9 +124,10 @@ def test_embed_norm(device):
     assert torch.isnan(rows[:, 5]).all() and not torch.isnan(rows[:, 4]).any()
 
 
-def test_mix_norm(device):
+@pytest.mark.parametrize('T', [64, 66])  # 4 rows per wave / one row per wave (T % 4 != 0)
+def test_mix_norm(device, T):
     g = _gen(5)
-    T, m = 64, 4
+    m = 4
     M = T * m
     x, x0 = torch.randn(M, 512, generator=g), torch.randn(M, 512, generator=g)
     lam = torch.tensor([1.1, 0.2])
