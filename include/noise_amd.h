@@ -86,6 +86,11 @@ typedef struct {
   int64_t ld_a_proj;
   const float* b_proj;       /* [noise rows, 2048] (c_proj in) */
   int64_t ld_b_proj;
+  /* Optional (NULL = none): the next layer's residual mixing + norm + dots, run on the finished
+   * rows in the epilogue, as noise_mix_norm would run them on `out` afterwards. Needs flags
+   * NORM | RESIDUAL, next->x == out, next->M == members * T with out contiguous
+   * (ld_out 512, member_stride_out T * 512), and next->h 16-byte aligned. */
+  const struct noise_mixnorm_s* next;
 } noise_mlp_t;
 
 /* out = [in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 in one launch, the [rows, 2048] hidden
@@ -115,7 +120,7 @@ int noise_embed_norm(const float* table, int64_t ld_table, int vocab, int d,
                      float* x0, float* x, void* stream);
 
 /* ---- residual mixing + RMSNorm + the dots of the consuming GEMMs ------------------------ */
-typedef struct {
+typedef struct noise_mixnorm_s {
   float* x;             /* [M, 512] fp32 stream (updated in place when mixing) */
   const float* x0;      /* [M, 512] fp32 normalised embedding; NULL = no mixing */
   int M, T, member_shift;
@@ -200,7 +205,8 @@ int noise_window_attention(const noise_attention_t* args, void* stream);
 typedef struct {
   const uint16_t* h;     /* [M, 512] bf16 norm(x) */
   const uint16_t* w_hi;  /* [V, 512] bf16(W) */
-  const uint16_t* w_lo;  /* [V, 512] bf16(W - bf16(W)): W ~ w_hi + w_lo to ~2^-17 */
+  const uint16_t* w_lo;  /* [V, 512] bf16(W - bf16(W)): W ~ w_hi + w_lo to ~2^-17; NULL = the
+                            bf16 head alone (the reference trainer's autocast product) */
   int M, V, T, member_shift;
   const float* sign;
   const float* a;        /* [noise rows, V] */

@@ -43,7 +43,8 @@ class Mlp(C.Structure):
     _fields_ = [('in_', P), ('ld_in', I64), ('member_stride_in', I64), ('out', P), ('ld_out', I64),
                 ('member_stride_out', I64), ('T', INT), ('members', INT), ('flags', INT), ('w_fc', P),
                 ('w_proj', P), ('sign', P), ('member_shift', INT), ('a_fc', P), ('ld_a_fc', I64), ('b_fc', P),
-                ('ld_b_fc', I64), ('a_proj', P), ('ld_a_proj', I64), ('b_proj', P), ('ld_b_proj', I64)]
+                ('ld_b_fc', I64), ('a_proj', P), ('ld_a_proj', I64), ('b_proj', P), ('ld_b_proj', I64),
+                ('next', C.POINTER(MixNorm))]
 
 
 class Attention(C.Structure):

@@ -39,6 +39,11 @@ constexpr int WMP_PART = D * FC * 2;             // 32768: [512 rows][32 k] bf16
 constexpr int STAGE = WFC_PART + WMP_PART;       // 66048
 constexpr int NOISE_OFS = 2 * STAGE;             // a_fc [2048] | b_proj [2048] | a_proj [512] | b_fc [512]
 constexpr int LDS_BYTES = NOISE_OFS + (2 * F + 2 * D) * 4;  // 152576
+// With the next layer's mix_norm in the epilogue: its dot vectors b[0..2] [3][512] | gate W [8][32]
+// | gate b [32], staged in the prologue.
+constexpr int NEXT_OFS = LDS_BYTES;
+constexpr int NEXT_FLOATS = 3 * D + 8 * 32 + 32;  // 1824
+constexpr int LDS_NEXT_BYTES = NEXT_OFS + NEXT_FLOATS * 4;  // 159872
 constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (F.rms_norm default)
 #ifndef MLP_AHEAD
 #define MLP_AHEAD 3  // MFMAs of fragment-read lookahead
@@ -50,7 +55,7 @@ constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (
 #define MLP_LSTRIDE 1  // MFMAs between two loads of the next stage
 #endif
 
-static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+static_assert(LDS_NEXT_BYTES <= 160 * 1024, "LDS budget");
 
 // Position q (0..15) of a 16-deep k-step of the packed c_proj copy holds hidden feature
 // perm16(q) of that step: lanes 0-31 supply k-slots 0-7 from accumulators j = 0..7 of the c_fc
@@ -242,10 +247,146 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
   }(std::make_integer_sequence<int, O::N>{});
 }
 
-template <bool NORM, bool RESID>
+// The next layer's mix_norm on the wave's finished rows, straight from the c_proj accumulators
+// (lane l: column 32 nb + l % 32 of rows tb + 8 (j / 4) + 4 (l / 32) + j % 4), in the arithmetic of
+// noise_mix_norm (norm.hip): x = (lr + s er) (acc + rank-1) + (l0 + s e0) x0 (MIX: x0 given),
+// written back to the stream; h = bf16(x rsqrt(mean x^2 + eps)) into the wave's 32 KB LDS tile,
+// one row at a time (the norm is a half-wave sum); then from the tile: h as whole rows, the dots
+// u_k = h . b_k (lane l: columns 8 l .. 8 l + 7 of every row, summed across the wave), and the gate
+// 2 sigmoid(h[:32] (Wg + s a b^T)^T). The accumulators are only read; b, Wg and b_g were staged
+// in LDS by the prologue.
+template <bool MIX>
+NOISE_DEV void mix_norm_epilogue(const noise_mlp_t& g, const noise_mixnorm_t& nx, const floatx16 (&acc)[16],
+                                 const float (&am)[16], float sup, unsigned char* lds, int wave, int lane, int p,
+                                 int tb) {
+  // Opaque copies of the row coordinates: the addresses below are then formed here, not hoisted
+  // above the main loop (where they would only wait in scratch memory).
+  float* const out = g.out;
+  const float* const x0p = nx.x0;
+  uint16_t* const hp = nx.h;
+  __asm__ volatile("" : "+s"(tb), "+v"(lane));
+  const int r = lane & 31, half = lane >> 5;
+  const int64_t pn = (int64_t)(p >> nx.member_shift);
+  const float s = nx.sign ? nx.sign[p] : 0.f;
+  const float* s_next = reinterpret_cast<const float*>(lds + NEXT_OFS);
+  float lr = 1.f, l0 = 0.f;
+  if constexpr (MIX) {
+    lr = *nx.resid;
+    l0 = *nx.mix;
+    if (nx.sign) {
+      lr += s * nx.eps_resid[pn * nx.ld_eps];
+      l0 += s * nx.eps_mix[pn * nx.ld_eps];
+    }
+  }
+  const int64_t mrow0 = (int64_t)p * g.T;  // the member's first row in nx's [M, 512] layout
+  // x0 rows arrive XA rows ahead of their use, in a ring of XA x 16 registers
+  constexpr int XA = 2;
+  float x0v[XA][16];
+  auto x0_load = [&](int j, float (&dst)[16]) {
+    const int rj = tb + 8 * (j >> 2) + 4 * half + (j & 3);
+    const float* src = x0p + (mrow0 + (rj < g.T ? rj : g.T - 1)) * D + r;
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) dst[nb] = src[nb * 32];
+  };
+  if constexpr (MIX) {
+#pragma unroll
+    for (int j = 0; j < XA; ++j) x0_load(j, x0v[j]);
+  }
+  // The wave's LDS tile [32 rows][1 KB] of h: the four tiles cover both stage buffers, which
+  // other waves may still be reading in their last step.
+  static_assert(4 * 32 * 1024 <= NOISE_OFS, "h tiles must fit below the noise vectors");
+  __syncthreads();
+  uint16_t* tile = reinterpret_cast<uint16_t*>(lds + wave * 32 * 1024);
+  float h0[16];  // h of column r (block 0) of each of the lane's rows: the gate's inputs
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int rl = 8 * (j >> 2) + 4 * half + (j & 3);
+    const float sr = __shfl(sup, rl, 64);
+    float v[16], ss = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) {
+      v[nb] = acc[nb][j] + sr * am[nb];
+      if constexpr (MIX) v[nb] = lr * v[nb] + l0 * x0v[j % XA][nb];
+      ss += v[nb] * v[nb];
+    }
+    if constexpr (MIX) {
+      if (j + XA < 16) x0_load(j + XA, x0v[j % XA]);
+    }
+    if (tb + rl < g.T) {
+      float* dst = out + (mrow0 + tb + rl) * D + r;
+#pragma unroll
+      for (int nb = 0; nb < 16; ++nb) dst[nb * 32] = v[nb];
+    }
+    const float rr = rsqrtf(noise::halfwave_sum(ss) * (1.0f / D) + RMS_EPS);
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) {
+      const uint16_t hb = f2bf(v[nb] * rr);
+      tile[rl * 512 + nb * 32 + r] = hb;
+      if (nb == 0) h0[j] = bf2f(hb);
+    }
+  }
+  // From the tile (a wave's LDS operations run in order; the compiler barrier keeps the 16-byte
+  // reads after the 2-byte writes): lane l holds bytes 16 l .. 16 l + 15 (columns 8 l .. 8 l + 7)
+  // of each row. Pass k = 0 also writes the rows out.
+  __asm__ volatile("" ::: "memory");
+  const int nbv = nx.nb;
+  // after the transpose sum, lane l (even) holds the total of row 16 (l / 32) + ((l % 32) >> 1)
+  const int rw = tb + 16 * half + (r >> 1);
+  const bool writer = (r & 1) == 0 && rw < g.T;
+#pragma unroll 1
+  for (int k = 0; k < (nbv > 1 ? nbv : 1); ++k) {
+    float bk[8];
+    {
+      const float4 b0 = *reinterpret_cast<const float4*>(s_next + k * D + 8 * lane);
+      const float4 b1 = *reinterpret_cast<const float4*>(s_next + k * D + 8 * lane + 4);
+      bk[0] = b0.x; bk[1] = b0.y; bk[2] = b0.z; bk[3] = b0.w;
+      bk[4] = b1.x; bk[5] = b1.y; bk[6] = b1.z; bk[7] = b1.w;
+    }
+    float part[32];
+#pragma unroll
+    for (int rl = 0; rl < 32; ++rl) {
+      const u32x4 hv = *reinterpret_cast<const u32x4*>(tile + rl * 512 + 8 * lane);
+      if (k == 0 && tb + rl < g.T) *reinterpret_cast<u32x4*>(hp + (mrow0 + tb + rl) * D + 8 * lane) = hv;
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d += bf_lo(hv[e]) * bk[2 * e] + bf_hi(hv[e]) * bk[2 * e + 1];
+      part[rl] = d;
+    }
+    if (k < nbv) {
+      const float tot = noise::wave_transpose_sum32(part, lane);
+      if (writer) nx.u[(mrow0 + rw) * nx.ldu + k] = tot;
+    }
+  }
+  if (nx.gate_w) {
+    // gate logit q of a row: its 32 columns of h . Wg[q], plus s (h[:32] . b_g) a_g[q]; rows in the
+    // accumulator layout, lane q (even) of a half ends with row 8 (jj / 4) + 4 half + jj % 4,
+    // jj = (q >> 1) & 15
+    const int jj = (r >> 1) & 15;
+    const int rg = tb + 8 * (jj >> 2) + 4 * half + (jj & 3);
+    const bool gw = (r & 1) == 0 && rg < g.T;
+    float t[16];
+    const float bg = s_next[3 * D + 256 + r];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t[j] = h0[j] * bg;
+    const float nd = noise::halfwave_transpose_sum16(t, lane);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float wq = s_next[3 * D + q * 32 + r];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t[j] = h0[j] * wq;
+      float z = noise::halfwave_transpose_sum16(t, lane);
+      if (nx.sign) z += s * nd * nx.gate_a[pn * nx.ld_gate_a + q];
+      if (gw) nx.gate[(mrow0 + rg) * 8 + q] = 2.0f / (1.0f + expf(-z));
+    }
+  }
+}
+
+// NEXT 1 | 2: the next layer's mix_norm (noise_mixnorm_t `nx`; 2: with x0 mixing) runs in the
+// epilogue on the finished rows.
+template <bool NORM, bool RESID, int NEXT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-mlp_fused_kernel(const noise_mlp_t g) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NEXT ? LDS_NEXT_BYTES : LDS_BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, half = lane >> 5;
@@ -337,6 +478,25 @@ mlp_fused_kernel(const noise_mlp_t g) {
       v = *reinterpret_cast<const float4*>(src);
     }
     *reinterpret_cast<float4*>(s_afc + e) = v;
+  }
+  if constexpr (NEXT != 0) {  // the next mix_norm's vectors (zeros where absent)
+    float* s_next = reinterpret_cast<float*>(lds + NEXT_OFS);
+    const int64_t pnx = (int64_t)(p >> nx.member_shift);
+#pragma unroll
+    for (int k = 0; k < (NEXT_FLOATS + 255) / 256; ++k) {
+      const int e = k * 256 + tid;
+      if (e < NEXT_FLOATS) {
+        float v = 0.f;
+        if (e < 3 * D) {
+          if (e / D < nx.nb) v = nx.b[e / D][pnx * nx.ldb + e % D];
+        } else if (e < 3 * D + 256) {
+          if (nx.gate_w) v = nx.gate_w[e - 3 * D];
+        } else if (nx.gate_w && nx.sign) {
+          v = nx.gate_b[pnx * nx.ld_gate_b + (e - 3 * D - 256)];
+        }
+        s_next[e] = v;
+      }
+    }
   }
 
   // Row norms: per-lane partial sums over the 16 column blocks, then across the half-wave
@@ -445,6 +605,10 @@ mlp_fused_kernel(const noise_mlp_t g) {
   float am[16];
 #pragma unroll
   for (int nb = 0; nb < 16; ++nb) am[nb] = s_amp[nb * 32 + r];
+  if constexpr (NEXT != 0) {
+    mix_norm_epilogue<NEXT == 2>(g, nx, acc, am, sup, lds, wave, lane, p, tb);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int rl = 8 * (j >> 2) + 4 * half + (j & 3);
@@ -539,11 +703,34 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
   if (blocks == 0) return NOISE_OK;
   const dim3 grid((unsigned)blocks);
   hipStream_t st = (hipStream_t)stream;
+  const noise_mixnorm_t none{};
+  if (g.next) {
+    const noise_mixnorm_t& nx = *g.next;
+    NOISE_REQUIRE(g.flags == (NOISE_MLP_NORM | NOISE_MLP_RESIDUAL),
+                  "mlp_fused: the next layer's mix_norm needs the normed residual MLP");
+    NOISE_REQUIRE(nx.x == g.out && nx.h && nx.T == g.T && (int64_t)nx.M == (int64_t)g.members * g.T &&
+                      g.ld_out == D && g.member_stride_out == (int64_t)g.T * D,
+                  "mlp_fused: the next mix_norm must cover exactly the output rows, [members * T, 512] contiguous");
+    NOISE_REQUIRE(nx.nb >= 0 && nx.nb <= 3 && (nx.nb == 0 || (nx.u && nx.ldu >= nx.nb && nx.ldb >= D)),
+                  "mlp_fused: next mix_norm dots need u, ldu >= nb and ldb >= 512");
+    for (int j = 0; j < nx.nb; ++j) NOISE_REQUIRE(nx.b[j], "mlp_fused: next mix_norm has a null b[%d]", j);
+    NOISE_REQUIRE(!nx.x0 || (nx.resid && nx.mix && (!nx.sign || (nx.eps_resid && nx.eps_mix))),
+                  "mlp_fused: next mixing needs the lambda scalars (and eps when perturbed)");
+    NOISE_REQUIRE(!nx.gate_w || (nx.gate && (!nx.sign || (nx.gate_a && nx.gate_b))),
+                  "mlp_fused: next gate needs its output and perturbation vectors");
+    NOISE_REQUIRE(((uintptr_t)nx.h % 16) == 0, "mlp_fused: next h must be 16-byte aligned");
+    NOISE_REQUIRE(nx.member_shift >= 0 && nx.member_shift < 31, "mlp_fused: next mix_norm has a bad member_shift");
+    if (nx.x0)
+      mlp_fused_kernel<true, true, 2><<<grid, 256, 0, st>>>(g, nx);
+    else
+      mlp_fused_kernel<true, true, 1><<<grid, 256, 0, st>>>(g, nx);
+    return noise::check_launch("mlp_fused (with the next mix_norm)");
+  }
   switch (g.flags) {
-    case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL: mlp_fused_kernel<true, true><<<grid, 256, 0, st>>>(g); break;
-    case NOISE_MLP_NORM: mlp_fused_kernel<true, false><<<grid, 256, 0, st>>>(g); break;
-    case NOISE_MLP_RESIDUAL: mlp_fused_kernel<false, true><<<grid, 256, 0, st>>>(g); break;
-    default: mlp_fused_kernel<false, false><<<grid, 256, 0, st>>>(g); break;
+    case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL: mlp_fused_kernel<true, true, 0><<<grid, 256, 0, st>>>(g, none); break;
+    case NOISE_MLP_NORM: mlp_fused_kernel<true, false, 0><<<grid, 256, 0, st>>>(g, none); break;
+    case NOISE_MLP_RESIDUAL: mlp_fused_kernel<false, true, 0><<<grid, 256, 0, st>>>(g, none); break;
+    default: mlp_fused_kernel<false, false, 0><<<grid, 256, 0, st>>>(g, none); break;
   }
   return noise::check_launch("mlp_fused");
 }

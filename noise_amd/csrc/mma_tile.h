@@ -228,4 +228,29 @@ NOISE_DEV float halfwave_transpose_sum16(float (&v)[16], int lane) {
   return v[0] + dpp_row<0xB1>(v[0]);  // quad_perm [1, 0, 3, 2]: the lane's neighbour q ^ 1
 }
 
+// Sum over the 64 lanes of 32 per-lane values; lane l ends with the total of value
+// 16 (l / 32) + ((l % 32) >> 1) (lanes l and l ^ 1 hold the same total). v_permlane32_swap pairs
+// value i with value i + 16 across the two halves, then each half sums its 16 values.
+NOISE_DEV float wave_transpose_sum32(float (&v)[32], int lane) {
+  float w[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // half 0 keeps value i, half 1 value i + 16
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 16]), false, false);
+    w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return halfwave_transpose_sum16(w, lane);
+}
+
+// Sum over the 32 lanes of each half-wave, in every lane of the half: 16-lane row sums by DPP
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror), then the two rows of
+// the half added through v_permlane16_swap.
+NOISE_DEV float halfwave_sum(float v) {
+  v += dpp_row<0xB1>(v);
+  v += dpp_row<0x4E>(v);
+  v += dpp_row<0x141>(v);
+  v += dpp_row<0x140>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 }  // namespace noise

@@ -34,7 +34,7 @@ NOISE = 2 ** 28
 
 class Eggroll:
     def __init__(self, model, pairs, rank=0, world=1, sigma=SIGMA, chunk=CHUNK, noise_size=NOISE, seed=SEED,
-                 fitness='zscore'):
+                 fitness='zscore', head_split=False):
         if fitness not in ('zscore', 'ranks'):
             raise ValueError(f"fitness must be 'zscore' (the reference's) or 'ranks', not {fitness!r}")
         self.fitness = fitness
@@ -48,7 +48,7 @@ class Eggroll:
             raise ValueError('model parameters do not follow the fixed GPT layout')
         self.buffer = torch.randn(noise_size, device=self.device,
                                   generator=torch.Generator(self.device).manual_seed(seed))
-        self.weights = PreparedWeights(self.params, self.cfg)
+        self.weights = PreparedWeights(self.params, self.cfg, head_split)
         self.engine = Engine(self.device, self.cfg)
         self.grad_flat = torch.zeros(sum(torch.Size(s).numel() for s in self.shapes.values()),
                                      dtype=torch.float32, device=self.device)

@@ -108,10 +108,11 @@ def mlp_pack(w_fc=None, fc_packed=None, w_proj=None, proj_packed=None):
 
 
 def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=None, fc=None, proj=None,
-              member_stride_in=None, member_stride_out=None):
+              member_stride_in=None, member_stride_out=None, next_norm=None):
     """x_out = [x_in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 with h = bf16(norm x_in) under
     MLP_NORM (else bf16(x_in)), in one launch. x_in / x_out: fp32 rows of 512; member p's rows
-    start at p * member_stride (default T rows). fc / proj: NoiseRows of c_fc and c_proj."""
+    start at p * member_stride (default T rows). fc / proj: NoiseRows of c_fc and c_proj.
+    next_norm: a mix_norm_args record over x_out, run on the finished rows in the same launch."""
     _on_gpu(x_in, x_out, w_fc_packed, w_proj_packed, sign)
     ld_in = _rows(x_in, 512, torch.float32, 'x_in')
     ld_out = _rows(x_out, 512, torch.float32, 'x_out')
@@ -142,6 +143,10 @@ def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=N
         g.b_fc, g.ld_b_fc = fc.b.data_ptr(), fc.b.stride(0)
         g.a_proj, g.ld_a_proj = proj.a.data_ptr(), proj.a.stride(0)
         g.b_proj, g.ld_b_proj = proj.b.data_ptr(), proj.b.stride(0)
+    if next_norm is not None:
+        _need(isinstance(next_norm, MixNorm) and next_norm.x == x_out.data_ptr() and next_norm.M == members * T,
+              'mlp_fused: next_norm must be a mix_norm_args record over the rows of x_out')
+        g.next = C.pointer(next_norm)
     _lib.call('noise_mlp_fused', C.byref(g), _stream())
 
 
@@ -161,6 +166,18 @@ def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0):
 
 def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,
              bs=(), u=None, gate_w=None, gate_nz=None, gate=None):
+    """x = (lr + s er) x + (l0 + s e0) x0 (when x0 is given), h = bf16(norm x), u[:, j] = h . bs[j],
+    gate = 2 sigmoid(h[:32] (Wg + s a b^T)^T) (when gate_w is given), in one launch."""
+    run_mix_norm(mix_norm_args(x, h, T, sign, x0, resid, mix, eps_r, eps_m, shift, bs, u, gate_w, gate_nz, gate))
+
+
+def run_mix_norm(g):
+    _lib.call('noise_mix_norm', C.byref(g), _stream())
+
+
+def mix_norm_args(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,
+                  bs=(), u=None, gate_w=None, gate_nz=None, gate=None):
+    """The MixNorm launch record of `mix_norm`, for run_mix_norm or mlp_fused(next_norm=...)."""
     g = MixNorm()
     g.x, g.x0, g.M, g.T, g.member_shift = x.data_ptr(), _ptr(x0), x.shape[0], T, shift
     g.sign = _ptr(sign)
@@ -179,7 +196,7 @@ def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_
         if sign is not None:
             g.gate_a, g.gate_b = gate_nz.a.data_ptr(), gate_nz.b.data_ptr()
             g.ld_gate_a, g.ld_gate_b = gate_nz.a.stride(0), gate_nz.b.stride(0)
-    _lib.call('noise_mix_norm', C.byref(g), _stream())
+    return g
 
 
 def _rope_args(g, T, cos, sin, sign, gate, ve_table, idx, ve_nz, idx_stride):
@@ -236,9 +253,9 @@ def window_attention(qkv16, y, members, T, window, b_proj=None, shift=0, u_proj=
 def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_stride=0, ignore_index=-100,
             logits=None):
     """ce [M] (0 where the target is `ignore_index`); with `logits` [M, >= V] fp32 also the capped
-    logits."""
+    logits. w_lo None: the bf16 head alone; else h (w_hi + w_lo)^T, fp32-accurate."""
     g = Head()
-    g.h, g.w_hi, g.w_lo = h.data_ptr(), w_hi.data_ptr(), w_lo.data_ptr()
+    g.h, g.w_hi, g.w_lo = h.data_ptr(), w_hi.data_ptr(), _ptr(w_lo)
     g.M, g.V, g.T = h.shape[0], w_hi.shape[0], T
     if sign is not None:
         g.sign, g.a, g.lda, g.u, g.member_shift = (sign.data_ptr(), nz.a.data_ptr(), nz.a.stride(0),

@@ -13,8 +13,10 @@ Per layer the engine runs (one launch each, all on the current stream):
   attention     y = bf16(softmax_window(q k^T / 8) v); u_o = y.b_o per head
   lowrank_gemm  x += y Wo^T + s u_o a_o^T
   mlp_fused     x += bf16(relu(h Wfc^T + s u_fc a_fc^T)^2) Wmp^T + s u_mp a_mp^T with
-                h = bf16(norm x), u_fc = h.b_fc, u_mp = hid.b_mp: the hidden stays on chip
-then mix_norm (final norm + u_head), head_ce (fp32-accurate head, soft-cap, CE) and member_mean.
+                h = bf16(norm x), u_fc = h.b_fc, u_mp = hid.b_mp: the hidden stays on chip;
+                its epilogue runs the next layer's mix_norm on the finished rows
+then the final norm + u_head (in the last MLP's epilogue), head_ce (fp32-accurate head, soft-cap,
+CE) and member_mean. Only layer 0's mix_norm is a launch of its own.
 """
 import math
 
@@ -41,9 +43,13 @@ def rotary_tables(length, device, cfg=GPTConfig()):
 
 class PreparedWeights:
     """The device-side weight set the kernels read: bf16 copies of every block matrix (q|k|v
-    concatenated), the head split into bf16 hi + lo, and the fp32 tables, gates and scalars."""
+    concatenated) and of the head, and the fp32 tables, gates and scalars.
 
-    def __init__(self, params, cfg=GPTConfig()):
+    head_split: also keep the head's bf16 remainder lo = bf16(W - bf16(W)), so that head_ce
+    forms h (hi + lo)^T, the fp32-weight product (twice the MFMA work). The default bf16 head is
+    the product the reference's trainer runs under autocast (train/val/eggroll.py:144-145)."""
+
+    def __init__(self, params, cfg=GPTConfig(), head_split=False):
         self.cfg = cfg
         self.params = params
         dev = params['transformer.wte.weight'].device
@@ -57,7 +63,7 @@ class PreparedWeights:
         self.mp_packed = [torch.empty(K.MLP_PACKED_ELEMS, **bf) for _ in range(L)]
         v = cfg.padded_vocab
         self.head_hi = torch.empty(v, d, **bf)
-        self.head_lo = torch.empty(v, d, **bf)
+        self.head_lo = torch.empty(v, d, **bf) if head_split else None
         self.refresh()
 
     def refresh(self):
@@ -117,6 +123,9 @@ class Engine:
         # False runs the MLP as mix_norm + two lowrank_gemm launches through an HBM hidden
         # (kept to compare the two on the same inputs).
         self.fused_mlp = True
+        # With the fused MLP: True runs the next layer's mix_norm (and the final norm) in the
+        # MLP's epilogue instead of as launches of their own.
+        self.fuse_next_norm = True
 
     def _mark(self):
         if self.probe is None:
@@ -159,19 +168,31 @@ class Engine:
         wins = window_sizes(cfg)
         P = W.params
 
+        hd = g('lm_head.weight')
+
+        def mixing(i):
+            """Layer i's mix_norm (i == n_layer: the final norm with the head's dot)."""
+            if i == cfg.n_layer:
+                return K.mix_norm_args(x, h, T, sign, shift=shift, bs=(hd.b,) if pert else (), u=u1)
+            pre = f'transformer.h.{i}.'
+            ve = has_ve(i, cfg.n_layer)
+            return K.mix_norm_args(
+                x, h, T, sign, x0, P['resid_lambdas'][i], P['x0_lambdas'][i],
+                g('resid_lambdas').eps[:, i] if pert else None, g('x0_lambdas').eps[:, i] if pert else None, shift,
+                bs=tuple(g(pre + f'attn.{n}.weight').b for n in ('c_q', 'c_k', 'c_v')) if pert else (), u=u3,
+                gate_w=W.gate(i) if ve else None, gate_nz=g(pre + 'attn.ve_gate.weight') if ve else None,
+                gate=gate)
+
         K.embed_norm(P['transformer.wte.weight'], idx, T, members, sign, g('transformer.wte.weight'), x0, x,
                      idx_stride)
+        carried = False  # the previous MLP ran this layer's mix_norm in its epilogue
         for i in range(cfg.n_layer):
             pre = f'transformer.h.{i}.'
             q, k, v, o = (g(pre + f'attn.{n}.weight') for n in ('c_q', 'c_k', 'c_v', 'c_proj'))
             fc, mp = g(pre + 'mlp.c_fc.weight'), g(pre + 'mlp.c_proj.weight')
             ve = has_ve(i, cfg.n_layer)
-            er = g('resid_lambdas').eps[:, i] if pert else None
-            em = g('x0_lambdas').eps[:, i] if pert else None
-            K.mix_norm(x, h, T, sign, x0, P['resid_lambdas'][i], P['x0_lambdas'][i], er, em, shift,
-                       bs=(q.b, k.b, v.b) if pert else (), u=u3,
-                       gate_w=W.gate(i) if ve else None, gate_nz=g(pre + 'attn.ve_gate.weight') if ve else None,
-                       gate=gate)
+            if not carried:
+                K.run_mix_norm(mixing(i))
             r1 = K.rank1(sign, T, [q.a, k.a, v.a], [u3[:, 0], u3[:, 1], u3[:, 2]], 1, 3, shift) if pert else None
             K.qkv_rope_gemm(h, W.qkv[i], r1, qkv16, T, cos, sin, sign, gate if ve else None,
                             W.table(f'value_embeds.{i}.weight') if ve else None, idx,
@@ -181,9 +202,10 @@ class Engine:
             r1 = K.rank1(sign, T, [o.a], [uproj], cfg.n_head, cfg.n_head, shift) if pert else None
             K.lowrank_gemm(y, W.o[i], r1, _lib.EPI_ADD_F32, x)
             ev = self._mark()
+            carried = self.fused_mlp and self.fuse_next_norm
             if self.fused_mlp:
                 K.mlp_fused(x, x, T, members, W.fc_packed[i], W.mp_packed[i], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
-                            sign, fc, mp)
+                            sign, fc, mp, next_norm=mixing(i + 1) if carried else None)
             else:
                 K.mix_norm(x, h, T, sign, shift=shift, bs=(fc.b,) if pert else (), u=u1)
                 r1 = K.rank1(sign, T, [fc.a], [u1], 1, 1, shift) if pert else None
@@ -193,8 +215,8 @@ class Engine:
                 K.lowrank_gemm(hid, W.mp[i], r1, _lib.EPI_ADD_F32, x)
             if ev is not None:
                 self.probe.append((ev, self._mark(), M))
-        hd = g('lm_head.weight')
-        K.mix_norm(x, h, T, sign, shift=shift, bs=(hd.b,) if pert else (), u=u1)
+        if not carried:
+            K.run_mix_norm(mixing(cfg.n_layer))
         out_ce = ce if ce_out is None else ce_out
         K.head_ce(h, W.head_hi, W.head_lo, T, targets, out_ce, sign, hd, u1, idx_stride, ignore_index, logits_out)
         if losses_out is not None:
@@ -232,11 +254,13 @@ def engine_for(device):
     return _ENGINES[key]
 
 
-def population_loss(model, p, noise, sign, idx, targets, chunk=DEFAULT_CHUNK):
+def population_loss(model, p, noise, sign, idx, targets, chunk=DEFAULT_CHUNK, head_split=False):
     """Mean cross-entropy [m] fp32 of m perturbed models on one sequence (train/val/eggroll.py:66).
 
     model: anything with a `config` (GPTConfig-compatible); p: parameters by name (device fp32);
     noise: name -> (a [m, out], b [m, in]) or eps [m, L]; sign [m]; idx, targets [T] int64.
+    head_split: the head as the fp32-weight product (bf16 hi + lo halves) instead of the bf16
+    product of the reference's autocast trainer (eggroll.py:144-145).
     """
     cfg = getattr(model, 'config', GPTConfig())
     cfg = GPTConfig(**{k: getattr(cfg, k) for k in GPTConfig.__dataclass_fields__})
@@ -248,7 +272,7 @@ def population_loss(model, p, noise, sign, idx, targets, chunk=DEFAULT_CHUNK):
     m, T = sign.shape[0], idx.shape[0]
     if targets.shape[0] != T:
         raise ValueError('idx and targets must have the same length')
-    W = PreparedWeights(p, cfg)
+    W = PreparedWeights(p, cfg, head_split)
     eng = engine_for(device)
     names = [n for n, _ in param_shapes(cfg)]
     idx = idx.to(device=device, dtype=torch.int64).contiguous()
@@ -262,15 +286,16 @@ def population_loss(model, p, noise, sign, idx, targets, chunk=DEFAULT_CHUNK):
     return losses
 
 
-def clean_loss(model_params, idx, targets, cfg=GPTConfig(), batch_chunk=64, ignore_index=-100, logits=None):
+def clean_loss(model_params, idx, targets, cfg=GPTConfig(), batch_chunk=64, ignore_index=-100, logits=None,
+               head_split=False):
     """Per-token cross-entropy [B, T] of the unperturbed model on B sequences (utils/model.py:193-210):
     0 where the target is `ignore_index`; `logits` [B, T, V] fp32, when given, receives the capped
-    logits."""
+    logits. head_split: the fp32-weight head product instead of the bf16 one."""
     device = model_params['transformer.wte.weight'].device
     if device.type != 'cuda':
         raise ValueError('clean_loss runs on the GPU; move the parameters to a HIP device')
     B, T = idx.shape
-    W = PreparedWeights(model_params, cfg)
+    W = PreparedWeights(model_params, cfg, head_split)
     eng = engine_for(device)
     idx = idx.to(device=device, dtype=torch.int64).contiguous()
     targets = targets.to(device=device, dtype=torch.int64).contiguous()

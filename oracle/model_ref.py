@@ -24,8 +24,10 @@ Precision policies:
   'build' -- float64 arithmetic with bfloat16 rounding exactly where the HIP path rounds:
              GEMM inputs (normalised activations, attention inputs and output, relu^2 hidden)
              and the bf16 weight copies of every block matrix, plus the attention probabilities
-             (bf16 under a constant softmax shift, `window_attention_shifted`); the head
-             weight stays fp32, the residual stream, norms, rank-1 terms, soft-cap and
+             (bf16 under a constant softmax shift, `window_attention_shifted`), and the head
+             weight (the bf16 product the reference's trainer runs under autocast,
+             eggroll.py:144-145; `head_split=True` keeps it full precision, as the HIP path's
+             hi + lo split does); the residual stream, norms, rank-1 terms, soft-cap and
              log-sum-exp stay full precision;
   'build32' -- the same cast points in float32 arithmetic. |build - build32| measures how far the
              bf16 cast points alone let two correct implementations drift on given inputs;
@@ -167,7 +169,8 @@ def softcap_ce(logits, targets):
     return torch.logsumexp(z, -1) - z.gather(-1, targets.unsqueeze(-1)).squeeze(-1)
 
 
-def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTConfig(), capped_logits=False):
+def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTConfig(), capped_logits=False,
+            head_split=False):
     """Per-token cross-entropy [m, T] of m perturbed models (or, with noise=None, of the clean
     model on the rows of idx [B, T]).
 
@@ -241,30 +244,30 @@ def forward(params, idx, targets, noise=None, sign=None, policy='fp32', cfg=GPTC
         hid = rb(F.relu(linear(pre + 'mlp.c_fc.weight', h2)).square())
         x = x + linear(pre + 'mlp.c_proj.weight', hid)
     hf = rb(rms_norm(x))
-    logits = linear('lm_head.weight', hf, round_weight=False)[..., :cfg.vocab_size]
+    logits = linear('lm_head.weight', hf, round_weight=not head_split)[..., :cfg.vocab_size]
     if capped_logits:  # GPT.forward without targets (utils/model.py:203-204, 210)
         return SOFTCAP * torch.tanh(logits / SOFTCAP)
     tgt = targets.expand(m, length) if noise is not None else targets
     return softcap_ce(logits, tgt)
 
 
-def population_loss(params, noise, sign, idx, targets, policy='fp32', cfg=GPTConfig()):
+def population_loss(params, noise, sign, idx, targets, policy='fp32', cfg=GPTConfig(), head_split=False):
     """Mean cross-entropy [m] of the m perturbed members (train/val/eggroll.py:66-103)."""
-    return forward(params, idx, targets, noise, sign, policy, cfg).mean(-1)
+    return forward(params, idx, targets, noise, sign, policy, cfg, head_split=head_split).mean(-1)
 
 
-def clean_loss(params, idx, targets, policy='fp32', cfg=GPTConfig()):
+def clean_loss(params, idx, targets, policy='fp32', cfg=GPTConfig(), head_split=False):
     """Per-token cross-entropy [B, T] of the unperturbed model (utils/model.py:193-210).
     policy 'score16' is the reference's GPU scoring arithmetic (`scoring_loss_bf16`)."""
     if policy == 'score16':
         return scoring_loss_bf16(params, idx, targets, cfg)
-    return forward(params, idx, targets, None, None, policy, cfg)
+    return forward(params, idx, targets, None, None, policy, cfg, head_split=head_split)
 
 
-def clean_logits(params, idx, policy='fp32', cfg=GPTConfig()):
+def clean_logits(params, idx, policy='fp32', cfg=GPTConfig(), head_split=False):
     """Soft-capped logits [B, T, vocab] of the unperturbed model (GPT.forward without targets,
     utils/model.py:193-210)."""
-    return forward(params, idx, None, None, None, policy, cfg, capped_logits=True)
+    return forward(params, idx, None, None, None, policy, cfg, capped_logits=True, head_split=head_split)
 
 
 def scoring_loss_bf16(params, idx, targets, cfg=GPTConfig()):

@@ -252,7 +252,16 @@ def test_window_attention(device, T, window, members, unit):
     torch.testing.assert_close(mom.cpu().double(), want, rtol=1e-5, atol=1e-5)
 
 
-def test_head_ce(device):
+def _head_weights(W, device, split):
+    """bf16 hi (+ lo when split) copies of W, and the fp64 weight the kernel's product equals."""
+    hi = torch.empty(W.shape[0], 512, dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi) if split else None
+    nk.cast_bf16(W.to(device), hi, lo)
+    return hi, lo, (W.double() if split else W.to(torch.bfloat16).double())
+
+
+@pytest.mark.parametrize('split', [False, True])  # the bf16 head / the fp32-weight hi + lo head
+def test_head_ce(device, split):
     g = _gen(7)
     T, m, V = 64, 4, 4096
     M = T * m
@@ -262,14 +271,12 @@ def test_head_ce(device):
     u = torch.randn(M, generator=g)
     sign = torch.tensor([0.01, -0.01, 0.002, -0.002])
     targets = torch.randint(0, V, (T,), generator=g)
-    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
-    lo = torch.empty_like(hi)
-    nk.cast_bf16(W.to(device), hi, lo)
+    hi, lo, Wd = _head_weights(W, device, split)
     ce = torch.empty(M, device=device)
     nk.head_ce(h.to(device), hi, lo, T, targets.to(device), ce, sign.to(device),
               NoiseRows(a=a.to(device), shift=0), u.to(device))
     p = torch.arange(M) // T
-    z = h.double() @ W.double().t() + (sign[p] * u).double()[:, None] * a[p].double()
+    z = h.double() @ Wd.t() + (sign[p] * u).double()[:, None] * a[p].double()
     ref = R.softcap_ce(z, targets.repeat(m))
     torch.testing.assert_close(ce.cpu().double(), ref, rtol=0, atol=2e-5)
     losses = torch.empty(m, device=device)
@@ -277,8 +284,8 @@ def test_head_ce(device):
     torch.testing.assert_close(losses.cpu().double(), ce.cpu().double().view(m, T).mean(1), rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize('T', [256, 300])
-def test_head_ce_ignore_index_and_logits(device, T):
+@pytest.mark.parametrize('T,split', [(256, False), (300, False), (256, True)])
+def test_head_ce_ignore_index_and_logits(device, T, split):
     """F.cross_entropy's ignore_index in the fused head: a target equal to it scores 0, any other
     target outside [0, V) scores NaN (torch raises there); the optional capped-logits output
     matches 15 tanh(z / 15) of the fp64 product, and asking for it leaves ce unchanged. T = 300
@@ -294,13 +301,11 @@ def test_head_ce_ignore_index_and_logits(device, T):
     targets = torch.randint(0, V, (m, T), generator=g)
     targets[0, 3], targets[1, 7], targets[0, T - 1] = -1, -1, -1
     targets[1, 11], targets[0, 20] = -100, V + 5
-    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
-    lo = torch.empty_like(hi)
-    nk.cast_bf16(W.to(device), hi, lo)
+    hi, lo, Wd = _head_weights(W, device, split)
     dh, dt, ds, du = h.to(device), targets.to(device), sign.to(device), u.to(device)
     nz = NoiseRows(a=a.to(device), shift=0)
     p = torch.arange(M) // T
-    z = h.double() @ W.double().t() + (sign[p] * u).double()[:, None] * a[p].double()
+    z = h.double() @ Wd.t() + (sign[p] * u).double()[:, None] * a[p].double()
     tf = targets.reshape(-1)
     valid = (tf >= 0) & (tf < V)
     ref = torch.zeros(M, dtype=torch.float64)
@@ -535,11 +540,12 @@ def test_config2_attention_full_size(device, window):
         torch.testing.assert_close(mom[p, h].double().cpu(), want, rtol=1e-5, atol=1e-6)
 
 
-def test_config3_head_full_size(device):
+@pytest.mark.parametrize('split', [False, True])
+def test_config3_head_full_size(device, split):
     """Config 3 at its full shape: h [512 members x 2048 tokens, 512] bf16 N(0, 1) normalised,
     W [4096, 512] fp32 ~ N(0, 1/512) with a rank-1 perturbation (sigma = 1e-3, a, b ~ N(0, 1)),
-    Zipf targets. 256 sampled rows against float64, and the per-member means against the kernel's
-    own per-token losses."""
+    Zipf targets. 256 sampled rows against float64 (split: of W itself; else of bf16(W), the
+    product of the bf16 head), and the per-member means against the kernel's own per-token losses."""
     from noise_amd.synthetic import zipf_tokens
     members, T, V = 512, 2048, 4096
     M = members * T
@@ -553,12 +559,13 @@ def test_config3_head_full_size(device):
     sign = torch.tensor([1e-3, -1e-3]).repeat(members // 2)
     targets = zipf_tokens(T, seed=5)
     db = b.to(device)
+    Wd = W.double() if split else W.to(torch.bfloat16).double()
     u = torch.empty(M, device=device)
     for p0 in range(0, members, 64):  # u = h . b of each member's noise row, in slices
         rows = h[p0 * T:(p0 + 64) * T].float().view(64, T, 512)
         u[p0 * T:(p0 + 64) * T] = torch.einsum('ptd,pd->pt', rows, db[torch.arange(p0, p0 + 64, device=device) // 2]).reshape(-1)
     hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
-    lo = torch.empty_like(hi)
+    lo = torch.empty_like(hi) if split else None
     nk.cast_bf16(W.to(device), hi, lo)
     ce = torch.empty(M, device=device)
     nk.head_ce(h, hi, lo, T, targets.to(device), ce, sign.to(device), NoiseRows(a=a.to(device), shift=1), u)
@@ -568,7 +575,7 @@ def test_config3_head_full_size(device):
     rows = torch.randint(0, M, (256,), generator=gc)
     hr = h[rows.to(device)].double().cpu()
     p = rows // T
-    z = hr @ W.double().t() + (sign[p].double() * u[rows.to(device)].double().cpu())[:, None] * a[p // 2].double()
+    z = hr @ Wd.t() + (sign[p].double() * u[rows.to(device)].double().cpu())[:, None] * a[p // 2].double()
     ref = R.softcap_ce(z, targets[rows % T])
     torch.testing.assert_close(ce[rows.to(device)].double().cpu(), ref, rtol=0, atol=5e-5)
     torch.testing.assert_close(losses.double().cpu(), ce.double().view(members, T).mean(1).cpu(), rtol=1e-6, atol=1e-6)

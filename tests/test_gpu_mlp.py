@@ -112,6 +112,89 @@ def test_mlp_fused_in_place_equals_out_of_place(device):
     assert torch.equal(out, xi)
 
 
+@pytest.mark.parametrize('T,members,shift,pert,kind', [
+    (256, 4, 1, True, 'mix_gate'),    # a value-embedding layer: mixing, q/k/v dots, gate
+    (100, 3, 0, True, 'mix'),         # ragged row blocks, no gate
+    (37, 5, 0, False, 'mix_gate'),    # T < 128, unperturbed (no dots, gate without noise)
+    (2048, 2, 1, True, 'mix'),
+    (256, 9, 1, True, 'final'),       # the final norm: no mixing, the head's dot only
+    (300, 2, 0, False, 'final'),
+])
+def test_mlp_fused_next_norm_matches_separate_mix_norm(device, T, members, shift, pert, kind):
+    """The next layer's mix_norm run in the MLP epilogue equals mlp_fused followed by mix_norm on
+    the same inputs: x to fp32 rounding of the same mixing formula, h bf16 within one rounding step
+    (the norm's sum runs in another order), the dots and gate of that h to fp32 summation order."""
+    g = torch.Generator().manual_seed(4000 + T + members)
+    w1, w2 = _weights(g)
+    M = members * T
+    rows = (members >> shift) + 1
+    x = torch.randn(M, D, generator=g) * 1.5
+    x0 = torch.randn(M, D, generator=g)
+    sign = torch.tensor([0.02 if j % 2 == 0 else -0.02 for j in range(members)], device=device)
+    nz = lambda w_a, w_b: NoiseRows(a=torch.randn(rows, w_a, generator=g).to(device),
+                                    b=torch.randn(rows, w_b, generator=g).to(device), shift=shift)
+    fc, pr = nz(F, D), nz(D, F)
+    w1p, w2p = _packed(w1, w2, device)
+    mix = kind != 'final'
+    nb = (3 if mix else 1) if pert else 0
+    bs = tuple(torch.randn(rows, D, generator=g).to(device) for _ in range(nb))
+    lam = torch.tensor([1.1, 0.2], device=device)
+    eps = torch.randn(rows, 8, generator=g).to(device), torch.randn(rows, 8, generator=g).to(device)
+    gate_w = torch.randn(8, 32, generator=g).to(device) if kind == 'mix_gate' else None
+    gate_nz = nz(8, 32) if kind == 'mix_gate' and pert else None
+    x0d = x0.to(device)
+    flags = _lib.MLP_NORM | _lib.MLP_RESIDUAL
+    s = sign if pert else None
+
+    def outputs():
+        return (torch.full((M, D), float('nan'), dtype=torch.bfloat16, device=device),
+                torch.full((M, max(nb, 1)), float('nan'), device=device),
+                torch.full((M, 8), float('nan'), device=device))
+
+    def args(xs, h, u, gate):
+        return K.mix_norm_args(xs, h, T, s, x0d if mix else None, lam[0] if mix else None, lam[1] if mix else None,
+                               eps[0][:, 3] if mix and pert else None, eps[1][:, 3] if mix and pert else None,
+                               shift, bs=bs, u=u, gate_w=gate_w, gate_nz=gate_nz, gate=gate)
+
+    xr, (hr, ur, gr) = x.to(device), outputs()
+    K.mlp_fused(xr, xr, T, members, w1p, w2p, flags, s, fc, pr)
+    K.run_mix_norm(args(xr, hr, ur, gr))
+    xf, (hf, uf, gf) = x.to(device), outputs()
+    K.mlp_fused(xf, xf, T, members, w1p, w2p, flags, s, fc, pr, next_norm=args(xf, hf, uf, gf))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(xf, xr, rtol=1e-6, atol=1e-5)
+    hf, hr = hf.float().cpu(), hr.float().cpu()
+    assert not hf.isnan().any()
+    assert ((hf - hr).abs() <= 2.0 ** -7 * hr.abs()).all()
+    assert (hf == hr).double().mean() >= 0.999
+    # the dots and the gate of the fused h (where the two h differ by a rounding step, so do they)
+    pn = (torch.arange(M) // T) >> shift
+    hd = hf.double()
+    for j in range(nb):
+        torch.testing.assert_close(uf[:, j].cpu().double(), (hd * bs[j].cpu().double()[pn]).sum(1),
+                                   rtol=1e-5, atol=1e-4)
+    if gate_w is not None:
+        z = hd[:, :32] @ gate_w.cpu().double().t()
+        if pert:
+            sp = sign.cpu().double()[torch.arange(M) // T][:, None]
+            z = z + sp * (hd[:, :32] * gate_nz.b.cpu().double()[pn]).sum(1, keepdim=True) * gate_nz.a.cpu().double()[pn]
+        torch.testing.assert_close(gf.cpu().double(), 2 * torch.sigmoid(z), rtol=1e-5, atol=1e-5)
+
+
+def test_mlp_fused_next_norm_rejects_a_mismatched_record(device):
+    g = torch.Generator().manual_seed(3)
+    w1p, w2p = _packed(*_weights(g), device)
+    T, members = 128, 2
+    x = torch.randn(members * T, D, generator=g).to(device)
+    other = torch.empty_like(x)
+    h = torch.empty(members * T, D, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match='next_norm'):
+        K.mlp_fused(x, x, T, members, w1p, w2p, _lib.MLP_NORM | _lib.MLP_RESIDUAL,
+                    next_norm=K.mix_norm_args(other, h, T))
+    with pytest.raises(ValueError, match='normed residual'):
+        K.mlp_fused(x, x, T, members, w1p, w2p, _lib.MLP_NORM, next_norm=K.mix_norm_args(x, h, T))
+
+
 PERM16 = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
 
 
