@@ -119,6 +119,17 @@ int noise_embed_norm(const float* table, int64_t ld_table, int vocab, int d,
                      const float* a, int64_t lda, const float* b, int64_t ldb, int member_shift,
                      float* x0, float* x, void* stream);
 
+struct noise_mixnorm_s;
+/* noise_embed_norm followed by the first layer's noise_mix_norm in one launch, on the rows still in
+ * registers: `next` mixes with this x0 (next->x0 == x0) over the same members * T rows and writes
+ * the stream next->x, h, the dots and the gate (the plain copy x of noise_embed_norm is not
+ * written). Replaces eggroll.py:74 (`x = x0 = norm(lowrank_embed(...))`) together with the first
+ * iteration of eggroll.py:77-81, 88. */
+int noise_embed_mix_norm(const float* table, int64_t ld_table, int vocab, int d,
+                         const int64_t* idx, int64_t idx_stride, int T, int members, const float* sign,
+                         const float* a, int64_t lda, const float* b, int64_t ldb, int member_shift,
+                         float* x0, const struct noise_mixnorm_s* next, void* stream);
+
 /* ---- residual mixing + RMSNorm + the dots of the consuming GEMMs ------------------------ */
 typedef struct noise_mixnorm_s {
   float* x;             /* [M, 512] fp32 stream (updated in place when mixing) */

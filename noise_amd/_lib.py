@@ -100,6 +100,7 @@ SIGNATURES = {
     'noise_mlp_fused': [C.POINTER(Mlp), P],
     'noise_mlp_pack': [P, I64, P, I64, P, P, P],
     'noise_embed_norm': [P, I64, INT, INT, P, I64, INT, INT, P, P, I64, P, I64, INT, P, P, P],
+    'noise_embed_mix_norm': [P, I64, INT, INT, P, I64, INT, INT, P, P, I64, P, I64, INT, P, C.POINTER(MixNorm), P],
     'noise_mix_norm': [C.POINTER(MixNorm), P],
     'noise_rope_norm_ve': [C.POINTER(Rope), P],
     'noise_qkv_rope_gemm': [P, I64, P, I64, INT, INT, C.POINTER(Rank1), C.POINTER(Rope), P],

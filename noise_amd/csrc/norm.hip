@@ -43,10 +43,16 @@ NOISE_DEV void store8(float* p, const float (&v)[8]) {
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
+NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, int row, int lane, float (&v)[8], const float (&v0)[8]);
+
+// NEXT: the first layer's mix_norm (noise_mixnorm_t `nx`, mixing with x0 = this row) follows on
+// the row still in registers; it writes the stream nx.x instead of the plain copy x.
+template <bool NEXT>
 __global__ __launch_bounds__(256) void embed_norm_kernel(
     const float* __restrict__ table, int64_t ld_table, int vocab, const int64_t* __restrict__ idx,
     int64_t idx_stride, int T, int M, const float* __restrict__ sign, const float* __restrict__ a, int64_t lda,
-    const float* __restrict__ b, int64_t ldb, int shift, float* __restrict__ x0, float* __restrict__ x) {
+    const float* __restrict__ b, int64_t ldb, int shift, float* __restrict__ x0, float* __restrict__ x,
+    const noise_mixnorm_t nx) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -76,31 +82,32 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(
 #pragma unroll
   for (int k = 0; k < 8; ++k) v[k] *= r;
   store8(x0 + (int64_t)row * D + c, v);
-  if (x) store8(x + (int64_t)row * D + c, v);
+  if constexpr (NEXT) {
+    float w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = v[k];
+    mix_norm_row(nx, row, lane, w, v);
+  } else {
+    if (x) store8(x + (int64_t)row * D + c, v);
+  }
 }
 
-__global__ __launch_bounds__(256) void mix_norm_kernel(const noise_mixnorm_t g) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= g.M) return;
+// mix_norm of one row (one wavefront, lane l: columns 8 l .. 8 l + 7) from its x values v and, when
+// mixing, its x0 values v0.
+NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, int row, int lane, float (&v)[8], const float (&v0)[8]) {
   const int p = row / g.T;
   const int64_t pn = p >> g.member_shift;
   const float s = g.sign ? g.sign[p] : 0.f;
   const int c = lane * 8;
-  float* xr = g.x + (int64_t)row * D + c;
-  float v[8];
-  load8(xr, v);
   if (g.x0) {
     float r = *g.resid, m = *g.mix;
     if (g.sign) {
       r += s * g.eps_resid[pn * g.ld_eps];
       m += s * g.eps_mix[pn * g.ld_eps];
     }
-    float v0[8];
-    load8(g.x0 + (int64_t)row * D + c, v0);
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = r * v[k] + m * v0[k];
-    store8(xr, v);
+    store8(g.x + (int64_t)row * D + c, v);
   }
   float ss = 0.f;
 #pragma unroll
@@ -155,6 +162,16 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(const noise_mixnorm_t g) 
       g.gate[(int64_t)row * 8 + q] = 2.0f / (1.0f + expf(-z));
     }
   }
+}
+
+__global__ __launch_bounds__(256) void mix_norm_kernel(const noise_mixnorm_t g) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.M) return;
+  float v[8], v0[8];
+  load8(g.x + (int64_t)row * D + lane * 8, v);
+  if (g.x0) load8(g.x0 + (int64_t)row * D + lane * 8, v0);
+  mix_norm_row(g, row, lane, v, v0);
 }
 
 // One wavefront per row of the [M, 1536] fp32 q | k | v block.
@@ -238,9 +255,34 @@ extern "C" int noise_embed_norm(const float* table, int64_t ld_table, int vocab,
   const int64_t M = (int64_t)members * T;
   NOISE_REQUIRE(M < (1ll << 31), "embed_norm: too many rows");
   if (M == 0) return NOISE_OK;
-  embed_norm_kernel<<<(int)((M + 3) / 4), 256, 0, (hipStream_t)stream>>>(
-      table, ld_table, vocab, idx, idx_stride, T, (int)M, sign, a, lda, b, ldb, member_shift, x0, x);
+  embed_norm_kernel<false><<<(int)((M + 3) / 4), 256, 0, (hipStream_t)stream>>>(
+      table, ld_table, vocab, idx, idx_stride, T, (int)M, sign, a, lda, b, ldb, member_shift, x0, x,
+      noise_mixnorm_t{});
   return noise::check_launch("embed_norm");
+}
+
+extern "C" int noise_embed_mix_norm(const float* table, int64_t ld_table, int vocab, int d,
+                                    const int64_t* idx, int64_t idx_stride, int T, int members,
+                                    const float* sign, const float* a, int64_t lda, const float* b, int64_t ldb,
+                                    int member_shift, float* x0, const noise_mixnorm_t* next, void* stream) {
+  NOISE_REQUIRE(next, "embed_mix_norm: null mix_norm record");
+  const noise_mixnorm_t& g = *next;
+  NOISE_REQUIRE(g.x && g.h && g.x0 == x0 && g.T == T && (int64_t)g.M == (int64_t)members * T,
+                "embed_mix_norm: the mix_norm must mix with this x0 over the same members * T rows");
+  // the same checks as the two launches it replaces
+  int rc = noise_embed_norm(table, ld_table, vocab, d, idx, idx_stride, T, 0, sign, a, lda, b, ldb, member_shift,
+                            x0, nullptr, stream);
+  if (rc != NOISE_OK) return rc;
+  noise_mixnorm_t empty = g;
+  empty.M = 0;
+  rc = noise_mix_norm(&empty, stream);
+  if (rc != NOISE_OK) return rc;
+  const int64_t M = (int64_t)members * T;
+  NOISE_REQUIRE(M < (1ll << 31), "embed_mix_norm: too many rows");
+  if (M == 0) return NOISE_OK;
+  embed_norm_kernel<true><<<(int)((M + 3) / 4), 256, 0, (hipStream_t)stream>>>(
+      table, ld_table, vocab, idx, idx_stride, T, (int)M, sign, a, lda, b, ldb, member_shift, x0, nullptr, g);
+  return noise::check_launch("embed_mix_norm");
 }
 
 extern "C" int noise_mix_norm(const noise_mixnorm_t* args, void* stream) {

@@ -150,7 +150,9 @@ def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=N
     _lib.call('noise_mlp_fused', C.byref(g), _stream())
 
 
-def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0):
+def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0, next_norm=None):
+    """x0 = norm(W[idx] + s a[idx] b) and x = x0 (when given), or, with next_norm (a mix_norm_args
+    record mixing with this x0), the first layer's mix_norm on the rows in the same launch."""
     _on_gpu(table, idx, x0, x)
     _need(idx.dtype == torch.int64, 'idx must be int64')
     a = b = None
@@ -159,9 +161,13 @@ def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0):
     if sign is not None:
         a, b, shift = nz.a, nz.b, nz.shift
         lda, ldb = a.stride(0), b.stride(0)
-    _lib.call('noise_embed_norm', _ptr(table), table.stride(0), table.shape[0], table.shape[1], _ptr(idx),
-              idx_stride, T, members, _ptr(sign), _ptr(a), lda, _ptr(b), ldb, shift, _ptr(x0), _ptr(x),
-              _stream())
+    head = (_ptr(table), table.stride(0), table.shape[0], table.shape[1], _ptr(idx), idx_stride, T, members,
+            _ptr(sign), _ptr(a), lda, _ptr(b), ldb, shift, _ptr(x0))
+    if next_norm is None:
+        _lib.call('noise_embed_norm', *head, _ptr(x), _stream())
+    else:
+        _need(isinstance(next_norm, MixNorm) and x is None, 'embed_norm: next_norm replaces the copy x')
+        _lib.call('noise_embed_mix_norm', *head, C.byref(next_norm), _stream())
 
 
 def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,

@@ -15,8 +15,8 @@ Per layer the engine runs (one launch each, all on the current stream):
   mlp_fused     x += bf16(relu(h Wfc^T + s u_fc a_fc^T)^2) Wmp^T + s u_mp a_mp^T with
                 h = bf16(norm x), u_fc = h.b_fc, u_mp = hid.b_mp: the hidden stays on chip;
                 its epilogue runs the next layer's mix_norm on the finished rows
-then the final norm + u_head (in the last MLP's epilogue), head_ce (fp32-accurate head, soft-cap,
-CE) and member_mean. Only layer 0's mix_norm is a launch of its own.
+then the final norm + u_head (in the last MLP's epilogue), head_ce (bf16 head, soft-cap, CE) and
+member_mean. Layer 0's mix_norm runs in the embedding launch.
 """
 import math
 
@@ -123,8 +123,8 @@ class Engine:
         # False runs the MLP as mix_norm + two lowrank_gemm launches through an HBM hidden
         # (kept to compare the two on the same inputs).
         self.fused_mlp = True
-        # With the fused MLP: True runs the next layer's mix_norm (and the final norm) in the
-        # MLP's epilogue instead of as launches of their own.
+        # True runs every mix_norm inside the launch before it (the embedding for the first layer,
+        # the fused MLP for the later ones and the final norm) instead of as launches of their own.
         self.fuse_next_norm = True
 
     def _mark(self):
@@ -183,9 +183,11 @@ class Engine:
                 gate_w=W.gate(i) if ve else None, gate_nz=g(pre + 'attn.ve_gate.weight') if ve else None,
                 gate=gate)
 
-        K.embed_norm(P['transformer.wte.weight'], idx, T, members, sign, g('transformer.wte.weight'), x0, x,
-                     idx_stride)
-        carried = False  # the previous MLP ran this layer's mix_norm in its epilogue
+        # the first layer's mix_norm runs in the embedding launch, every later one (and the final
+        # norm) in the epilogue of the MLP before it
+        carried = self.fuse_next_norm
+        K.embed_norm(P['transformer.wte.weight'], idx, T, members, sign, g('transformer.wte.weight'), x0,
+                     None if carried else x, idx_stride, next_norm=mixing(0) if carried else None)
         for i in range(cfg.n_layer):
             pre = f'transformer.h.{i}.'
             q, k, v, o = (g(pre + f'attn.{n}.weight') for n in ('c_q', 'c_k', 'c_v', 'c_proj'))

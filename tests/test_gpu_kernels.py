@@ -124,6 +124,53 @@ def test_embed_norm(device):
     assert torch.isnan(rows[:, 5]).all() and not torch.isnan(rows[:, 4]).any()
 
 
+@pytest.mark.parametrize('pert,gate', [(True, True), (False, True), (True, False)])
+def test_embed_mix_norm_matches_two_launches(device, pert, gate):
+    """embed_norm with the first layer's mix_norm in the same launch equals embed_norm (x = x0)
+    followed by mix_norm on the same inputs: x0 bit-exact, the rest to fp32 rounding."""
+    g = _gen(41)
+    V, T, m = 4096, 66, 4
+    M = m * T
+    table = torch.randn(V, 512, generator=g).to(device)
+    idx = torch.randint(0, V, (T,), generator=g).to(device)
+    sign = torch.tensor([0.5, -0.5, 0.1, -0.1], device=device) if pert else None
+    nz = NoiseRows(a=torch.randn(2, V, generator=g).to(device), b=torch.randn(2, 512, generator=g).to(device), shift=1)
+    lam = torch.tensor([1.1, 0.2], device=device)
+    eps = torch.randn(2, 8, generator=g).to(device), torch.randn(2, 8, generator=g).to(device)
+    bs = tuple(torch.randn(2, 512, generator=g).to(device) for _ in range(3)) if pert else ()
+    gw = torch.randn(8, 32, generator=g).to(device) if gate else None
+    gnz = NoiseRows(a=torch.randn(2, 8, generator=g).to(device), b=torch.randn(2, 32, generator=g).to(device),
+                    shift=1) if gate and pert else None
+    outs = []
+    for fused in (False, True):
+        x0 = torch.full((M, 512), float('nan'), device=device)
+        x = torch.full_like(x0, float('nan'))
+        h = torch.full((M, 512), float('nan'), dtype=torch.bfloat16, device=device)
+        u = torch.full((M, 3), float('nan'), device=device)
+        gt = torch.full((M, 8), float('nan'), device=device)
+        rec = nk.mix_norm_args(x, h, T, sign, x0, lam[0], lam[1], eps[0][:, 2] if pert else None,
+                               eps[1][:, 2] if pert else None, 1, bs=bs, u=u, gate_w=gw, gate_nz=gnz, gate=gt)
+        if fused:
+            nk.embed_norm(table, idx, T, m, sign, nz, x0, None, next_norm=rec)
+        else:
+            nk.embed_norm(table, idx, T, m, sign, nz, x0, x)
+            nk.run_mix_norm(rec)
+        outs.append((x0, x, h, u, gt))
+    (x0a, xa, ha, ua, ga), (x0b, xb, hb, ub, gb) = outs
+    assert torch.equal(x0a, x0b)
+    torch.testing.assert_close(xb, xa, rtol=1e-6, atol=1e-6)
+    hd = (hb.float() - ha.float()).abs()
+    assert (hd <= 2.0 ** -7 * ha.float().abs()).all() and (hd == 0).double().mean() >= 0.999
+    if pert:
+        torch.testing.assert_close(ub, ua, rtol=1e-5, atol=1e-4)
+    if gate:
+        torch.testing.assert_close(gb, ga, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError, match='same members'):
+        bad = nk.mix_norm_args(xb, hb, T, sign, x0a, lam[0], lam[1], eps[0][:, 2] if pert else None,
+                               eps[1][:, 2] if pert else None, 1)
+        nk.embed_norm(table, idx, T, m, sign, nz, x0b, None, next_norm=bad)
+
+
 @pytest.mark.parametrize('T', [64, 66])  # 4 rows per wave / one row per wave (T % 4 != 0)
 def test_mix_norm(device, T):
     g = _gen(5)
