@@ -18,8 +18,8 @@ the rank-normalised fitness, the rank-1 gradient rebuild and an AdamW update of 
 Printed: one JSON line. `value` = members * tokens * steps / wall time of the timed steps (inputs
 resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (`mlp_fused`: norm,
 c_fc with its rank-1 term, relu^2, c_proj with its rank-1 term and the residual add in one launch,
-the hidden kept on chip): algorithmic FLOPs per launch / its mean duration, timed live with HIP
-events on the launch stream.
+the hidden kept on chip, and the next layer's mix_norm on the finished rows): algorithmic MLP
+FLOPs per launch / its mean duration, timed live with HIP events on the launch stream.
 `cpu_baseline` times the CPU oracle (oracle/model_ref.py, float32) on a bounded sample of the same
 workload on this host.
 """
@@ -45,7 +45,7 @@ def mlp_flops(rows, d=512, f=2048):
 
 
 def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 1024, 1024, 2048) * 2):
-    """Algorithmic FLOPs of the population forward per step (fp32-accurate head counted once)."""
+    """Algorithmic FLOPs of the population forward per step (GEMMs, attention products, head)."""
     per_tok = 0
     for w in windows[:layers]:
         keys = sum(min(t, w) + 1 for t in range(T)) / T
@@ -86,10 +86,34 @@ def mlp_inputs(rows=512 * 2048, d=512, f=2048, seed=0):
     return dict(x=x, T=T, members=members, w_fc=w_fc, w_pr=w_pr, sign=sign, fc=fc, pr=pr)
 
 
+def next_mix_norm(a, seed=1):
+    """The record of the next layer's mix_norm as the step hands it to mlp_fused, for a layer with
+    a value embedding: x0 mixing with perturbed lambdas, h, the q/k/v dots and the gate."""
+    from noise_amd import kernels as K
+    from noise_amd.kernels import NoiseRows
+    x = a['x']
+    dev, M, rows, shift = x.device, x.shape[0], a['fc'].a.shape[0], a['fc'].shift
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a['x0'] = torch.randn(M, 512, device=dev, generator=g)
+    a['h'] = torch.empty(M, 512, dtype=torch.bfloat16, device=dev)
+    a['u3'] = torch.empty(M, 3, device=dev)
+    a['gate'] = torch.empty(M, 8, device=dev)
+    a['bs'] = tuple(torch.randn(rows, 512, device=dev, generator=g) for _ in range(3))
+    a['lam'] = torch.tensor([1.1, 0.2], device=dev)
+    a['eps'] = torch.randn(rows, 2, device=dev, generator=g)
+    a['gw'] = torch.randn(8, 32, device=dev, generator=g) * 0.1
+    a['gnz'] = NoiseRows(a=torch.randn(rows, 8, device=dev, generator=g), b=torch.randn(rows, 32, device=dev, generator=g),
+                         shift=shift)
+    return K.mix_norm_args(x, a['h'], a['T'], a['sign'], a['x0'], a['lam'][0], a['lam'][1], a['eps'][:, 0],
+                           a['eps'][:, 1], shift, bs=a['bs'], u=a['u3'], gate_w=a['gw'], gate_nz=a['gnz'],
+                           gate=a['gate'])
+
+
 def probe_mlp(reps=3):
     """Counter-collection workload: `reps` copies of a 1 GiB fp32 buffer (1 GiB read + 1 GiB
     written per dispatch), then `reps` fused-MLP launches at the bench shape (512 members x 2048
-    tokens, pair-shared noise rows), the step's kernel and flags."""
+    tokens, pair-shared noise rows) as the step runs them: normed residual MLP with the next
+    layer's mix_norm (a value-embedding layer's) in the epilogue."""
     import noise_amd  # noqa: F401  (loads the library)
     from noise_amd import _lib
     from noise_amd import kernels as K
@@ -101,11 +125,13 @@ def probe_mlp(reps=3):
         dst.copy_(src)
     del src, dst
     a = mlp_inputs()
+    nxt = next_mix_norm(a)
     for _ in range(reps):
         K.mlp_fused(a['x'], a['x'], a['T'], a['members'], a['w_fc'], a['w_pr'], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
-                    a['sign'], a['fc'], a['pr'])
+                    a['sign'], a['fc'], a['pr'], next_norm=nxt)
     torch.cuda.synchronize()
-    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused over {a["x"].shape[0]} rows', flush=True)
+    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused (with the next mix_norm) over {a["x"].shape[0]} rows',
+          flush=True)
 
 
 def probe_step(members=512, T=2048):
@@ -495,7 +521,8 @@ def main():
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
                      'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(),
-                     'kernel': 'mlp_fused: norm + c_fc + rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip',
+                     'kernel': 'mlp_fused: norm + c_fc + rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip, '
+                               "then the next layer's mix_norm (x0 mixing, norm, q/k/v dots, gate) in the epilogue",
                      'flops_per_launch': flops, 'rows_per_launch': rows, 'launch_ms': mlp_ms},
         'step_tflops': step_flops(members, T) / (elapsed / args.steps) / 1e12,
         'mean_loss': losses[-1],
