@@ -91,6 +91,19 @@ typedef struct {
    * NORM | RESIDUAL, next->x == out, next->M == members * T with out contiguous
    * (ld_out 512, member_stride_out T * 512), and next->h 16-byte aligned. */
   const struct noise_mixnorm_s* next;
+  /* Optional (attn_y NULL = none): the attention c_proj first, on the input rows:
+   * in + attn_y attn_w^T + sign (sum of attn_u's parts) attn_a^T, then the MLP on that (flags
+   * NORM | RESIDUAL). attn_y: bf16 [members * T, >= 512], row p * T + t; attn_w: the bf16 copy of
+   * attn.c_proj.weight [512 out, 512 in]; attn_u: [rows, >= attn_parts] per-head y . b dots;
+   * attn_a: [noise rows, 512]. */
+  const uint16_t* attn_y;
+  int64_t ld_attn_y;
+  const uint16_t* attn_w;
+  const float* attn_u;
+  int64_t ld_attn_u;
+  int attn_parts;
+  const float* attn_a;
+  int64_t ld_attn_a;
 } noise_mlp_t;
 
 /* out = [in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 in one launch, the [rows, 2048] hidden

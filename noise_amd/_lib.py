@@ -44,7 +44,8 @@ class Mlp(C.Structure):
                 ('member_stride_out', I64), ('T', INT), ('members', INT), ('flags', INT), ('w_fc', P),
                 ('w_proj', P), ('sign', P), ('member_shift', INT), ('a_fc', P), ('ld_a_fc', I64), ('b_fc', P),
                 ('ld_b_fc', I64), ('a_proj', P), ('ld_a_proj', I64), ('b_proj', P), ('ld_b_proj', I64),
-                ('next', C.POINTER(MixNorm))]
+                ('next', C.POINTER(MixNorm)), ('attn_y', P), ('ld_attn_y', I64), ('attn_w', P), ('attn_u', P),
+                ('ld_attn_u', I64), ('attn_parts', INT), ('attn_a', P), ('ld_attn_a', I64)]
 
 
 class Attention(C.Structure):

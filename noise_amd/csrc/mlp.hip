@@ -383,7 +383,66 @@ NOISE_DEV void mix_norm_epilogue(const noise_mlp_t& g, const noise_mixnorm_t& nx
 
 // NEXT 1 | 2: the next layer's mix_norm (noise_mixnorm_t `nx`; 2: with x0 mixing) runs in the
 // epilogue on the finished rows.
-template <bool NORM, bool RESID, int NEXT>
+// Chunk Q of the attention c_proj in the prologue (ATTN): wait for it, start chunk Q + 2 (and at
+// Q = 15 the first c_fc chunk), then its 32 MFMAs acc[8 hh + nbb] += y[k-step 4 kc + ks4] Wo^T,
+// the fragments of k-step ks4 + 1 read while those of ks4 run.
+template <int Q, class WoLoad>
+NOISE_DEV void attn_chunk(const noise_mlp_t& g, unsigned char* lds, floatx16 (&acc)[16], const bf16x8 (&yA)[32],
+                          const uint32_t (&fk)[4], uint32_t lds0a, int wave, int lane, int c0, WoLoad& wo_load) {
+  constexpr int kc = Q >> 1, hh = Q & 1, sl = Q & 3;
+  constexpr uint32_t sbase = (sl >> 1) * STAGE + (sl & 1) * 32768;
+  // chunk Q has landed for every wave, and every wave is done with chunk Q - 1
+  if constexpr (Q < 15)
+    __asm__ volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else
+    __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if constexpr (Q + 2 < 16) wo_load(Q + 2);  // into slot (Q + 2) % 4, last read at chunk Q - 2
+  if constexpr (Q == 15) load_stage(g, lds, wave, lane, 0, 0, -1, c0);  // slots 0 and 1 are free
+  // 8 groups of 4 MFMAs (k-step ks4 = G / 2, blocks 4 (G % 2) .. + 3); the fragments of group
+  // G + 1 are read while those of G run (two buffers of 4: fewer live registers than a whole
+  // k-step ahead, which made the compiler move accumulators through VGPRs).
+  bf16x8 fb[2][4];
+  auto rd = [&](int G, bf16x8 (&dst)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __asm__ volatile("ds_read_b128 %0, %1 offset:%2"
+                       : "=v"(dst[i]) : "v"(lds0a + sbase + fk[(G >> 1) & 3]), "i"(((G & 1) * 4 + i) * 4096));
+  };
+  rd(0, fb[0]);
+#pragma unroll
+  for (int G = 0; G < 8; ++G) {
+    if (G + 1 < 8) {
+      rd(G + 1, fb[(G + 1) & 1]);
+      MLP_LGKM(4);
+    } else {
+      MLP_LGKM(0);
+    }
+    __asm__ volatile("" : "+v"(fb[G & 1][0]), "+v"(fb[G & 1][1]), "+v"(fb[G & 1][2]), "+v"(fb[G & 1][3]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (kc == 0)  // an accumulator's first MFMA: the compiler may have just copied it into place
+        __asm__ volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                         : "+a"(acc[8 * hh + (G & 1) * 4 + i]) : "v"(yA[4 * kc + (G >> 1)]), "v"(fb[G & 1][i]));
+      else if constexpr (kc == 7)  // its last: the compiler may spill or copy it right after the asm
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 4"
+                         : "+a"(acc[8 * hh + (G & 1) * 4 + i]) : "v"(yA[4 * kc + (G >> 1)]), "v"(fb[G & 1][i]));
+      else
+        __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                         : "+a"(acc[8 * hh + (G & 1) * 4 + i]) : "v"(yA[4 * kc + (G >> 1)]), "v"(fb[G & 1][i]));
+    }
+  }
+}
+
+template <class WoLoad, int... Q>
+NOISE_DEV void attn_chunks(const noise_mlp_t& g, unsigned char* lds, floatx16 (&acc)[16], const bf16x8 (&yA)[32],
+                           const uint32_t (&fk)[4], uint32_t lds0a, int wave, int lane, int c0, WoLoad& wo_load,
+                           std::integer_sequence<int, Q...>) {
+  (attn_chunk<Q>(g, lds, acc, yA, fk, lds0a, wave, lane, c0, wo_load), ...);
+}
+
+// ATTN: the attention c_proj (x += y Wo^T + s u_o a_o^T) runs on the rows in the prologue, before
+// the norm.
+template <bool NORM, bool RESID, int NEXT, bool ATTN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[NEXT ? LDS_NEXT_BYTES : LDS_BYTES];
@@ -420,8 +479,33 @@ mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
   float* s_amp = s_bmp + F;
   float* s_bfc = s_amp + D;
 
-  // The first c_fc chunk starts streaming into stage 0 while the rows are normalised.
-  load_stage(g, lds, wave, lane, 0, 0, -1, c0);
+  // The first c_fc chunk starts streaming into stage 0 while the rows are normalised (with ATTN
+  // the stage buffers first carry the attention c_proj weight; the chunk follows it).
+  // With ATTN: Wo streams through the two stage buffers as 16 chunks of 256 output rows x 64 K
+  // (32 KB of 128-byte rows, chunk c of row n at c ^ ((n >> 1) & 7)); chunk q sits in the 32 KB
+  // slot q % 4 and is loaded two chunks ahead, 8 loads of 1 KB per wave.
+  auto wo_load = [&](int q) {
+    const int kc = q >> 1, hh = q & 1, sl = q & 3;
+    unsigned char* st = lds + (sl >> 1) * STAGE + (sl & 1) * 32768;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int blk = 8 * wave + i, rl = 8 * blk + (lane >> 3);
+      const int lc = (lane & 7) ^ ((rl >> 1) & 7);
+      __builtin_amdgcn_global_load_lds((const void*)(g.attn_w + (int64_t)(256 * hh + rl) * D + 64 * kc + 8 * lc),
+                                       (void*)(st + blk * 1024), 16, 0, 0);
+    }
+  };
+  bf16x8 yA[ATTN ? 32 : 1];  // the wave's 32 rows of y as the A operand (lane l: row l % 32)
+  if constexpr (ATTN) {
+    wo_load(0);
+    wo_load(1);
+    const int ry = tb + r < g.T ? tb + r : g.T - 1;
+    const uint16_t* ysrc = g.attn_y + ((int64_t)p * g.T + ry) * g.ld_attn_y + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < 32; ++ks) yA[ks] = *reinterpret_cast<const bf16x8*>(ysrc + 16 * ks);
+  } else {
+    load_stage(g, lds, wave, lane, 0, 0, -1, c0);
+  }
 
   // ---- prologue, one pass over the input: the wave's 32 rows land in the c_proj accumulator
   // layout (lane l holds column 32 nb + l % 32 of rows 8 (j / 4) + 4 (l / 32) + j % 4), where they
@@ -454,15 +538,54 @@ mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
   for (int j = 0; j < 16; ++j) {
     if (j + 3 < 16) MLP_XLOAD(j + 3)
     MLP_XWAIT(j, 16 * (15 - j < 3 ? 15 - j : 3));
-    ps[j] = 0.f;
+    if constexpr (!ATTN) {
+      ps[j] = 0.f;
 #pragma unroll
-    for (int nb = 0; nb < 16; ++nb) {
-      const float v = agpr_read(acc[nb][j]);
-      ps[j] += v * v;
+      for (int nb = 0; nb < 16; ++nb) {
+        const float v = agpr_read(acc[nb][j]);
+        ps[j] += v * v;
+      }
     }
   }
 #undef MLP_XWAIT
 #undef MLP_XLOAD
+  if constexpr (ATTN) {
+    // ---- the attention c_proj into the accumulators: 16 chunks x (4 k-steps x 8 column blocks).
+    // Fragment (k-step ks4, block nbb) of a chunk: row 32 nbb + r, logical 16-byte piece
+    // 2 ks4 + half.
+    const uint32_t lds0a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds;
+    uint32_t fk[4];
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) fk[ks4] = (uint32_t)(r * 128 + (((2 * ks4 + half) ^ ((r >> 1) & 7)) * 16));
+    attn_chunks(g, lds, acc, yA, fk, lds0a, wave, lane, c0, wo_load, std::make_integer_sequence<int, 16>{});
+    __asm__ volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // last MFMAs before VALU reads
+    // the rank-1 term s (sum over the per-head parts of y . b_o) a_o of the rows' member
+    if (pert) {
+      const int ry = tb + r < g.T ? tb + r : g.T - 1;
+      const float* up = g.attn_u + ((int64_t)p * g.T + ry) * g.ld_attn_u;
+      float u = 0.f;
+      for (int k = 0; k < g.attn_parts; ++k) u += up[k];
+      const float su_r = s * u;
+      float ao[16];
+#pragma unroll
+      for (int nb = 0; nb < 16; ++nb) ao[nb] = g.attn_a[pn * g.ld_attn_a + nb * 32 + r];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float suj = __shfl(su_r, 8 * (j >> 2) + 4 * half + (j & 3), 64);
+#pragma unroll
+        for (int nb = 0; nb < 16; ++nb) acc[nb][j] = agpr_read(acc[nb][j]) + suj * ao[nb];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      ps[j] = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < 16; ++nb) {
+        const float v = agpr_read(acc[nb][j]);
+        ps[j] += v * v;
+      }
+    }
+  }
 
   // The member's perturbation rows, 5120 floats (20 per thread); zeros when unperturbed, so the
   // rank-1 terms vanish without a branch in the main loop.
@@ -698,6 +821,16 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
                       ((uintptr_t)g.a_proj % 16) == 0 && ((uintptr_t)g.b_proj % 16) == 0,
                   "mlp_fused: noise rows must be 16-byte aligned");
   }
+  if (g.attn_y) {
+    NOISE_REQUIRE(g.flags == (NOISE_MLP_NORM | NOISE_MLP_RESIDUAL),
+                  "mlp_fused: the attention c_proj needs the normed residual MLP");
+    NOISE_REQUIRE(g.attn_w && g.ld_attn_y >= D && g.ld_attn_y % 8 == 0 && ((uintptr_t)g.attn_y % 16) == 0 &&
+                      ((uintptr_t)g.attn_w % 16) == 0,
+                  "mlp_fused: attention y [members * T, >= 512] bf16 and Wo [512, 512] bf16, 16-byte aligned rows");
+    NOISE_REQUIRE(!g.sign || (g.attn_u && g.attn_a && g.attn_parts >= 1 && g.ld_attn_u >= g.attn_parts &&
+                              g.ld_attn_a >= D),
+                  "mlp_fused: the perturbed attention c_proj needs u [rows, parts] and a [noise rows, 512]");
+  }
   const int64_t blocks = (int64_t)g.members * ((g.T + ROWS - 1) / ROWS);
   NOISE_REQUIRE(blocks < (1ll << 31), "mlp_fused: too many rows");
   if (blocks == 0) return NOISE_OK;
@@ -720,17 +853,23 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
                   "mlp_fused: next gate needs its output and perturbation vectors");
     NOISE_REQUIRE(((uintptr_t)nx.h % 16) == 0, "mlp_fused: next h must be 16-byte aligned");
     NOISE_REQUIRE(nx.member_shift >= 0 && nx.member_shift < 31, "mlp_fused: next mix_norm has a bad member_shift");
-    if (nx.x0)
-      mlp_fused_kernel<true, true, 2><<<grid, 256, 0, st>>>(g, nx);
-    else
-      mlp_fused_kernel<true, true, 1><<<grid, 256, 0, st>>>(g, nx);
+    if (g.attn_y) {
+      if (nx.x0) mlp_fused_kernel<true, true, 2, true><<<grid, 256, 0, st>>>(g, nx);
+      else mlp_fused_kernel<true, true, 1, true><<<grid, 256, 0, st>>>(g, nx);
+    } else {
+      if (nx.x0) mlp_fused_kernel<true, true, 2, false><<<grid, 256, 0, st>>>(g, nx);
+      else mlp_fused_kernel<true, true, 1, false><<<grid, 256, 0, st>>>(g, nx);
+    }
     return noise::check_launch("mlp_fused (with the next mix_norm)");
   }
   switch (g.flags) {
-    case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL: mlp_fused_kernel<true, true, 0><<<grid, 256, 0, st>>>(g, none); break;
-    case NOISE_MLP_NORM: mlp_fused_kernel<true, false, 0><<<grid, 256, 0, st>>>(g, none); break;
-    case NOISE_MLP_RESIDUAL: mlp_fused_kernel<false, true, 0><<<grid, 256, 0, st>>>(g, none); break;
-    default: mlp_fused_kernel<false, false, 0><<<grid, 256, 0, st>>>(g, none); break;
+    case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL:
+      if (g.attn_y) mlp_fused_kernel<true, true, 0, true><<<grid, 256, 0, st>>>(g, none);
+      else mlp_fused_kernel<true, true, 0, false><<<grid, 256, 0, st>>>(g, none);
+      break;
+    case NOISE_MLP_NORM: mlp_fused_kernel<true, false, 0, false><<<grid, 256, 0, st>>>(g, none); break;
+    case NOISE_MLP_RESIDUAL: mlp_fused_kernel<false, true, 0, false><<<grid, 256, 0, st>>>(g, none); break;
+    default: mlp_fused_kernel<false, false, 0, false><<<grid, 256, 0, st>>>(g, none); break;
   }
   return noise::check_launch("mlp_fused");
 }

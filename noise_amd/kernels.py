@@ -108,11 +108,14 @@ def mlp_pack(w_fc=None, fc_packed=None, w_proj=None, proj_packed=None):
 
 
 def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=None, fc=None, proj=None,
-              member_stride_in=None, member_stride_out=None, next_norm=None):
+              member_stride_in=None, member_stride_out=None, next_norm=None, attn=None):
     """x_out = [x_in +] c_proj(relu(c_fc(h) + rank-1)^2) + rank-1 with h = bf16(norm x_in) under
     MLP_NORM (else bf16(x_in)), in one launch. x_in / x_out: fp32 rows of 512; member p's rows
     start at p * member_stride (default T rows). fc / proj: NoiseRows of c_fc and c_proj.
-    next_norm: a mix_norm_args record over x_out, run on the finished rows in the same launch."""
+    next_norm: a mix_norm_args record over x_out, run on the finished rows in the same launch.
+    attn: (y, w_o, u, nz_o) -- the attention c_proj first, x_in + y w_o^T + s (u summed over its
+    columns) a_o^T: y [members * T, 512] bf16, w_o [512, 512] bf16, u [members * T, parts] fp32
+    and nz_o the c_proj NoiseRows (u and nz_o None when unperturbed)."""
     _on_gpu(x_in, x_out, w_fc_packed, w_proj_packed, sign)
     ld_in = _rows(x_in, 512, torch.float32, 'x_in')
     ld_out = _rows(x_out, 512, torch.float32, 'x_out')
@@ -147,6 +150,21 @@ def mlp_fused(x_in, x_out, T, members, w_fc_packed, w_proj_packed, flags, sign=N
         _need(isinstance(next_norm, MixNorm) and next_norm.x == x_out.data_ptr() and next_norm.M == members * T,
               'mlp_fused: next_norm must be a mix_norm_args record over the rows of x_out')
         g.next = C.pointer(next_norm)
+    if attn is not None:
+        y, w_o, u, nz_o = attn
+        _on_gpu(y, w_o, u)
+        ld_y = _rows(y, 512, torch.bfloat16, 'attn y')
+        _need(y.shape[0] >= members * T, 'mlp_fused: attn y has too few rows')
+        _need(w_o.dtype == torch.bfloat16 and tuple(w_o.shape) == (512, 512) and w_o.is_contiguous(),
+              'mlp_fused: attn w_o must be a contiguous [512, 512] bf16 tensor')
+        g.attn_y, g.ld_attn_y, g.attn_w = y.data_ptr(), ld_y, w_o.data_ptr()
+        if sign is not None:
+            _need(u is not None and nz_o is not None and u.dtype == torch.float32 and u.dim() == 2 and
+                  u.stride(1) == 1 and u.shape[0] >= members * T, 'mlp_fused: attn u [rows, parts] fp32')
+            _need(nz_o.shift == fc.shift, 'mlp_fused: the attention c_proj noise rows must share member_shift')
+            _rows(nz_o.a, 512, torch.float32, 'attn a')
+            g.attn_u, g.ld_attn_u, g.attn_parts = u.data_ptr(), u.stride(0), u.shape[1]
+            g.attn_a, g.ld_attn_a = nz_o.a.data_ptr(), nz_o.a.stride(0)
     _lib.call('noise_mlp_fused', C.byref(g), _stream())
 
 

@@ -11,8 +11,8 @@ Per layer the engine runs (one launch each, all on the current stream):
   qkv_rope_gemm [q|k|v] = h Wqkv^T + s u a^T, then in the epilogue
                 q, k = bf16(norm(rot(.))); v = bf16(v + gate ve)
   attention     y = bf16(softmax_window(q k^T / 8) v); u_o = y.b_o per head
-  lowrank_gemm  x += y Wo^T + s u_o a_o^T
-  mlp_fused     x += bf16(relu(h Wfc^T + s u_fc a_fc^T)^2) Wmp^T + s u_mp a_mp^T with
+  mlp_fused     x += y Wo^T + s u_o a_o^T (the attention c_proj, in the prologue), then
+                x += bf16(relu(h Wfc^T + s u_fc a_fc^T)^2) Wmp^T + s u_mp a_mp^T with
                 h = bf16(norm x), u_fc = h.b_fc, u_mp = hid.b_mp: the hidden stays on chip;
                 its epilogue runs the next layer's mix_norm on the finished rows
 then the final norm + u_head (in the last MLP's epilogue), head_ce (bf16 head, soft-cap, CE) and
@@ -123,6 +123,9 @@ class Engine:
         # False runs the MLP as mix_norm + two lowrank_gemm launches through an HBM hidden
         # (kept to compare the two on the same inputs).
         self.fused_mlp = True
+        # With the fused MLP: True runs the attention c_proj (+ its rank-1 term and the residual
+        # add) in the MLP's prologue instead of as a GEMM launch of its own.
+        self.fuse_attn_proj = True
         # True runs every mix_norm inside the launch before it (the embedding for the first layer,
         # the fused MLP for the later ones and the final norm) instead of as launches of their own.
         self.fuse_next_norm = True
@@ -201,13 +204,16 @@ class Engine:
                             g(f'value_embeds.{i}.weight') if ve else None, idx_stride)
             K.window_attention(qkv16, y, members, T, wins[i], o.b if pert else None, shift,
                                uproj if pert else None)
-            r1 = K.rank1(sign, T, [o.a], [uproj], cfg.n_head, cfg.n_head, shift) if pert else None
-            K.lowrank_gemm(y, W.o[i], r1, _lib.EPI_ADD_F32, x)
+            fold = self.fused_mlp and self.fuse_attn_proj
+            if not fold:
+                r1 = K.rank1(sign, T, [o.a], [uproj], cfg.n_head, cfg.n_head, shift) if pert else None
+                K.lowrank_gemm(y, W.o[i], r1, _lib.EPI_ADD_F32, x)
             ev = self._mark()
             carried = self.fused_mlp and self.fuse_next_norm
             if self.fused_mlp:
                 K.mlp_fused(x, x, T, members, W.fc_packed[i], W.mp_packed[i], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
-                            sign, fc, mp, next_norm=mixing(i + 1) if carried else None)
+                            sign, fc, mp, next_norm=mixing(i + 1) if carried else None,
+                            attn=(y, W.o[i], uproj if pert else None, o) if fold else None)
             else:
                 K.mix_norm(x, h, T, sign, shift=shift, bs=(fc.b,) if pert else (), u=u1)
                 r1 = K.rank1(sign, T, [fc.a], [u1], 1, 1, shift) if pert else None

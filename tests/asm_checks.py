@@ -9,7 +9,14 @@ are checked here on the assembly it does emit:
 * `async_load_touches`: no instruction reads or writes the destination registers of a vector
   load before an `s_waitcnt vmcnt(N)` that covers the load (an inline-asm load's destination is
   written when the data lands, not when the asm statement ends; a register the compiler reuses
-  or copies in between is overwritten or read early).
+  or copies in between is overwritten or read early);
+* `mfma_result_touches`: no instruction other than the next MFMA of the same accumulation chain
+  (same destination, same C operand) reads or writes an MFMA's destination registers fewer than
+  12 wait states after it. 12 is what the compiler itself leaves after its own
+  v_mfma_f32_32x32x16_bf16 on gfx950 before reading the result (8 passes + 4); for an inline-asm
+  MFMA it leaves nothing, so a spill or copy it places right after one reads stale registers.
+  An intervening MFMA counts as 4 wait states (its issue waits for the matrix pipeline, which
+  the earlier 8-pass MFMA holds for longer than that).
 """
 import re
 import subprocess
@@ -67,6 +74,33 @@ def mfma_hazards(asm, need=2):
             waits += int(prev.split()[1]) + 1 if prev.startswith('s_nop') else 1
             if waits >= need:
                 break
+    return bad
+
+
+def mfma_result_touches(asm, need=12, mfma_waits=4):
+    ins = _instructions(asm)
+    bad = []
+    for i, line in enumerate(ins):
+        if not line.startswith('v_mfma'):
+            continue
+        dst = _regs(_operands(line)[0])
+        waits = 0
+        for nxt in ins[i + 1:]:
+            if waits >= need or nxt.startswith(('s_endpgm', 's_branch', 's_setpc')):
+                break
+            ops = _operands(nxt)
+            if nxt.startswith('v_mfma'):
+                d2, c2 = _regs(ops[0]), _regs(ops[3])
+                ab = _regs(ops[1]) | _regs(ops[2])
+                if ab & dst or ((d2 | c2) & dst and not (d2 == dst and c2 == dst)):
+                    bad.append((line, nxt))
+                    break
+                waits += mfma_waits
+                continue
+            if ops and set().union(*(_regs(o) for o in ops)) & dst:
+                bad.append((line, nxt))
+                break
+            waits += int(nxt.split()[1], 0) + 1 if nxt.startswith('s_nop') else 1
     return bad
 
 

@@ -1,7 +1,8 @@
 """The inline-asm kernels (proj.hip, mlp.hip, head.hip) checked on their gfx950 assembly, on the CPU: see
-tests/asm_checks.py for the two properties. A variant that uses none of its prefetched values
+tests/asm_checks.py for the three properties. A variant that uses none of its prefetched values
 (so that the compiler may reuse their registers while the loads are in flight) must fail the
-load check: the check sees the failure it exists for."""
+load check, and an asm MFMA whose result the compiler reads at once must fail the result check:
+each check sees the failure it exists for."""
 import shutil
 
 import pytest
@@ -19,6 +20,7 @@ def test_inline_asm_kernels_are_hazard_free(name, tmp_path):
     assert asm.count('v_mfma') > 0
     assert A.mfma_hazards(asm) == []
     assert A.async_load_touches(asm) == []
+    assert A.mfma_result_touches(asm) == []
 
 
 def test_load_check_catches_reused_destinations(tmp_path):
@@ -40,3 +42,21 @@ __global__ void k(const float* p, float* o, int n) {
 ''')
     asm = A.device_asm(src, tmp_path)
     assert A.async_load_touches(asm) != []
+
+
+def test_result_check_catches_early_reads(tmp_path):
+    # an asm MFMA followed at once by compiler code that reads its accumulator
+    src = tmp_path / 'early_read.hip'
+    src.write_text('''
+#include <hip/hip_runtime.h>
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__global__ void k(const bf16x8* a, float* o) {
+  floatx16 acc = {};
+  bf16x8 x = a[threadIdx.x];
+  __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, %0" : "+a"(acc) : "v"(x));
+  o[threadIdx.x] = acc[0] + acc[15];
+}
+''')
+    asm = A.device_asm(src, tmp_path)
+    assert A.mfma_result_touches(asm) != []

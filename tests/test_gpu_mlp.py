@@ -181,6 +181,88 @@ def test_mlp_fused_next_norm_matches_separate_mix_norm(device, T, members, shift
         torch.testing.assert_close(gf.cpu().double(), 2 * torch.sigmoid(z), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize('T,members,shift,pert,with_next', [
+    (256, 4, 1, True, False),
+    (100, 3, 0, True, True),      # ragged row blocks, and the next mix_norm in the same launch
+    (37, 5, 0, False, False),     # T < 128, unperturbed
+    (2048, 2, 1, True, True),
+])
+def test_mlp_fused_attention_proj_matches_separate_gemm(device, T, members, shift, pert, with_next):
+    """The attention c_proj run in the MLP prologue (attn=...) equals lowrank_gemm ADD_F32 (the same
+    c_proj as a GEMM launch) followed by mlp_fused: x + y Wo^T + s (sum of the 8 per-head dots)
+    a_o^T, then the MLP. The two add the same fp32 terms in another order, and h = bf16(norm x)
+    may round the other way where x differs in its last bit, so the bar is the MLP test's."""
+    g = torch.Generator().manual_seed(5000 + T + members)
+    w1, w2 = _weights(g)
+    M = members * T
+    rows = (members >> shift) + 1
+    x = torch.randn(M, D, generator=g)
+    y = (torch.randn(M, D, generator=g) * 0.5).to(torch.bfloat16)
+    wo = (torch.randn(D, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    u = torch.randn(M, 8, generator=g)
+    sign = torch.tensor([0.02 if j % 2 == 0 else -0.02 for j in range(members)], device=device)
+    nz = lambda w_a, w_b: NoiseRows(a=torch.randn(rows, w_a, generator=g).to(device),
+                                    b=torch.randn(rows, w_b, generator=g).to(device), shift=shift)
+    fc, pr, o = nz(F, D), nz(D, F), nz(D, D)
+    w1p, w2p = _packed(w1, w2, device)
+    s = sign if pert else None
+    flags = _lib.MLP_NORM | _lib.MLP_RESIDUAL
+    dy, dwo, du = y.to(device), wo.to(device), u.to(device)
+
+    def nxt(xs, h, uu):
+        return K.mix_norm_args(xs, h, T, s, shift=shift, bs=(o.b,) if pert else (), u=uu) if with_next else None
+
+    # separate: the c_proj GEMM into x, then the MLP
+    xr = x.to(device)
+    hr = torch.empty(M, D, dtype=torch.bfloat16, device=device)
+    ur = torch.empty(M, 1, device=device)
+    r1 = K.rank1(s, T, [o.a], [du], 8, 8, shift) if pert else None
+    K.lowrank_gemm(dy, dwo, r1, _lib.EPI_ADD_F32, xr)
+    K.mlp_fused(xr, xr, T, members, w1p, w2p, flags, s, fc, pr, next_norm=nxt(xr, hr, ur))
+    # fused
+    xf = x.to(device)
+    hf = torch.empty(M, D, dtype=torch.bfloat16, device=device)
+    uf = torch.empty(M, 1, device=device)
+    K.mlp_fused(xf, xf, T, members, w1p, w2p, flags, s, fc, pr, next_norm=nxt(xf, hf, uf),
+                attn=(dy, dwo, du if pert else None, o if pert else None))
+    torch.cuda.synchronize()
+    err = (xf.double() - xr.double()).abs()
+    scale = float(xr.abs().max())
+    print(f'T={T} members={members}: max |fused - separate| {float(err.max()):.3e} (max |x| {scale:.3e}), '
+          f'exact {float((err == 0).double().mean()):.4f}')
+    assert float(err.max()) <= 1e-2 * scale
+    assert float(err.square().mean().sqrt()) <= 1e-3 * float(xr.double().square().mean().sqrt())
+    if with_next:
+        hd = (hf.float() - hr.float()).abs()
+        assert (hd <= 2.0 ** -6 * hr.float().abs() + 1e-6).double().mean() >= 0.999
+
+
+@pytest.mark.parametrize('T,members,pert', [(256, 4, True), (100, 3, True), (37, 2, False)])
+def test_mlp_fused_attention_proj_alone(device, T, members, pert):
+    """With zero MLP weights and noise rows the fused launch is the attention c_proj alone:
+    x + y Wo^T + s (sum of the per-head dots) a_o^T, equal to lowrank_gemm ADD_F32 up to the order
+    of the fp32 additions."""
+    g = torch.Generator().manual_seed(6000 + T)
+    M = members * T
+    x = torch.randn(M, D, generator=g).to(device)
+    y = (torch.randn(M, D, generator=g) * 0.5).to(torch.bfloat16).to(device)
+    wo = (torch.randn(D, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(device)
+    u = torch.randn(M, 8, generator=g).to(device)
+    sign = torch.tensor([0.3 if j % 2 == 0 else -0.3 for j in range(members)], device=device)
+    o = NoiseRows(a=torch.randn(members, D, generator=g).to(device), b=torch.randn(members, D, generator=g).to(device),
+                  shift=0)
+    zeros = lambda w_a, w_b: NoiseRows(a=torch.zeros(members, w_a, device=device), b=torch.zeros(members, w_b, device=device),
+                                       shift=0)
+    w1p, w2p = _packed(torch.zeros(F, D), torch.zeros(D, F), device)
+    s = sign if pert else None
+    want = x.clone()
+    K.lowrank_gemm(y, wo, K.rank1(s, T, [o.a], [u], 8, 8, 0) if pert else None, _lib.EPI_ADD_F32, want)
+    got = x.clone()
+    K.mlp_fused(got, got, T, members, w1p, w2p, _lib.MLP_NORM | _lib.MLP_RESIDUAL, s, zeros(F, D), zeros(D, F),
+                attn=(y, wo, u if pert else None, o if pert else None))
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
 def test_mlp_fused_next_norm_rejects_a_mismatched_record(device):
     g = torch.Generator().manual_seed(3)
     w1p, w2p = _packed(*_weights(g), device)
