@@ -16,10 +16,11 @@ the rank-normalised fitness, the rank-1 gradient rebuild and an AdamW update of 
 `Eggroll.step`. Weights are the seeded initialisation; tokens are synthetic.
 
 Printed: one JSON line. `value` = members * tokens * steps / wall time of the timed steps (inputs
-resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (`mlp_fused`: norm,
-c_fc with its rank-1 term, relu^2, c_proj with its rank-1 term and the residual add in one launch,
-the hidden kept on chip, and the next layer's mix_norm on the finished rows): algorithmic MLP
-FLOPs per launch / its mean duration, timed live with HIP events on the launch stream.
+resident in HBM). `roofline` is for the dominant kernel, the fused relu^2 MLP (`mlp_fused`: the
+attention c_proj with its rank-1 term into the residual rows, then norm, c_fc with its rank-1
+term, relu^2, c_proj with its rank-1 term and the residual add in one launch, the hidden kept on
+chip, and the next layer's mix_norm on the finished rows): algorithmic FLOPs per launch / its
+mean duration, timed live with HIP events on the launch stream.
 `cpu_baseline` times the CPU oracle (oracle/model_ref.py, float32) on a bounded sample of the same
 workload on this host.
 """
@@ -38,10 +39,11 @@ ROOT = Path(__file__).resolve().parent
 TRAFFIC_FILE = ROOT / 'profiles' / 'mlp_fused_traffic.md'
 
 
-def mlp_flops(rows, d=512, f=2048):
+def mlp_flops(rows, d=512, f=2048, attn=True):
     """Algorithmic FLOPs of one fused-MLP launch over `rows` member-token rows: both GEMMs (2 d f
-    each) plus the two rank-1 terms (2 f + 2 d), per row."""
-    return rows * (4 * d * f + 2 * (d + f))
+    each) plus the two rank-1 terms (2 f + 2 d), per row; with `attn`, also the attention c_proj
+    the launch runs first (2 d d and its rank-1 term 2 d per row)."""
+    return rows * (4 * d * f + 2 * (d + f) + (2 * d * d + 2 * d if attn else 0))
 
 
 def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 1024, 1024, 2048) * 2):
@@ -109,11 +111,27 @@ def next_mix_norm(a, seed=1):
                            gate=a['gate'])
 
 
+def attention_proj(a, seed=2, parts=8):
+    """The attention c_proj operands the step folds into mlp_fused: y [M, 512] bf16 (the attention
+    output), w_o [512, 512] bf16, the per-head parts of y . b_o [M, 8] and the c_proj noise rows."""
+    from noise_amd.kernels import NoiseRows
+    x = a['x']
+    dev, M, rows, shift = x.device, x.shape[0], a['fc'].a.shape[0], a['fc'].shift
+    g = torch.Generator(device=dev).manual_seed(seed)
+    y = torch.randn(M, 512, device=dev, generator=g).to(torch.bfloat16)
+    w_o = (torch.randn(512, 512, device=dev, generator=g) / 512 ** 0.5).to(torch.bfloat16)
+    u = torch.randn(M, parts, device=dev, generator=g)
+    nz = NoiseRows(a=torch.randn(rows, 512, device=dev, generator=g), b=torch.randn(rows, 512, device=dev, generator=g),
+                   shift=shift)
+    return (y, w_o, u, nz)
+
+
 def probe_mlp(reps=3):
     """Counter-collection workload: `reps` copies of a 1 GiB fp32 buffer (1 GiB read + 1 GiB
     written per dispatch), then `reps` fused-MLP launches at the bench shape (512 members x 2048
-    tokens, pair-shared noise rows) as the step runs them: normed residual MLP with the next
-    layer's mix_norm (a value-embedding layer's) in the epilogue."""
+    tokens, pair-shared noise rows) as the step runs them: the attention c_proj into the residual
+    rows, then the normed residual MLP with the next layer's mix_norm (a value-embedding layer's)
+    in the epilogue."""
     import noise_amd  # noqa: F401  (loads the library)
     from noise_amd import _lib
     from noise_amd import kernels as K
@@ -126,12 +144,13 @@ def probe_mlp(reps=3):
     del src, dst
     a = mlp_inputs()
     nxt = next_mix_norm(a)
+    att = attention_proj(a)
     for _ in range(reps):
         K.mlp_fused(a['x'], a['x'], a['T'], a['members'], a['w_fc'], a['w_pr'], _lib.MLP_NORM | _lib.MLP_RESIDUAL,
-                    a['sign'], a['fc'], a['pr'], next_norm=nxt)
+                    a['sign'], a['fc'], a['pr'], next_norm=nxt, attn=att)
     torch.cuda.synchronize()
-    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused (with the next mix_norm) over {a["x"].shape[0]} rows',
-          flush=True)
+    print(f'probe-mlp: {reps} x copy 1 GiB, {reps} x mlp_fused (attention c_proj first, next mix_norm last) over '
+          f'{a["x"].shape[0]} rows', flush=True)
 
 
 def probe_step(members=512, T=2048):
@@ -498,7 +517,7 @@ def main():
 
     mlp_ms = sum(a.elapsed_time(b) for a, b, _ in probe) / len(probe)
     rows = probe[0][2]
-    flops = mlp_flops(rows)
+    flops = mlp_flops(rows, attn=es.engine.fused_mlp and es.engine.fuse_attn_proj)
     achieved = flops / (mlp_ms / 1e3) / 1e12
     members = 2 * pairs
     value = members * T * args.steps / elapsed
@@ -521,8 +540,9 @@ def main():
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
                      'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(),
-                     'kernel': 'mlp_fused: norm + c_fc + rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip, '
-                               "then the next layer's mix_norm (x0 mixing, norm, q/k/v dots, gate) in the epilogue",
+                     'kernel': 'mlp_fused: attention c_proj + rank-1 into the residual rows, then norm + c_fc + '
+                               'rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip, then the next '
+                               "layer's mix_norm (x0 mixing, norm, q/k/v dots, gate) in the epilogue",
                      'flops_per_launch': flops, 'rows_per_launch': rows, 'launch_ms': mlp_ms},
         'step_tflops': step_flops(members, T) / (elapsed / args.steps) / 1e12,
         'mean_loss': losses[-1],
