@@ -255,6 +255,18 @@ int noise_head_ce(const noise_head_t* args, void* stream);
 int noise_member_mean(const float* ce, int members, int T, float* out, void* stream);
 
 /* ---- EGGROLL update -------------------------------------------------------------------- */
+/* The perturbation rows of n pairs, gathered from the shared noise buffer (train/val/eggroll.py:
+ * 122-128, `Eggroll.noise`: buffer[offsets[name][directions] + arange(sum(shape))]): for every
+ * row d < n and parameter k < nparams, out[d * ld_out + starts[k] + i] = buffer[o + min(i,
+ * widths[k] - 1)] for i < widths[k] rounded up to 4, o = offsets[k * ld_offsets + directions[d]]
+ * (the int64 [nparams, >= pairs] table of `Eggroll.offsets`, eggroll.py:116-120). widths and
+ * starts are host arrays (nparams <= 64; starts 4-aligned, increasing, disjoint); out 16-byte
+ * aligned with ld_out % 4 == 0. A direction outside [0, pairs) or a slice outside the buffer gives
+ * NaN columns. */
+int noise_pair_gather(const float* buffer, int64_t buffer_len, const int64_t* offsets, int64_t ld_offsets,
+                      int64_t pairs, const int64_t* directions, int n, int nparams, const int* widths,
+                      const int* starts, float* out, int64_t ld_out, void* stream);
+
 /* f_j = L[2j+1] - L[2j], f /= (std(f) + 1e-8) (unbiased std), weight[i] = sum_{j = i mod pairs}
  * f_j (train/val/eggroll.py:151-154). n_losses even; weight [pairs]. Raises NOISE_ENONFINITE
  * through *status_out (device int) if a loss is not finite. */

@@ -108,6 +108,7 @@ SIGNATURES = {
     'noise_window_attention': [C.POINTER(Attention), P],
     'noise_head_ce': [C.POINTER(Head), P],
     'noise_member_mean': [P, INT, INT, P, P],
+    'noise_pair_gather': [P, I64, P, I64, I64, P, INT, INT, P, P, P, I64, P],
     'noise_fitness': [P, INT, INT, P, P, P],
     'noise_fitness_ranks': [P, INT, INT, P, P, P, P],
     'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P, I64, P],

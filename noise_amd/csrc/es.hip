@@ -9,6 +9,8 @@
 //   the same kernel reads materialised [pairs, out] noise or slices of one shared noise buffer.
 // * adamw (eggroll.py:164-167 with the torch.optim.AdamW of eggroll.py:205): one pass over a flat
 //   fp32 parameter buffer.
+// * pair_gather (eggroll.py:122-128, `Eggroll.noise`): the perturbation rows of a batch of pairs,
+//   every parameter's [out + in] slice of the shared noise buffer side by side in one block.
 #include <mutex>
 
 #include "common.h"
@@ -320,6 +322,59 @@ extern "C" int noise_es_gradient_noalloc(const float* w, int n, const float* a_b
   // The same kernels and split as noise_es_gradient with a workspace of `need` floats: every partial
   // tile the reduction reads is written by this call first, so the array needs no clearing.
   return noise_es_gradient(w, n, a_base, a_off, b_base, b_off, out, in, scale, accumulate, G, work, need, stream);
+}
+
+// One workgroup per (parameter k, pair row d): out[d, start_k + i] = buffer[o + min(i, w_k - 1)]
+// for i < pad4(w_k), o = offsets[k, directions[d]] -- a contiguous slice copied with coalesced
+// 4-byte reads (o is any index) into a 16-byte-aligned column range. Indices that fall outside
+// the buffer or the offsets table give NaN columns instead of a read.
+constexpr int PG_MAX = 64;
+struct PairLayout {
+  int widths[PG_MAX];
+  int starts[PG_MAX];
+};
+
+__global__ __launch_bounds__(256) void pair_gather_kernel(const float* __restrict__ buffer, int64_t buffer_len,
+                                                          const int64_t* __restrict__ offsets, int64_t ld_offsets,
+                                                          int64_t pairs, const int64_t* __restrict__ directions,
+                                                          const PairLayout lay, float* __restrict__ out,
+                                                          int64_t ld_out) {
+  const int k = blockIdx.x, d = blockIdx.y;
+  const int w = lay.widths[k], pw = (w + 3) & ~3;
+  const int64_t dir = directions[d];
+  const bool dir_ok = dir >= 0 && dir < pairs;
+  const int64_t o = dir_ok ? offsets[k * ld_offsets + dir] : -1;
+  const bool ok = dir_ok && o >= 0 && o + w <= buffer_len;
+  float* dst = out + (int64_t)d * ld_out + lay.starts[k];
+  for (int i = threadIdx.x; i < pw; i += 256) dst[i] = ok ? buffer[o + (i < w ? i : w - 1)] : __builtin_nanf("");
+}
+
+extern "C" int noise_pair_gather(const float* buffer, int64_t buffer_len, const int64_t* offsets,
+                                 int64_t ld_offsets, int64_t pairs, const int64_t* directions, int n,
+                                 int nparams, const int* widths, const int* starts, float* out, int64_t ld_out,
+                                 void* stream) {
+  NOISE_REQUIRE(buffer && offsets && directions && out && widths && starts, "pair_gather: null argument");
+  NOISE_REQUIRE(nparams > 0 && nparams <= PG_MAX, "pair_gather: nparams=%d must be in 1..%d", nparams, PG_MAX);
+  NOISE_REQUIRE(n >= 0 && n < 65536 && pairs > 0 && ld_offsets >= pairs && buffer_len > 0,
+                "pair_gather: bad sizes (n=%d pairs=%lld ld_offsets=%lld)", n, (long long)pairs,
+                (long long)ld_offsets);
+  NOISE_REQUIRE(((uintptr_t)out % 16) == 0 && ld_out % 4 == 0, "pair_gather: out rows must be 16-byte aligned");
+  PairLayout lay;
+  int64_t end = 0;
+  for (int k = 0; k < nparams; ++k) {
+    NOISE_REQUIRE(widths[k] > 0 && starts[k] >= end && starts[k] % 4 == 0,
+                  "pair_gather: parameter %d: width %d at column %d (columns must be 4-aligned, in order, disjoint)",
+                  k, widths[k], starts[k]);
+    end = (int64_t)starts[k] + ((widths[k] + 3) & ~3);
+    lay.widths[k] = widths[k];
+    lay.starts[k] = starts[k];
+  }
+  NOISE_REQUIRE(end <= ld_out, "pair_gather: the layout needs %lld columns, ld_out=%lld", (long long)end,
+                (long long)ld_out);
+  if (n == 0) return NOISE_OK;
+  pair_gather_kernel<<<dim3(nparams, n), 256, 0, (hipStream_t)stream>>>(buffer, buffer_len, offsets, ld_offsets, pairs,
+                                                                       directions, lay, out, ld_out);
+  return noise::check_launch("pair_gather");
 }
 
 extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,

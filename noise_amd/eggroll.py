@@ -75,22 +75,19 @@ class Eggroll:
             out[name] = rows.split(list(p.shape), dim=1) if p.dim() == 2 else rows
         return out
 
-    def _pair_rows(self, offsets, directions):
-        """name -> NoiseRows for the pairs `directions`: one gather of every parameter's [out + in]
-        block side by side (each block's first column a multiple of 4 floats, so every a and b view
-        starts 16-byte aligned), instead of one gather per parameter."""
+    def _pair_rows(self, table, directions):
+        """name -> NoiseRows for the pairs `directions`: one gather (noise_pair_gather) of every
+        parameter's [out + in] slice side by side (each block's first column a multiple of 4 floats,
+        so every a and b view starts 16-byte aligned), instead of one gather per parameter.
+        table: the int64 [params, pairs] stack of this step's offsets."""
         if self._layout is None:
             widths = [sum(s) for s in self.shapes.values()]
             padded = [-(-w // 4) * 4 for w in widths]
             starts = [sum(padded[:k]) for k in range(len(padded))]
-            # column c of the block reads buffer[offset of parameter pid[c] + local[c]]; the pad
-            # columns repeat their block's last element and are never read
-            pid = torch.cat([torch.full((p,), k, dtype=torch.int64) for k, p in enumerate(padded)])
-            local = torch.cat([torch.arange(p).clamp(max=w - 1) for w, p in zip(widths, padded)])
-            self._layout = (pid.to(self.device), local.to(self.device), starts)
-        pid, local, starts = self._layout
-        table = torch.stack([offsets[name] for name in self.shapes])[:, directions].t()   # [n, params]
-        block = self.buffer[table[:, pid] + local]
+            self._layout = (widths, starts, sum(padded))
+        widths, starts, total = self._layout
+        block = torch.empty(directions.numel(), total, dtype=torch.float32, device=self.device)
+        K.pair_gather(self.buffer, table, directions, widths, starts, block)
         out = {}
         for (name, shape), st in zip(self.shapes.items(), starts):
             if len(shape) == 2:
@@ -108,10 +105,11 @@ class Eggroll:
         losses = torch.empty(per_rank, device=self.device)
         sign = torch.tensor([self.sigma, -self.sigma], device=self.device).repeat(chunk)
         T = x.shape[1]
+        table = torch.stack([offsets[name] for name in self.shapes])  # [params, pairs]
         for start in range(self.rank * per_rank, (self.rank + 1) * per_rank, 2 * chunk):
             n = min(2 * chunk, (self.rank + 1) * per_rank - start)
             directions = torch.arange(start, start + n, 2, device=self.device) % (2 * pairs) // 2
-            nz = self._pair_rows(offsets, directions)
+            nz = self._pair_rows(table, directions)
             seq = start // per_seq
             lo = start - self.rank * per_rank
             self.engine.forward(self.weights, nz, sign[:n], x[seq].contiguous(), y[seq].contiguous(), T, n,

@@ -304,6 +304,24 @@ def cast_bf16(x, hi, lo=None):
     _lib.call('noise_cast_bf16', _ptr(x), x.numel(), _ptr(hi), _ptr(lo), _stream())
 
 
+def pair_gather(buffer, offsets, directions, widths, starts, out):
+    """out[d, starts[k] + i] = buffer[offsets[k, directions[d]] + min(i, widths[k] - 1)] for
+    i < widths[k] rounded up to 4: every parameter's noise slice of the pairs `directions`, side by
+    side (eggroll.py:122-128). offsets: int64 [params, pairs]; widths / starts: Python ints."""
+    _on_gpu(buffer, offsets, directions, out)
+    _need(buffer.dtype == torch.float32 and buffer.is_contiguous(), 'pair_gather: contiguous fp32 buffer')
+    _need(offsets.dtype == torch.int64 and offsets.dim() == 2 and offsets.stride(1) == 1 and
+          offsets.shape[0] == len(widths), 'pair_gather: offsets must be int64 [params, pairs] rows')
+    _need(directions.dtype == torch.int64 and directions.is_contiguous(), 'pair_gather: int64 directions')
+    _need(out.dtype == torch.float32 and out.dim() == 2 and out.stride(1) == 1 and
+          out.shape[0] >= directions.numel(), 'pair_gather: out must be fp32 [n, cols] rows')
+    n, k = directions.numel(), len(widths)
+    w = (C.c_int * k)(*widths)
+    st = (C.c_int * k)(*starts)
+    _lib.call('noise_pair_gather', _ptr(buffer), buffer.numel(), _ptr(offsets), offsets.stride(0), offsets.shape[1],
+              _ptr(directions), n, k, w, st, _ptr(out), out.stride(0), _stream())
+
+
 def fitness(losses, pairs, weight, status, mode='zscore', ranked=None):
     """weight [pairs] from antithetic losses: the reference z-score (mode 'zscore') or centred ranks
     ('ranks'; `ranked` [len(losses) / 2] receives the per-pair values)."""

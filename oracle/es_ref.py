@@ -11,8 +11,40 @@ Restates `Eggroll.step` after the population forward (train/val/eggroll.py:151-1
                     corrections, eps outside the square root), the optimizer eggroll.py:205 builds;
 * `centred_ranks`-- the optional rank-normalised fitness: ranks from a stable argsort, mapped to
                     rank / (n - 1) - 0.5 (a mode of this build, not of the reference).
+
+and the perturbation source the update and the forward read (eggroll.py:110-128):
+* `noise_buffer` -- the fixed N(0, 1) buffer, drawn once from a generator seeded with `seed`
+                    (eggroll.py:113);
+* `offsets`      -- per step, one generator seeded with 1,000,003 * seed + step, and per
+                    parameter in named_parameters() order one randint(0, size - sum(shape)) draw of
+                    `pairs` offsets (eggroll.py:116-120);
+* `noise`        -- per parameter the rows buffer[offset + arange(sum(shape))] of the chosen pairs,
+                    split into (a [n, out], b [n, in]) for a matrix or embedding, eps [n, L] for a
+                    vector (eggroll.py:122-128).
+These three are pinned by the reference's own draws on the CPU (tests/golden/golden_noise.npz).
 """
 import torch
+
+
+def noise_buffer(size, seed, device='cpu'):
+    return torch.randn(size, device=device, generator=torch.Generator(device).manual_seed(seed))
+
+
+def offsets(shapes, pairs, step, seed, size, device='cpu'):
+    """name -> int64 [pairs] offsets of `step`; `shapes` in named_parameters() order."""
+    g = torch.Generator(device).manual_seed(1_000_003 * seed + step)
+    return {name: torch.randint(0, size - sum(shape), (pairs,), device=device, generator=g)
+            for name, shape in shapes.items()}
+
+
+def noise(buffer, offs, shapes, directions):
+    """name -> (a, b) or eps for the pairs `directions` (an int64 tensor of pair indices)."""
+    out = {}
+    for name, shape in shapes.items():
+        width = sum(shape)
+        rows = buffer[offs[name][directions, None] + torch.arange(width, device=buffer.device)]
+        out[name] = (rows[:, :shape[0]], rows[:, shape[0]:]) if len(shape) == 2 else rows
+    return out
 
 
 def fitness(losses, pairs):

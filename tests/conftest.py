@@ -37,6 +37,13 @@ def golden_scoring():
 
 
 @pytest.fixture(scope='session')
+def golden_noise():
+    """The reference's perturbation source as drawn on the CPU (tests/golden/make_golden.py --noise)."""
+    with np.load(GOLDEN / 'golden_noise.npz', allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope='session')
 def golden_json():
     import json
     return json.loads((GOLDEN / 'golden.json').read_text())

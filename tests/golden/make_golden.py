@@ -174,11 +174,50 @@ def scoring_losses(ref_root):
     print(json.dumps({k: [float(v.mean()), float(v.min()), float(v.max())] for k, v in arrays.items()}))
 
 
+NOISE_PAIRS = 4
+NOISE_STEPS = (1, 2)
+NOISE_DIRECTIONS = (0, 3, 3)
+NOISE_PARAMS = ('resid_lambdas', 'transformer.wte.weight', 'transformer.h.0.attn.c_q.weight',
+                'transformer.h.1.attn.ve_gate.weight', 'transformer.h.7.mlp.c_proj.weight', 'lm_head.weight')
+
+
+def noise_source(ref_root):
+    """golden_noise.npz: the reference's perturbation source as its own code draws it on the CPU
+    (train/val/eggroll.py:110-128): the edges of the 2^28-float buffer, `Eggroll.offsets` of two
+    steps for 4 pairs (one int64 row per parameter, named_parameters() order), and `Eggroll.noise`
+    of pairs (0, 3, 3) for a few parameters. Generator draws have no closed form, so these pin the
+    seeds, the draw order, the offset ranges and the slicing."""
+    sys.path.insert(0, str(ref_root))
+    from train.val.eggroll import Eggroll, make_model
+
+    torch.set_grad_enabled(False)
+    model = make_model(torch.device('cpu'), 0)
+    es = Eggroll(model, NOISE_PAIRS)
+    arrays = {'buffer_head': es.buffer[:64].numpy(), 'buffer_tail': es.buffer[-64:].numpy(),
+              'buffer_size': np.array(es.buffer.numel())}
+    names = list(es.params)
+    for step in NOISE_STEPS:
+        offs = es.offsets(step)
+        arrays[f'step{step}/offsets'] = torch.stack([offs[n] for n in names]).numpy()
+        if step == NOISE_STEPS[0]:
+            nz = es.noise(offs, torch.tensor(NOISE_DIRECTIONS))
+            for n in NOISE_PARAMS:
+                v = nz[n]
+                if isinstance(v, (tuple, list)):
+                    arrays[f'noise/{n}/a'], arrays[f'noise/{n}/b'] = v[0].numpy(), v[1].numpy()
+                else:
+                    arrays[f'noise/{n}/eps'] = v.numpy()
+    np.savez_compressed(HERE / 'golden_noise.npz', **arrays)
+    print(json.dumps({k: list(v.shape) for k, v in arrays.items()}))
+
+
 if __name__ == '__main__':
     root = Path(sys.argv[1] if len(sys.argv) > 1 else '/root/reference')
     if '--autocast' in sys.argv:
         autocast_losses(root)
     elif '--scoring' in sys.argv:
         scoring_losses(root)
+    elif '--noise' in sys.argv:
+        noise_source(root)
     else:
         main(root)

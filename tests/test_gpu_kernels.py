@@ -386,6 +386,72 @@ def test_cast_bf16_round_to_nearest_even(device):
     assert torch.equal(lo.cpu(), (x - x.to(torch.bfloat16).float()).to(torch.bfloat16))
 
 
+def _gather_layout(shapes):
+    widths = [sum(s) for s in shapes.values()]
+    padded = [-(-w // 4) * 4 for w in widths]
+    return widths, [sum(padded[:k]) for k in range(len(padded))], sum(padded)
+
+
+def test_pair_gather(device):
+    """noise_pair_gather against torch indexing and the oracle's `noise` (eggroll.py:122-128), bit
+    for bit, on the model's 60 parameter slices: repeated and out-of-order pairs, the last
+    admissible offset, the pad columns (the slice's last value), and NaN for a pair index outside
+    the table or a slice past the buffer's end."""
+    from noise_amd.config import param_shapes
+    from oracle import es_ref
+    shapes = dict(param_shapes())
+    widths, starts, total = _gather_layout(shapes)
+    size, pairs = 1 << 20, 9
+    g = _gen(21)
+    buf = torch.randn(size, generator=g).to(device)
+    offs = {n: torch.randint(0, size - w, (pairs,), generator=g) for n, w in zip(shapes, widths)}
+    offs['lm_head.weight'][2] = size - widths[list(shapes).index('lm_head.weight')]  # ends at the last float
+    table = torch.stack(list(offs.values())).to(device)
+    dirs = torch.tensor([0, 8, 2, 2, 5], device=device)
+    out = torch.full((dirs.numel(), total + 8), 7.0, device=device)
+    nk.pair_gather(buf, table, dirs, widths, starts, out)
+    ref = es_ref.noise(buf.cpu(), offs, shapes, dirs.cpu())
+    got = out.cpu()
+    for (name, shape), st, w in zip(shapes.items(), starts, widths):
+        v = ref[name]
+        want = torch.cat(v, 1) if isinstance(v, tuple) else v
+        assert torch.equal(got[:, st:st + w], want), name
+        pw = -(-w // 4) * 4
+        assert torch.equal(got[:, st + w:st + pw], want[:, -1:].expand(-1, pw - w)), name  # pad columns
+    assert (got[:, total:] == 7.0).all()  # nothing past the layout
+    # a pair index outside [0, pairs), a slice past the buffer: NaN rows / columns, no read
+    bad = table.clone()
+    bad[0, 1] = size - 4  # resid_lambdas (8 wide) would end 4 floats past the buffer
+    dirs2 = torch.tensor([1, pairs, -1], device=device)
+    out2 = torch.zeros(3, total, device=device)
+    nk.pair_gather(buf, bad, dirs2, widths, starts, out2)
+    o2 = out2.cpu()
+    assert torch.isnan(o2[0, :8]).all() and not torch.isnan(o2[0, 8:]).any()
+    assert torch.isnan(o2[1:]).all()
+    with pytest.raises(ValueError):
+        nk.pair_gather(buf, table, dirs, widths, [s + 1 for s in starts], out)  # misaligned columns
+
+
+def test_pair_rows_match_noise(device):
+    """Eggroll's per-chunk gather (the HIP kernel) against Eggroll.noise, the reference's slicing,
+    on the device buffer and the device generator's offsets of a step."""
+    from noise_amd import make_model
+    from noise_amd.eggroll import Eggroll
+    model = make_model(device, 0)
+    es = Eggroll(model, 6)
+    offsets = es.offsets(3)
+    table = torch.stack([offsets[n] for n in es.shapes])
+    dirs = torch.tensor([5, 0, 3, 3, 1], device=device)
+    rows = es._pair_rows(table, dirs)
+    ref = es.noise(offsets, dirs)
+    for name, v in ref.items():
+        r = rows[name]
+        if isinstance(v, (tuple, list)):
+            assert torch.equal(r.a, v[0]) and torch.equal(r.b, v[1]), name
+        else:
+            assert torch.equal(r.eps, v), name
+
+
 def test_fitness_gradient_adamw(device):
     from oracle import es_ref
     g = _gen(9)
