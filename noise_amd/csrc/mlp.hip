@@ -52,7 +52,7 @@ constexpr float RMS_EPS = 1.1920928955078125e-07f;  // float32 machine epsilon (
 #define MLP_NTSTORE 0  // output rows stored past L2 (non-temporal)
 #endif
 #ifndef MLP_LSTRIDE
-#define MLP_LSTRIDE 1  // MFMAs between two loads of the next stage
+#define MLP_LSTRIDE 2  // MFMAs between two loads of the next stage (measured: 2 is 1.5% faster than 1)
 #endif
 
 static_assert(LDS_NEXT_BYTES <= 160 * 1024, "LDS budget");
@@ -143,7 +143,8 @@ struct StepOps {
 // One step of the chunk pipeline. FCP: the c_fc MFMAs of chunk `cf` into fc[FB]; PRJ: turn
 // fc[1 - FB] (chunk cf - 1) into the c_proj operand (rank-1 term, relu^2, bf16, u_proj dots) and
 // run its 32 c_proj MFMAs. Stage buffer `buf` holds c_fc rows of chunk cf and c_proj chunk cf - 1;
-// the loads of the next stage (LFC, LMP) are issued one per MFMA during the first 16. Every MFMA is
+// the 16 loads of the next stage (LFC, LMP) are issued one every MLP_LSTRIDE MFMAs from the
+// step's first. Every MFMA is
 // inline asm so that the c_fc accumulators stay in VGPRs and the c_proj ones in AGPRs; the hazards
 // the compiler then cannot see are covered explicitly: 2 wait states between the VALU writing the
 // c_proj operand and its first MFMA, and 24 after a chunk's last MFMA before VALU reads its result.
