@@ -1,4 +1,4 @@
-"""The inline-asm kernels (proj.hip, mlp.hip, head.hip) checked on their gfx950 assembly, on the CPU: see
+"""The kernels with inline asm (their own, or the MFMA tiles of mma_tile.h) checked on their gfx950 assembly, on the CPU: see
 tests/asm_checks.py for the three properties. A variant that uses none of its prefetched values
 (so that the compiler may reuse their registers while the loads are in flight) must fail the
 load check, and an asm MFMA whose result the compiler reads at once must fail the result check:
@@ -14,7 +14,7 @@ pytestmark = pytest.mark.skipif(shutil.which('hipcc') is None and not (B.Path('/
                                 reason='hipcc not available')
 
 
-@pytest.mark.parametrize('name', ['proj', 'mlp', 'head'])
+@pytest.mark.parametrize('name', ['proj', 'mlp', 'head', 'attention', 'chain', 'gemm'])
 def test_inline_asm_kernels_are_hazard_free(name, tmp_path):
     asm = A.device_asm(B.CSRC / f'{name}.hip', tmp_path)
     assert asm.count('v_mfma') > 0
