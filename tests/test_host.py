@@ -93,6 +93,98 @@ def test_argument_errors_raise_before_launch():
     assert lib.noise_es_gradient_work(0, 70, 90) == 0
 
 
+def _rejects(st, match):
+    assert st == _lib.NOISE_EINVAL
+    with pytest.raises(ValueError, match=match):
+        _lib.check(st)
+
+
+def test_step_entry_points_reject_bad_arguments():
+    """Every entry point of the population step validates its arguments on the host: each call
+    here is either refused before any device call or an empty batch that returns at once (the
+    pointers are placeholders that no call dereferences)."""
+    lib = _lib.load()
+    fake, odd = 256, 264  # 16-byte aligned; 8-byte but not 16-byte aligned
+
+    head = _lib.Head(h=fake, w_hi=fake, M=1024, V=100, T=256, targets=fake, targets_stride=256, ce=fake,
+                     ignore_index=-1)
+    _rejects(lib.noise_head_ce(C.byref(head), None), 'multiple of 256')
+    head.V, head.ignore_index = 4096, 5
+    _rejects(lib.noise_head_ce(C.byref(head), None), 'class index')
+    head.ignore_index, head.h = -1, odd
+    _rejects(lib.noise_head_ce(C.byref(head), None), '16-byte aligned')
+    head.h, head.sign = fake, fake
+    _rejects(lib.noise_head_ce(C.byref(head), None), 'perturbation needs')
+    head.sign, head.M = None, 0
+    assert lib.noise_head_ce(C.byref(head), None) == _lib.NOISE_OK
+
+    att = _lib.Attention(qkv=fake, ldqkv=1536, y=fake, members=2, T=256, heads=4, window=1024, scale=0.125)
+    _rejects(lib.noise_window_attention(C.byref(att), None), 'heads == 8')
+    att.heads, att.scale = 8, 0.5
+    _rejects(lib.noise_window_attention(C.byref(att), None), 'scale')
+    att.scale, att.ldqkv = 0.125, 1540
+    _rejects(lib.noise_window_attention(C.byref(att), None), 'ldqkv')
+    att.ldqkv, att.moments = 1536, fake
+    _rejects(lib.noise_window_attention(C.byref(att), None), 'scratch')
+    att.moments, att.members = None, 0
+    assert lib.noise_window_attention(C.byref(att), None) == _lib.NOISE_OK
+
+    mlp = _lib.Mlp(in_=fake, ld_in=512, member_stride_in=512 * 256, out=fake, ld_out=512,
+                   member_stride_out=512 * 256, T=256, members=2, flags=8, w_fc=fake, w_proj=fake)
+    _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'unknown flags')
+    mlp.flags, mlp.in_ = 0, odd
+    _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'aligned')
+    mlp.in_, mlp.members = fake, 0
+    assert lib.noise_mlp_fused(C.byref(mlp), None) == _lib.NOISE_OK
+    _rejects(lib.noise_mlp_pack(None, 0, None, 0, fake, None, None), 'c_fc needs')
+    assert lib.noise_mlp_pack(None, 0, None, 0, None, None, None) == _lib.NOISE_OK
+
+    # pair_gather: two parameters of 512 and 100 floats per row, laid out at columns 0 and 512
+    # (the second padded to 104), so a row needs 616 columns.
+    widths = (C.c_int * 2)(512, 100)
+
+    def gather(starts, n=4, nparams=2, out=fake, ld_out=616):
+        return lib.noise_pair_gather(fake, 1 << 28, fake, 8, 8, fake, n, nparams, widths,
+                                     (C.c_int * 2)(*starts), out, ld_out, None)
+
+    _rejects(gather((0, 512), nparams=0), 'nparams')
+    _rejects(gather((0, 514)), 'pair_gather')      # a start that is not a multiple of 4
+    _rejects(gather((0, 256)), 'pair_gather')      # overlapping slices
+    _rejects(gather((0, 512), ld_out=600), 'columns')
+    _rejects(gather((0, 512), out=odd), '16-byte')
+    assert gather((0, 512), n=0) == _lib.NOISE_OK
+
+    _rejects(lib.noise_fitness_ranks(fake, 7, 3, fake, fake, None, None), 'even')
+    _rejects(lib.noise_member_mean(fake, 4, 0, fake, None), 'member_mean')
+    assert lib.noise_member_mean(fake, 0, 256, fake, None) == _lib.NOISE_OK
+    _rejects(lib.noise_cast_bf16(fake + 4, 64, fake, None, None), 'cast_bf16')
+    assert lib.noise_cast_bf16(fake, 0, fake, None, None) == _lib.NOISE_OK
+
+    mix = _lib.MixNorm(x=fake, h=fake, M=512, T=256, nb=4)
+    _rejects(lib.noise_mix_norm(C.byref(mix), None), 'nb=4')
+    mix.nb, mix.u, mix.ldb, mix.ldu = 1, fake, 512, 1
+    _rejects(lib.noise_mix_norm(C.byref(mix), None), r'null b\[0\]')
+    mix.nb, mix.x0 = 0, fake
+    _rejects(lib.noise_mix_norm(C.byref(mix), None), 'lambda scalars')
+    mix.x0, mix.M = None, 0
+    assert lib.noise_mix_norm(C.byref(mix), None) == _lib.NOISE_OK
+    _rejects(lib.noise_embed_mix_norm(fake, 512, 4096, 512, fake, 256, 256, 2, None, None, 0, None, 0, 0, fake,
+                                      None, None), 'null mix_norm')
+
+    rope = _lib.Rope(qkv=fake, out=fake, M=512, T=256, cos=fake, sin=fake, gate=fake)
+    _rejects(lib.noise_rope_norm_ve(C.byref(rope), None), 'gate needs')
+    rope.gate = None
+    _rejects(lib.noise_qkv_rope_gemm(fake, 512, fake, 512, 1024, 512, None, C.byref(rope), None), 'must equal')
+    rope.M = 0
+    assert lib.noise_rope_norm_ve(C.byref(rope), None) == _lib.NOISE_OK
+
+    # The allocation-free gradient refuses a split that would not fit its fixed array.
+    need = lib.noise_es_gradient_work(1536, 4096, 768)
+    assert need > lib.noise_es_gradient_noalloc_capacity()
+    _rejects(lib.noise_es_gradient_noalloc(fake, 1536, fake, fake, fake, fake, 4096, 768, -1.0, 0, fake, None),
+             'beyond the fixed')
+
+
 def test_state_dict_strict_round_trip():
     a = noise_amd.make_model('cpu', 0)
     sd = a.state_dict()
