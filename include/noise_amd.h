@@ -71,7 +71,8 @@ int noise_lowrank_gemm(const uint16_t* A, int64_t lda, const uint16_t* W, int64_
 typedef struct {
   const float* in;           /* fp32 [*, 512]: row t of member p at in + p*member_stride_in + t*ld_in */
   int64_t ld_in, member_stride_in; /* member_stride_in 0: one set of rows shared by every member */
-  float* out;                /* fp32 [*, 512], indexed alike with ld_out / member_stride_out; may be in */
+  float* out;                /* fp32 [*, 512], indexed alike with ld_out / member_stride_out; may be in
+                                (then with the same strides); members' rows must not overlap */
   int64_t ld_out, member_stride_out;
   int T, members, flags;
   const uint16_t* w_fc;      /* mlp.c_fc.weight as packed by noise_mlp_pack */

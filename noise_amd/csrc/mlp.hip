@@ -812,6 +812,13 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
                 "mlp_fused: rows need ld >= 512 with ld_in and member_stride_in multiples of 4");
   NOISE_REQUIRE(((uintptr_t)g.in % 16) == 0 && ((uintptr_t)g.w_fc % 16) == 0 && ((uintptr_t)g.w_proj % 16) == 0,
                 "mlp_fused: in, w_fc and w_proj must be 16-byte aligned");
+  // Every output row has one writer, and a launch that overwrites its input does so row for row
+  // (each workgroup reads its rows before it writes them).
+  NOISE_REQUIRE(g.members <= 1 || g.member_stride_out >= (int64_t)g.T * g.ld_out,
+                "mlp_fused: members' output rows overlap (member_stride_out %lld < T * ld_out)",
+                (long long)g.member_stride_out);
+  NOISE_REQUIRE(g.in != g.out || (g.ld_in == g.ld_out && g.member_stride_in == g.member_stride_out),
+                "mlp_fused: in-place (out == in) needs equal row and member strides");
   if (g.sign) {
     NOISE_REQUIRE(g.a_fc && g.b_fc && g.a_proj && g.b_proj, "mlp_fused: perturbation needs a/b of both matrices");
     NOISE_REQUIRE(g.member_shift >= 0 && g.member_shift < 31, "mlp_fused: bad member_shift");

@@ -14,10 +14,13 @@ This module computes the same quantity with its own plan:
   device in float64, and reads one number back per rank; ranks combine their sums with one
   all_reduce. A non-finite score raises FloatingPointError.
 
-Arithmetic: the forward keeps an fp32 residual stream with bf16 GEMM operands and an
-fp32-accurate head. The reference scores in a bf16 stream under autocast; over 8192 tokens the
+Arithmetic: the forward keeps an fp32 residual stream with bf16 GEMM operands, and the head's
+product takes the bf16 weight as the reference's autocast does (the fp32 soft cap and
+log-sum-exp follow it). The reference scores in a bf16 stream under autocast; over 8192 tokens the
 two differ by 2e-4 +- 1.7e-4 on perturbed weights and 3e-6 at initialisation, the per-token
-scatter (sd 0.015) averaging out over the 1.1M validation predictions.
+scatter (sd 0.015) averaging out over the 1.1M validation predictions. A target of -1 scores 0,
+as in GPT.forward's cross-entropy (ignore_index=-1, utils/model.py:206-209), and still counts in
+the denominator, which is every prediction of the split (utils/eval.py:47-48).
 
     python -m noise_amd.evaluate CHECKPOINT [--data-dir DIR] [--rows-per-launch N]
 """
@@ -33,7 +36,7 @@ import torch
 from torch import distributed as dist
 
 from .config import GPTConfig
-from .model import GPT
+from .model import GPT, IGNORE
 from .population import clean_loss
 
 ROW_TOKENS = 2049                 # 2048 predictions per row
@@ -105,7 +108,8 @@ def row_loss_sums(model, tokens, rows_per_launch=16):
     sums = torch.zeros(tokens.shape[0], dtype=torch.float64, device=device)
     for lo in range(0, tokens.shape[0], rows_per_launch):
         block = tokens[lo:lo + rows_per_launch].to(device, non_blocking=True)
-        ce = clean_loss(params, block[:, :-1], block[:, 1:], model.config, batch_chunk=rows_per_launch)
+        ce = clean_loss(params, block[:, :-1], block[:, 1:], model.config, batch_chunk=rows_per_launch,
+                        ignore_index=IGNORE)
         sums[lo:lo + block.shape[0]] = ce.sum(1, dtype=torch.float64)
     return sums
 

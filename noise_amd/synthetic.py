@@ -52,9 +52,10 @@ def antithetic(noise, sigma):
 
 
 def hadamard(d, dtype=torch.float32):
-    """The Sylvester Hadamard matrix of order d (a power of two), entries +-1."""
-    if d & (d - 1):
-        raise ValueError(f'Orthogonal draws need a power-of-two width, not {d}.')
+    """H_d by Sylvester's doubling H_2n = [[H_n, H_n], [H_n, -H_n]] from H_1 = [1]: d x d, +-1
+    entries, rows mutually orthogonal. d must be a power of two."""
+    if d < 1 or d & (d - 1):
+        raise ValueError(f'hadamard: Sylvester doubling gives orders 1, 2, 4, ...; got {d}')
     H = torch.ones(1, 1, dtype=dtype)
     while H.shape[0] < d:
         H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)

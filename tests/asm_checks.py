@@ -10,6 +10,11 @@ are checked here on the assembly it does emit:
   load before an `s_waitcnt vmcnt(N)` that covers the load (an inline-asm load's destination is
   written when the data lands, not when the asm statement ends; a register the compiler reuses
   or copies in between is overwritten or read early);
+* `lds_load_touches`: the same for LDS reads (`ds_read*`), against the `s_waitcnt lgkmcnt(N)` that
+  covers them: several kernels issue fragment reads as inline asm and wait for them with hand-counted
+  lgkmcnt values, which rests on the same property. LDS operations complete in issue order, scalar
+  memory loads in any order, so a wait covers a read when N is at most the number of LDS
+  operations issued after it;
 * `mfma_result_touches`: no instruction other than the next MFMA of the same accumulation chain
   (same destination, same C operand) reads or writes an MFMA's destination registers fewer than
   12 wait states after it. 12 is what the compiler itself leaves after its own
@@ -127,3 +132,58 @@ def async_load_touches(asm):
             if re.match(r'(global_|buffer_|flat_|scratch_)(load|store|atomic)', nxt):
                 later += 1
     return bad
+
+
+def lds_load_touches(asm):
+    ins = _instructions(asm)
+    bad = []
+    for i, line in enumerate(ins):
+        if not line.startswith('ds_read'):
+            continue
+        dst = _regs(_operands(line)[0])
+        if not dst:
+            continue
+        later = 0  # LDS operations issued after this read
+        for nxt in ins[i + 1:]:
+            m = re.match(r's_waitcnt\s.*lgkmcnt\((\d+)\)', nxt)
+            if (m and int(m.group(1)) <= later) or re.match(r's_waitcnt\s+0\s*$', nxt):
+                break
+            if nxt.startswith(('s_endpgm', 's_branch', 's_setpc')):
+                break
+            ops = _operands(nxt)
+            if ops and set().union(*(_regs(o) for o in ops)) & dst:
+                bad.append((line, nxt))
+                break
+            if nxt.startswith('ds_'):
+                later += 1
+    return bad
+
+
+def kernel_spills(asm):
+    """{kernel symbol: .vgpr_spill_count} from the code object metadata."""
+    names = re.findall(r'\.name:\s+(_Z\S+)', asm)
+    spills = [int(v) for v in re.findall(r'\.vgpr_spill_count:\s+(\d+)', asm)]
+    return dict(zip(names, spills))
+
+
+def loop_scratch(asm):
+    """(loop headers seen, [(kernel, block, instruction)]): scratch-memory (spill) instructions in
+    basic blocks that belong to a loop, as the compiler annotates each block label ('Loop Header',
+    'in Loop: Header=...', 'Parent Loop ...')."""
+    bad, loops = [], 0
+    for m in re.finditer(r'^(_Z\S+):(?:[ \t]*;[^\n]*)?$(.*?)^\.Lfunc_end\d+:', asm, re.M | re.S):
+        kernel, body = m.group(1), m.group(2).splitlines()
+        in_loop, block = False, 'entry'
+        for i, line in enumerate(body):
+            lab = re.match(r'^(\.LBB\d+_\d+:|; %bb\.\d+:)', line)
+            if lab:
+                block = lab.group(1)
+                notes = [line] + [body[j] for j in range(i + 1, min(i + 4, len(body)))
+                                  if re.match(r'^\s+;', body[j])]
+                text = ' '.join(notes)
+                in_loop = 'Loop' in text
+                loops += 'Loop Header' in text
+                continue
+            if in_loop and re.match(r'\s*scratch_', line):
+                bad.append((kernel, block, line.strip()))
+    return loops, bad

@@ -44,6 +44,14 @@ def golden_noise():
 
 
 @pytest.fixture(scope='session')
+def golden_sensitive_small():
+    """The reference's population losses on the sensitive weights at sigma = 1e-3, in float32 and
+    under bf16 autocast (tests/golden/make_golden.py --sensitive-small)."""
+    with np.load(GOLDEN / 'golden_sensitive_small.npz', allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope='session')
 def golden_json():
     import json
     return json.loads((GOLDEN / 'golden.json').read_text())

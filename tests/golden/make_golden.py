@@ -3,6 +3,7 @@
 Run once, in the build container only (the reference is not present on GPU machines):
 
     python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference --autocast | --scoring | --noise | --sensitive-small
 
 The reference has no tests, fixtures or known-answer vectors, so nothing else pins its
 `population_loss` *as written* (train/val/eggroll.py:66-103), its seeded initialisation
@@ -26,6 +27,9 @@ from noise_amd.synthetic import antithetic, pair_noise, sequence  # noqa: E402
 
 CONFIG0 = dict(length=256, pairs=4, sigma=1e-3, token_seed=0, noise_seed=1)
 SENSITIVE = dict(length=128, pairs=2, sigma=2e-2, token_seed=3, noise_seed=4, weight_seed=5)
+# The sensitive weights at the configs' sigma: antithetic differences of order sigma, losses far
+# from the chaotic regime of sigma = 0.02.
+SENSITIVE_SMALL = dict(length=256, pairs=4, sigma=1e-3, token_seed=6, noise_seed=7, weight_seed=5)
 
 
 def sensitive_weights(params, seed):
@@ -174,6 +178,29 @@ def scoring_losses(ref_root):
     print(json.dumps({k: [float(v.mean()), float(v.min()), float(v.max())] for k, v in arrays.items()}))
 
 
+def sensitive_small_sigma(ref_root):
+    """golden_sensitive_small.npz: the reference's population_loss on the sensitive weights (O(1)
+    logits, open gates) at sigma = 1e-3, once in float32 and once under bf16 autocast (the
+    trainer's arithmetic, train/val/eggroll.py:144-145). Their distance is the envelope of a
+    correct bf16 evaluation at the sigma the configs use."""
+    sys.path.insert(0, str(ref_root))
+    from train.val.eggroll import make_model, population_loss
+
+    torch.set_grad_enabled(False)
+    model = make_model(torch.device('cpu'), 0)
+    c = SENSITIVE_SMALL
+    p = sensitive_weights(dict(model.named_parameters()), c['weight_seed'])
+    idx, targets = sequence(c['length'], seed=c['token_seed'])
+    noise, sign = antithetic(pair_noise(c['pairs'], seed=c['noise_seed']), c['sigma'])
+    arrays = {'idx': idx.numpy(), 'targets': targets.numpy(),
+              'losses': population_loss(model, p, noise, sign, idx, targets).numpy()}
+    with torch.autocast('cpu', dtype=torch.bfloat16):
+        arrays['losses_autocast'] = population_loss(model, p, noise, sign, idx, targets).float().numpy()
+    np.savez_compressed(HERE / 'golden_sensitive_small.npz', **arrays)
+    print(json.dumps(dict(c, losses=[float(v) for v in arrays['losses']],
+                          losses_autocast=[float(v) for v in arrays['losses_autocast']])))
+
+
 NOISE_PAIRS = 4
 NOISE_STEPS = (1, 2)
 NOISE_DIRECTIONS = (0, 3, 3)
@@ -219,5 +246,7 @@ if __name__ == '__main__':
         scoring_losses(root)
     elif '--noise' in sys.argv:
         noise_source(root)
+    elif '--sensitive-small' in sys.argv:
+        sensitive_small_sigma(root)
     else:
         main(root)

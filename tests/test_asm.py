@@ -20,7 +20,30 @@ def test_inline_asm_kernels_are_hazard_free(name, tmp_path):
     assert asm.count('v_mfma') > 0
     assert A.mfma_hazards(asm) == []
     assert A.async_load_touches(asm) == []
+    assert A.lds_load_touches(asm) == []
     assert A.mfma_result_touches(asm) == []
+
+
+# Spill budgets (.vgpr_spill_count) of the kernels the population step launches: the fused MLP spills
+# a few prologue/epilogue values (its waves hold 512 registers), the others none or one.
+SPILL_BUDGET = {'mlp_fused_kernel': 48, 'qkv_proj_kernel': 0, 'window_attention_kernel': 2,
+                'head_ce_kernelILb1ELb0E': 0, 'embed_norm_kernel': 0, 'es_gradient_kernel': 0}
+
+
+@pytest.mark.parametrize('name', ['mlp', 'proj', 'attention', 'head', 'norm', 'es'])
+def test_step_kernels_spill_within_budget_and_never_in_a_loop(name, tmp_path):
+    asm = A.device_asm(B.CSRC / f'{name}.hip', tmp_path)
+    spills = A.kernel_spills(asm)
+    checked = 0
+    for kernel, n in spills.items():
+        for key, budget in SPILL_BUDGET.items():
+            if key in kernel:
+                assert n <= budget, (kernel, n)
+                checked += 1
+    assert checked > 0
+    loops, bad = A.loop_scratch(asm)
+    assert loops > 0
+    assert [b for b in bad if any(key in b[0] for key in SPILL_BUDGET)] == []
 
 
 def test_load_check_catches_reused_destinations(tmp_path):
@@ -42,6 +65,57 @@ __global__ void k(const float* p, float* o, int n) {
 ''')
     asm = A.device_asm(src, tmp_path)
     assert A.async_load_touches(asm) != []
+
+
+def test_lds_check_catches_reused_destinations(tmp_path):
+    # asm LDS reads whose results are never used: the compiler may hand their registers to other
+    # values while the reads are in flight
+    src = tmp_path / 'dead_lds.hip'
+    src.write_text('''
+#include <hip/hip_runtime.h>
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+__global__ void k(const float* p, float* o, int n) {
+  __shared__ float s[4096];
+  for (int i = threadIdx.x; i < 4096; i += 64) s[i] = p[i];
+  __syncthreads();
+  const unsigned a = (unsigned)(unsigned long)(__attribute__((address_space(3))) float*)s + threadIdx.x * 16;
+  float acc = 0.f;
+  for (int i = 0; i < n; ++i) {
+    floatx4 dead;
+    __asm__ volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(dead) : "v"(a));
+    acc += p[i * 64 + threadIdx.x] * acc + 1.f;
+  }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)");
+  o[threadIdx.x] = acc;
+}
+''')
+    asm = A.device_asm(src, tmp_path)
+    assert A.lds_load_touches(asm) != []
+
+
+def test_loop_scratch_check_catches_spills_in_a_loop(tmp_path):
+    # 200 live values per lane at 1024 threads per workgroup: the loop body spills
+    src = tmp_path / 'spill_loop.hip'
+    src.write_text('''
+#include <hip/hip_runtime.h>
+__global__ void __launch_bounds__(1024) k(const float* p, float* o, int n) {
+  float v[200];
+#pragma unroll
+  for (int j = 0; j < 200; ++j) v[j] = p[threadIdx.x + j * 1024];
+  for (int i = 0; i < n; ++i) {
+#pragma unroll
+    for (int j = 0; j < 200; ++j) v[j] = v[j] * v[(j + 1) % 200] + p[i * 200 + j];
+    __asm__ volatile("" ::: "memory");
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 200; ++j) s += v[j];
+  o[threadIdx.x] = s;
+}
+''')
+    asm = A.device_asm(src, tmp_path)
+    loops, bad = A.loop_scratch(asm)
+    assert loops == 1 and bad != []
 
 
 def test_result_check_catches_early_reads(tmp_path):

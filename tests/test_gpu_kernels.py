@@ -262,6 +262,48 @@ def test_qkv_rope_gemm_matches_unfused(device, T, members, shift, ve, pert):
     assert float((got - want).abs().max()) <= 2 ** -7 * max(1.0, float(want.abs().max()))
 
 
+@pytest.mark.parametrize('T,members,shift,ve', [(256, 4, 1, True), (128, 3, 0, False), (2048, 1, 0, True)])
+def test_qkv_row_resident_matches_oracle(device, T, members, shift, ve):
+    """The row-resident q|k|v projection (taken when T and the row count are multiples of 128)
+    against the float64 oracle directly: R.lowrank for each of q, k, v (rank-1 through the given
+    x . b dots), R.rotary and R.rms_norm per head for q and k, and v + gate * R.lowrank_embed."""
+    g = _gen(T + 31 * members)
+    M, K, V = T * members, 512, 4096
+    rows = (members >> shift) + 1
+    A = _bf(torch.randn(M, K, generator=g))
+    W = _bf(torch.randn(1536, K, generator=g) / math.sqrt(K))
+    sign = torch.randn(members, generator=g) * 0.3
+    a = [torch.randn(rows, 512, generator=g) for _ in range(3)]
+    b = [torch.randn(rows, K, generator=g) for _ in range(3)]
+    pr = torch.arange(members) >> shift
+    x = A.double().view(members, T, K)
+    u = [(x * b[k].double()[pr][:, None, :]).sum(-1).reshape(M, 1).float() for k in range(3)]
+    cos, sin = R.rotary_tables(T)
+    gate = torch.rand(M, 8, generator=g) * 2
+    table = torch.randn(V, 512, generator=g)
+    idx = torch.randint(0, V, (T,), generator=g)
+    nz = NoiseRows(a=torch.randn(rows, V, generator=g), b=torch.randn(rows, 512, generator=g), shift=shift)
+    dv = lambda z: z.to(device)
+    r1 = nk.rank1(dv(sign), T, [dv(z) for z in a], [dv(z) for z in u], 1, 1, shift)
+    out = torch.empty(M, 1536, dtype=torch.bfloat16, device=device)
+    nk.qkv_rope_gemm(dv(A), dv(W), r1, out, T, dv(cos), dv(sin), dv(sign), dv(gate) if ve else None,
+                     dv(table) if ve else None, dv(idx),
+                     NoiseRows(a=dv(nz.a), b=dv(nz.b), shift=shift) if ve else None)
+    s = sign.double()
+    proj = [R.lowrank(x, W.double()[512 * k:512 * (k + 1)], a[k].double()[pr], b[k].double()[pr], s)
+            for k in range(3)]
+    rq = R.rms_norm(R.rotary(proj[0].view(members, T, 8, 64), cos.double(), sin.double())).reshape(M, 512)
+    rk = R.rms_norm(R.rotary(proj[1].view(members, T, 8, 64), cos.double(), sin.double())).reshape(M, 512)
+    v = proj[2].reshape(M, 512)
+    if ve:
+        emb = R.lowrank_embed(table.double(), nz.a.double()[pr], nz.b.double()[pr], idx, s).reshape(M, 512)
+        v = v + gate.double().repeat_interleave(64, 1) * emb
+    got = out.cpu()
+    _close_bf16(got[:, :512], rq)
+    _close_bf16(got[:, 512:1024], rk)
+    _close_bf16(got[:, 1024:], v)
+
+
 @pytest.mark.parametrize('T,window,members,unit', [
     (96, 16, 2, True), (128, 64, 3, True), (256, 1024, 2, True), (300, 100, 2, True),
     (2048, 1024, 1, True), (2048, 2048, 1, True), (520, 0, 1, True), (700, 300, 2, False),

@@ -15,6 +15,7 @@ import torch
 from noise_amd import _lib
 from noise_amd import kernels as K
 from noise_amd.kernels import NoiseRows
+from oracle import model_ref as R
 
 pytestmark = pytest.mark.gpu
 
@@ -241,16 +242,19 @@ def test_mlp_fused_attention_proj_matches_separate_gemm(device, T, members, shif
 def test_mlp_fused_attention_proj_alone(device, T, members, pert):
     """With zero MLP weights and noise rows the fused launch is the attention c_proj alone:
     x + y Wo^T + s (sum of the per-head dots) a_o^T, equal to lowrank_gemm ADD_F32 up to the order
-    of the fp32 additions."""
+    of the fp32 additions, and to the float64 oracle x + R.lowrank(y, Wo, a_o, b_o, s) when the
+    per-head parts are the heads' y . b_o (the attention epilogue's dots)."""
     g = torch.Generator().manual_seed(6000 + T)
     M = members * T
     x = torch.randn(M, D, generator=g).to(device)
     y = (torch.randn(M, D, generator=g) * 0.5).to(torch.bfloat16).to(device)
     wo = (torch.randn(D, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(device)
-    u = torch.randn(M, 8, generator=g).to(device)
     sign = torch.tensor([0.3 if j % 2 == 0 else -0.3 for j in range(members)], device=device)
     o = NoiseRows(a=torch.randn(members, D, generator=g).to(device), b=torch.randn(members, D, generator=g).to(device),
                   shift=0)
+    y64 = y.double().cpu().view(members, T, D)
+    b64 = o.b.double().cpu()
+    u = (y64.view(members, T, 8, 64) * b64.view(members, 1, 8, 64)).sum(-1).reshape(M, 8).float().to(device)
     zeros = lambda w_a, w_b: NoiseRows(a=torch.zeros(members, w_a, device=device), b=torch.zeros(members, w_b, device=device),
                                        shift=0)
     w1p, w2p = _packed(torch.zeros(F, D), torch.zeros(D, F), device)
@@ -261,6 +265,9 @@ def test_mlp_fused_attention_proj_alone(device, T, members, pert):
     K.mlp_fused(got, got, T, members, w1p, w2p, _lib.MLP_NORM | _lib.MLP_RESIDUAL, s, zeros(F, D), zeros(D, F),
                 attn=(y, wo, u if pert else None, o if pert else None))
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+    s64 = sign.double().cpu() if pert else torch.zeros(members, dtype=torch.float64)
+    oracle = x.double().cpu() + R.lowrank(y64, wo.double().cpu(), o.a.double().cpu(), b64, s64).reshape(M, D)
+    torch.testing.assert_close(got.double().cpu(), oracle, rtol=1e-5, atol=2e-5)
 
 
 def test_mlp_fused_next_norm_rejects_a_mismatched_record(device):

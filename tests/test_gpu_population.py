@@ -76,6 +76,56 @@ def test_sensitive_population_loss(device, init_params, golden, golden_json, gol
     assert float((got - ref16).abs().max()) <= bar
 
 
+def test_sensitive_small_sigma_population_loss(device, init_params, golden_sensitive_small):
+    """The sensitive weights (O(1) logits, open gates) at the configs' sigma = 1e-3, against the
+    reference's own losses (golden_sensitive_small.npz): within the reference's bf16-autocast-vs-fp32
+    spread of its fp32 losses (1.2e-3 here; the oracle's build policy sits at 3.4e-4), within twice
+    that of its autocast losses, and within 1e-4 + 4x the float32 envelope of the build oracle."""
+    z = golden_sensitive_small
+    p = _sensitive(init_params)
+    idx, targets = t(z['idx']), t(z['targets'])
+    noise, sign = antithetic(pair_noise(4, seed=7), 1e-3)
+    got = noise_amd.population_loss(None, _params(p, device), _to(noise, device), sign.to(device),
+                                    idx.to(device), targets.to(device)).cpu().double()
+    oracle = R.population_loss(p, noise, sign, idx, targets, policy='build')
+    envelope = float((oracle - R.population_loss(p, noise, sign, idx, targets, policy='build32').double()).abs().max())
+    ref32, ref16 = t(z['losses']).double(), t(z['losses_autocast']).double()
+    spread = max(1e-4, float((ref16 - ref32).abs().max()))
+    e_or, e32, e16 = (float((got - r).abs().max()) for r in (oracle, ref32, ref16))
+    print(f'sensitive sigma=1e-3: |gpu - oracle| {e_or:.2e} (bar {1e-4 + 4 * envelope:.2e}), |gpu - ref fp32| '
+          f'{e32:.2e} (bar {spread:.2e}), |gpu - ref autocast| {e16:.2e} (bar {2 * spread:.2e})')
+    assert e_or <= 1e-4 + 4 * envelope
+    assert e32 <= spread
+    assert e16 <= 2 * spread
+    d = lambda v: v[0::2] - v[1::2]
+    assert torch.equal(torch.sign(d(got)), torch.sign(d(ref32)))
+
+
+def test_sensitive_clean_forward_and_logits(device, init_params, golden, golden_scoring):
+    """GPT.forward (utils/model.py:193-210) on the sensitive weights, against the reference's own
+    outputs: the capped logits of the first two tokens (golden.npz 'sensitive/logits', O(1), max
+    |z| 4.3, where the cap moves them by up to 0.12) within 1e-2 of max |z| -- the bf16 activation
+    bar --, and the per-token cross-entropy ('sensitive/clean', fp32) within the reference's own
+    scoring arithmetic's distance from it (its bf16 GPU scoring, golden_scoring.npz: 0.049 per
+    token, 1.1e-3 in the mean)."""
+    model = noise_amd.GPT(device=device)
+    model.load_state_dict(_sensitive(init_params), strict=True)
+    idx, targets = t(golden['sensitive/idx']), t(golden['sensitive/targets'])
+    logits = model(idx[None].to(device))[0, :2].cpu().double()
+    ref = t(golden['sensitive/logits']).double()
+    bar = 1e-2 * float(ref.abs().max())
+    err = float((logits - ref).abs().max())
+    print(f'sensitive logits: max |gpu - ref| {err:.3e}, bar {bar:.3e}')
+    assert err <= bar
+    ce = model(idx[None].to(device), targets[None].to(device), loss_reduction='none').cpu().double()
+    clean = t(golden['sensitive/clean']).double()
+    scored = t(golden_scoring['sensitive/scoring_ce']).double()
+    tok_bar, mean_bar = float((scored - clean).abs().max()), abs(float(scored.mean() - clean.mean()))
+    e_tok, e_mean = float((ce - clean).abs().max()), abs(float(ce.mean() - clean.mean()))
+    print(f'sensitive clean CE: per token {e_tok:.3e} (bar {tok_bar:.3e}), mean {e_mean:.3e} (bar {mean_bar:.3e})')
+    assert e_tok <= tok_bar and e_mean <= mean_bar
+
+
 def test_clean_forward_matches_reference(device, init_params, golden):
     model = noise_amd.GPT(device=device)
     model.load_state_dict(init_params, strict=True)  # the CPU-seeded weights of the goldens

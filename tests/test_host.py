@@ -134,6 +134,14 @@ def test_step_entry_points_reject_bad_arguments():
     _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'unknown flags')
     mlp.flags, mlp.in_ = 0, odd
     _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'aligned')
+    mlp.in_, mlp.member_stride_out = fake, 0  # every member would write the same rows
+    _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'overlap')
+    mlp.member_stride_out, mlp.member_stride_in = 512 * 256, 0  # in place over shared input rows
+    _rejects(lib.noise_mlp_fused(C.byref(mlp), None), 'in-place')
+    mlp.out = 1 << 20  # distinct output rows: shared input rows are fine
+    mlp.members = 0
+    assert lib.noise_mlp_fused(C.byref(mlp), None) == _lib.NOISE_OK
+    mlp.out, mlp.member_stride_in, mlp.members = fake, 512 * 256, 2
     mlp.in_, mlp.members = fake, 0
     assert lib.noise_mlp_fused(C.byref(mlp), None) == _lib.NOISE_OK
     _rejects(lib.noise_mlp_pack(None, 0, None, 0, fake, None, None), 'c_fc needs')

@@ -131,6 +131,47 @@ def test_population_loss_matches_reference_sensitive(init_params, golden, golden
     torch.testing.assert_close(clean, t(golden['sensitive/clean']), rtol=0, atol=5e-5)
 
 
+SMALL = dict(pairs=4, sigma=1e-3, noise_seed=7, weight_seed=5)  # make_golden.py SENSITIVE_SMALL
+
+
+def test_clean_logits_match_reference_sensitive(init_params, golden, golden_json):
+    """GPT.forward without targets (utils/model.py:202-210) on the sensitive weights, whose logits
+    are of order one (max |z| 4.3), where the soft cap 15 tanh(z / 15) moves them by up to 0.12:
+    the oracle's fp32 policy reproduces the reference's logits, and its bf16 build policy (the
+    GPU's cast points) lies within 1e-2 of max |z|, the bf16 activation bar, which a missing cap
+    does not meet."""
+    p = sensitive_params(init_params, golden_json['sensitive']['weight_seed'])
+    idx = t(golden['sensitive/idx'])
+    ref = t(golden['sensitive/logits']).double()
+    fp32 = R.clean_logits(p, idx[None], policy='fp32')[0, :2].double()
+    torch.testing.assert_close(fp32, ref, rtol=0, atol=2e-5)
+    bar = 1e-2 * float(ref.abs().max())
+    build = R.clean_logits(p, idx[None], policy='build')[0, :2].double()
+    assert float((build - ref).abs().max()) <= bar
+    uncapped = 15 * torch.atanh(ref / 15)
+    assert float((uncapped - ref).abs().max()) > bar
+
+
+def test_population_loss_matches_reference_sensitive_small_sigma(init_params, golden_sensitive_small):
+    """The sensitive weights at sigma = 1e-3 (golden_sensitive_small.npz): the oracle's fp32 policy
+    reproduces the reference's losses; the build policy lies within the reference's own
+    bf16-autocast-vs-fp32 spread of the fp32 losses, and within twice it of the autocast losses
+    (both are bf16 evaluations of the same forward); the antithetic differences keep their signs."""
+    z = golden_sensitive_small
+    p = sensitive_params(init_params, SMALL['weight_seed'])
+    idx, targets = t(z['idx']), t(z['targets'])
+    noise, sign = antithetic(pair_noise(SMALL['pairs'], seed=SMALL['noise_seed']), SMALL['sigma'])
+    ref32, ref16 = t(z['losses']).double(), t(z['losses_autocast']).double()
+    torch.testing.assert_close(R.population_loss(p, noise, sign, idx, targets, policy='fp32').double(), ref32,
+                               rtol=0, atol=2e-5)
+    spread = max(1e-4, float((ref16 - ref32).abs().max()))
+    build = R.population_loss(p, noise, sign, idx, targets, policy='build').double()
+    assert float((build - ref32).abs().max()) <= spread
+    assert float((build - ref16).abs().max()) <= 2 * spread
+    d = lambda v: v[0::2] - v[1::2]
+    assert torch.equal(torch.sign(d(build)), torch.sign(d(ref32)))
+
+
 def test_build_policy_within_reference_autocast_envelope(init_params, golden, golden_json, golden_autocast):
     """The oracle's bf16 build policy against the reference's own bf16-autocast losses
     (eggroll.py:144-145 wraps population_loss in torch.autocast): on both fixtures it stays
