@@ -21,8 +21,10 @@ attention c_proj with its rank-1 term into the residual rows, then norm, c_fc wi
 term, relu^2, c_proj with its rank-1 term and the residual add in one launch, the hidden kept on
 chip, and the next layer's mix_norm on the finished rows): algorithmic FLOPs per launch / its
 mean duration, timed live with HIP events on the launch stream.
-`cpu_baseline` times the CPU oracle (oracle/model_ref.py, float32) on a bounded sample of the same
-workload on this host.
+`mlp_only` is the MLP alone (config 1's kernel: no attention c_proj, no next-layer norm) at the same
+rows, timed the same way. `head_split` is one more step with the head's product on fp32-accurate
+weights (bf16 hi + lo halves), after the timed steps. `cpu_baseline` times the CPU oracle
+(oracle/model_ref.py, float32) on a bounded sample of the same workload on this host.
 """
 import argparse
 import json
@@ -547,9 +549,52 @@ def main():
         'step_tflops': step_flops(members, T) / (elapsed / args.steps) / 1e12,
         'mean_loss': losses[-1],
     }
+    # Outside the timed region: (1) the relu^2 MLP alone (config 1's kernel, no attention c_proj
+    # fold, no next-layer norm) at the same rows, its fraction of peak for the MLP's own FLOPs;
+    # (2) one step with the head as the fp32-weight product (bf16 hi + lo halves, config 4's
+    # "fp32 head") instead of the trainer's bf16 autocast product.
+    out['mlp_only'] = mlp_only_roofline()
+    from noise_amd.population import PreparedWeights
+    es.weights = PreparedWeights(es.params, es.cfg, head_split=True)
+    es.step(x, y, opt, args.warmup + args.steps + 1)  # warmup of the hi + lo head
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    es.step(x, y, opt, args.warmup + args.steps + 2)
+    torch.cuda.synchronize()
+    hs = time.perf_counter() - t0
+    out['head_split'] = {'ms_per_step': hs * 1e3, 'value': members * T / hs, 'unit': 'member-tokens/s',
+                         'steps': 1, 'warmup': 1,
+                         'note': 'one step with the head product on fp32-accurate weights (bf16 hi + lo halves)'}
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
     print(json.dumps(out), flush=True)
+
+
+def mlp_only_roofline(reps=5):
+    """The fused relu^2 MLP alone (norm, c_fc + rank-1, relu^2, c_proj + rank-1, residual, the hidden
+    on chip) at the bench's 512 members x 2048 tokens: mean launch time from HIP events on the
+    launch stream, and its fraction of bf16 peak for rows * (4 d f + 2 (d + f)) FLOPs."""
+    from noise_amd import _lib
+    from noise_amd import kernels as K
+    a = mlp_inputs()
+    stream = torch.cuda.current_stream()
+    launch = lambda: K.mlp_fused(a['x'], a['x'], a['T'], a['members'], a['w_fc'], a['w_pr'],
+                                 _lib.MLP_NORM | _lib.MLP_RESIDUAL, a['sign'], a['fc'], a['pr'])
+    launch()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in events:
+        e0.record(stream)
+        launch()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = sum(e0.elapsed_time(e1) for e0, e1 in events) / reps
+    rows = a['x'].shape[0]
+    flops = mlp_flops(rows, attn=False)
+    del a
+    torch.cuda.empty_cache()
+    return {'launch_ms': ms, 'flops_per_launch': flops, 'rows_per_launch': rows,
+            'achieved': flops / (ms / 1e3) / 1e12, 'unit': 'TFLOP/s', 'frac': flops / (ms / 1e3) / PEAK_BF16,
+            'kernel': 'mlp_fused alone (norm, c_fc, relu^2, c_proj, residual; no attention c_proj, no next norm)'}
 
 
 if __name__ == '__main__':

@@ -126,17 +126,38 @@ NOISE_DEV bf16x8 as_bf16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
 #define MLP_DSREAD(DST, ADDR, OFS) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(DST) : "v"(ADDR), "n"(OFS))
 #define MLP_LGKM(N) __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N))
 
-// The MFMA order of one step. With both halves: F0..F3 (c_fc k-steps 0-3) while the epilogue of
-// the previous chunk produces the c_proj operand, then P0 F4 P1 F5 ... P27 F31, then P28..P31 (P t:
-// c_proj block t & 15, k-step t >> 4). With one half, its 32 MFMAs in order.
+// The MFMA order of one step. With both halves: F0..F7 (c_fc k-steps 0-7) while the epilogue of
+// the previous chunk produces the operand of the first 16 c_proj MFMAs, then P0 F8 P1 F9 ... P23
+// F31, then P24..P31 (P t: c_proj block t & 15, k-step t >> 4); the epilogue's second half runs
+// among the interleaved ones, before P16. With one half, its 32 MFMAs in order.
 template <bool FCP, bool PRJ>
 struct StepOps {
   static constexpr int N = (FCP ? 32 : 0) + (PRJ ? 32 : 0);
+  static constexpr int NF0 = 8;  // leading c_fc MFMAs
   static constexpr bool is_fc(int s) {
-    return !PRJ ? true : !FCP ? false : s < 4 ? true : (s - 4 >= 56 ? false : ((s - 4) & 1) != 0);
+    return !PRJ ? true : !FCP ? false : s < NF0 ? true : (s - NF0 >= 2 * (32 - NF0) ? false : ((s - NF0) & 1) != 0);
   }
   static constexpr int idx(int s) {
-    return (!PRJ || !FCP || s < 4) ? s : (s - 4 >= 56 ? 28 + (s - 60) : (((s - 4) & 1) ? 4 + ((s - 4) >> 1) : (s - 4) >> 1));
+    return (!PRJ || !FCP || s < NF0) ? s
+           : (s - NF0 >= 2 * (32 - NF0) ? (32 - NF0) + (s - NF0 - 2 * (32 - NF0))
+                                         : (((s - NF0) & 1) ? NF0 + ((s - NF0) >> 1) : (s - NF0) >> 1));
+  }
+  // The epilogue piece that follows c_fc MFMA i, or -1: pieces 0-3 (the operand of P0..P15) after
+  // F3..F6, pieces 4-7 (that of P16..P31) after F10, F14, F18, F22 -- all after F3, whose fragment
+  // wait also covers the perturbation values (read after the first fragments).
+  static constexpr int piece_after(int i) {
+    return i >= 3 && i <= 6 ? i - 3 : i >= 10 && i <= 22 && (i - 10) % 4 == 0 ? 4 + (i - 10) / 4 : -1;
+  }
+  static constexpr int FIRST_PIECE = 3;
+  // With both halves: every piece runs before the c_proj MFMAs that read its values (pieces 0-3
+  // before P0, 4-7 before P16).
+  static constexpr bool pieces_in_order() {
+    int seen = 0;
+    for (int s = 0; s < N; ++s) {
+      if (is_fc(s) && piece_after(idx(s)) >= 0) ++seen;
+      if (!is_fc(s) && ((idx(s) == 0 && seen < 4) || (idx(s) == 16 && seen < 8))) return false;
+    }
+    return seen == 8;
   }
 };
 
@@ -148,8 +169,9 @@ struct StepOps {
 // inline asm so that the c_fc accumulators stay in VGPRs and the c_proj ones in AGPRs; the hazards
 // the compiler then cannot see are covered explicitly: 2 wait states between the VALU writing the
 // c_proj operand and its first MFMA, and 24 after a chunk's last MFMA before VALU reads its result.
-// Fragments are read MLP_AHEAD MFMAs ahead; the epilogue's perturbation values are read before
-// all of them, so the wait for the first fragment covers them too.
+// Fragments are read MLP_AHEAD MFMAs ahead; the epilogue's perturbation values right after the
+// first MLP_AHEAD fragments (before all of them in the last step), so the fragment wait before the
+// first piece covers them too.
 template <bool FCP, bool PRJ, int FB, bool LFC, bool LMP>
 NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&acc)[16], float& up,
                         uint32_t fcb, uint32_t mpb0, uint32_t mpb1, uint32_t ab_base, int chunk_prev, float su,
@@ -157,15 +179,20 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
   using O = StepOps<FCP, PRJ>;
   constexpr int NA = MLP_AHEAD + 1;
   floatx4 av[4], bv[4];
-  if (PRJ) {
-    // Perturbation values of the previous chunk: this lane's features base + 8 g + 4 half + q.
-    const uint32_t ab = ab_base + (uint32_t)(((chunk_prev + c0) & (NCH - 1)) * FC * 4);
+  // Perturbation values of the previous chunk: this lane's features base + 8 g + 4 half + q. In a
+  // step with both halves they are read after the first MLP_AHEAD fragments, so that the first
+  // MFMA waits for its own fragment only (measured: 1.5-2.5% per launch); the last step, whose
+  // epilogue runs before its MFMAs, reads them first.
+  constexpr bool LATE = FCP && PRJ;
+  const uint32_t ab = ab_base + (uint32_t)(((chunk_prev + c0) & (NCH - 1)) * FC * 4);
+  auto read_ab = [&av, &bv, ab]() __attribute__((always_inline)) {
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
       MLP_DSREAD(av[gi], ab, 32 * gi);
       MLP_DSREAD(bv[gi], ab, 4 * F + 32 * gi);
     }
-  }
+  };
+  if (PRJ && !LATE) read_ab();
   bf16x8 fr[NA];
   // Fragment read for op S (S a compile-time constant, so the offsets are immediates).
   auto read = [&, fcb, mpb0, mpb1]<int S>() __attribute__((always_inline)) {
@@ -177,6 +204,9 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
   [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
     (read.template operator()<S>(), ...);
   }(std::make_integer_sequence<int, MLP_AHEAD>{});
+  if (LATE) read_ab();
+  static_assert(!LATE || O::FIRST_PIECE >= MLP_AHEAD, "the perturbation values must be in by the first piece");
+  static_assert(!(FCP && PRJ) || O::pieces_in_order(), "an epilogue piece after the MFMA that reads it");
   uint32_t hw[8];
   bf16x8 hid[2];
   // Epilogue piece e (0..7): values 2 e, 2 e + 1 of the previous chunk's accumulators; pieces 0-3
@@ -210,7 +240,8 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
       __builtin_amdgcn_global_load_lds((const void*)(ld.mp_src + (LK - 8) * 512), (void*)(ld.mp_dst + (LK - 8) * 1024),
                                        16, 0, 0);
     if constexpr (SX + MLP_AHEAD < O::N) read.template operator()<SX + MLP_AHEAD>();
-    MLP_LGKM(O::N - 1 - SX < MLP_AHEAD ? O::N - 1 - SX : MLP_AHEAD);
+    // fragments read after this op's, plus the 8 perturbation reads while they are younger
+    MLP_LGKM((O::N - 1 - SX < MLP_AHEAD ? O::N - 1 - SX : MLP_AHEAD) + (LATE && SX < MLP_AHEAD ? 8 : 0));
     const bf16x8 f = fr[SX % NA];
     constexpr int i = O::idx(SX);
     if constexpr (O::is_fc(SX)) {
@@ -221,15 +252,12 @@ NOISE_DEV void mlp_step(const bf16x8 (&hB)[32], floatx16 (&fc)[2], floatx16 (&ac
       else
         __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                          : "+v"(fc[FB]) : "v"(f), "v"(hB[i]));
-      if constexpr (PRJ && i < 8) {
-        // Epilogue piece i after c_fc MFMA i (held there by the scheduling barriers): pieces 0-3
-        // before the first c_proj MFMA, 4-7 among the first ones; the perturbation values are in
-        // once the first fragment is.
-        if constexpr (i == 0)
-          __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]), "+v"(bv[1]),
-                           "+v"(bv[2]), "+v"(bv[3]));
+      if constexpr (PRJ && i == O::FIRST_PIECE)  // the wait before this MFMA covered them
+        __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]), "+v"(bv[1]),
+                         "+v"(bv[2]), "+v"(bv[3]));
+      if constexpr (PRJ && O::piece_after(i) >= 0) {  // held in place by the scheduling barriers
         __builtin_amdgcn_sched_barrier(0);
-        epi.template operator()<i>();
+        epi.template operator()<O::piece_after(i)>();
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {

@@ -24,9 +24,12 @@ def test_inline_asm_kernels_are_hazard_free(name, tmp_path):
     assert A.mfma_result_touches(asm) == []
 
 
-# Spill budgets (.vgpr_spill_count) of the kernels the population step launches: the fused MLP spills
-# a few prologue/epilogue values (its waves hold 512 registers), the others none or one.
-SPILL_BUDGET = {'mlp_fused_kernel': 48, 'qkv_proj_kernel': 0, 'window_attention_kernel': 2,
+# Spill budgets (.vgpr_spill_count) of the kernels the population step launches (for the fused MLP
+# the step's two instances, with the attention c_proj and the next mix_norm or final norm, and the
+# plain one bench.py times alone): the fused MLP spills a few prologue/epilogue values (its waves
+# hold 512 registers), the others none or one.
+SPILL_BUDGET = {'mlp_fused_kernelILb1ELb1ELi2ELb1E': 48, 'mlp_fused_kernelILb1ELb1ELi1ELb1E': 48,
+                'mlp_fused_kernelILb1ELb1ELi0ELb0E': 48, 'qkv_proj_kernel': 0, 'window_attention_kernel': 2,
                 'head_ce_kernelILb1ELb0E': 0, 'embed_norm_kernel': 0, 'es_gradient_kernel': 0}
 
 
