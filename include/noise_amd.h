@@ -249,7 +249,9 @@ typedef struct {
 
 /* logits = h (W + s a b^T)^T in fp32 accuracy, 15 tanh(logits / 15), cross-entropy against
  * the target (train/val/eggroll.py:94-102; utils/model.py:203-209), and, when `logits` is set,
- * the capped logits themselves (utils/model.py:203-204, 210). V % 256 == 0. */
+ * the capped logits themselves (utils/model.py:203-204, 210). V % 64 == 0; V % 256 == 0 as well
+ * unless T and M are multiples of 256, V <= 4096, a has 16-byte aligned rows and no logits are
+ * asked for (the shape of the population step, taken by a row-resident kernel). */
 int noise_head_ce(const noise_head_t* args, void* stream);
 
 /* out[p] = mean over t of ce[p*T + t] (eggroll.py:102). */

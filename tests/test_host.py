@@ -108,8 +108,10 @@ def test_step_entry_points_reject_bad_arguments():
 
     head = _lib.Head(h=fake, w_hi=fake, M=1024, V=100, T=256, targets=fake, targets_stride=256, ce=fake,
                      ignore_index=-1)
+    _rejects(lib.noise_head_ce(C.byref(head), None), 'multiple of 64')
+    head.V, head.T = 192, 300  # V % 64 == 0, but the ragged rows take the tile kernel (V % 256)
     _rejects(lib.noise_head_ce(C.byref(head), None), 'multiple of 256')
-    head.V, head.ignore_index = 4096, 5
+    head.V, head.T, head.ignore_index = 4096, 256, 5
     _rejects(lib.noise_head_ce(C.byref(head), None), 'class index')
     head.ignore_index, head.h = -1, odd
     _rejects(lib.noise_head_ce(C.byref(head), None), '16-byte aligned')
