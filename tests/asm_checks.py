@@ -187,3 +187,33 @@ def loop_scratch(asm):
             if in_loop and re.match(r'\s*scratch_', line):
                 bad.append((kernel, block, line.strip()))
     return loops, bad
+
+
+def step_barrier_waits(asm):
+    """(barriers checked, [(barrier line, wait count, ops after the loads)]), for kernels whose
+    stages are loaded one step ahead: every `s_waitcnt vmcnt(N)` that opens an `s_barrier` after
+    direct global -> LDS loads (global_load_lds*) must leave only vector memory operations issued
+    after the last of those loads in flight, i.e. at least N such operations follow it (they
+    retire in order), so that the stage is complete for this wave at the barrier. Scans each
+    kernel back to the previous barrier. (A ring loaded two stages ahead, as the fused MLP's
+    attention c_proj, waits for the older group on purpose and is not checked this way.)"""
+    bad, checked = [], 0
+    vmem = re.compile(r'(global_|buffer_|scratch_|flat_)(load|store|atomic)')
+    for m in re.finditer(r'^(_Z\S+):(?:[ \t]*;[^\n]*)?$(.*?)^\.Lfunc_end\d+:', asm, re.M | re.S):
+        ins = _instructions(m.group(2))
+        for i, line in enumerate(ins):
+            w = re.match(r's_waitcnt\s.*vmcnt\((\d+)\)', line)
+            if not w or not any(x.startswith('s_barrier') for x in ins[i + 1:i + 3]):
+                continue
+            n, after = int(w.group(1)), 0
+            for prev in reversed(ins[:i]):
+                if prev.startswith('s_barrier'):
+                    break
+                if prev.startswith('global_load_lds'):
+                    checked += 1
+                    if after < n:
+                        bad.append((line, n, after))
+                    break
+                if vmem.match(prev):
+                    after += 1
+    return checked, bad

@@ -49,6 +49,32 @@ def test_step_kernels_spill_within_budget_and_never_in_a_loop(name, tmp_path):
     assert [b for b in bad if any(key in b[0] for key in SPILL_BUDGET)] == []
 
 
+@pytest.mark.parametrize('name', ['proj', 'head'])
+def test_stage_barriers_cover_the_stage(name, tmp_path):
+    """The step barriers of the one-ahead pipelines (q|k|v projection, head) wait for their stage's
+    direct loads, whatever stores or table loads were issued after them."""
+    asm = A.device_asm(B.CSRC / f'{name}.hip', tmp_path)
+    checked, bad = A.step_barrier_waits(asm)
+    assert checked > 0 and bad == []
+
+
+def test_stage_barrier_check_catches_a_short_wait(tmp_path):
+    src = tmp_path / 'short_wait.hip'
+    src.write_text('''
+#include <hip/hip_runtime.h>
+__global__ void k(const float* p, float* o) {
+  __shared__ float s[1024];
+  __builtin_amdgcn_global_load_lds(p + threadIdx.x * 4, s, 16, 0, 0);
+  o[threadIdx.x] = 1.f;
+  __asm__ volatile("s_waitcnt vmcnt(2)\\n\\ts_barrier" ::: "memory");
+  o[threadIdx.x + 64] = s[threadIdx.x];
+}
+''')
+    asm = A.device_asm(src, tmp_path)
+    checked, bad = A.step_barrier_waits(asm)
+    assert checked == 1 and bad != []
+
+
 def test_load_check_catches_reused_destinations(tmp_path):
     # an in-repo stand-in for the failure: asm loads whose results are never used
     src = tmp_path / 'dead_loads.hip'
