@@ -1,6 +1,6 @@
 """Benchmark: perturbed member-tokens/s of one MI355X on the full EGGROLL population step.
 
-    python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--members 3072] [--no-cpu] [--no-extra]
     python bench.py --probe-mlp      # for rocprofv3 --pmc: a copy of known size, then the fused MLP
     python bench.py --probe-attention  # for rocprofv3 --pmc: the attention launches of one chunk
     python bench.py --probe-step     # for rocprofv3 --pmc: a copy of known size, then one step at 512 members
@@ -463,6 +463,8 @@ def main():
     ap.add_argument('--tokens', type=int, default=2048)
     ap.add_argument('--chunk', type=int, default=256, help='pairs per batched forward')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    ap.add_argument('--no-extra', action='store_true',
+                    help='skip the measurements after the timed steps (MLP alone, fp32-accurate head step)')
     ap.add_argument('--probe-mlp', action='store_true', help='run the MLP counter-collection workload only')
     ap.add_argument('--probe-attention', action='store_true', help='run the attention counter-collection workload only')
     ap.add_argument('--probe-step', action='store_true', help='run the whole-step counter-collection workload only')
@@ -553,18 +555,19 @@ def main():
     # fold, no next-layer norm) at the same rows, its fraction of peak for the MLP's own FLOPs;
     # (2) one step with the head as the fp32-weight product (bf16 hi + lo halves, config 4's
     # "fp32 head") instead of the trainer's bf16 autocast product.
-    out['mlp_only'] = mlp_only_roofline()
-    from noise_amd.population import PreparedWeights
-    es.weights = PreparedWeights(es.params, es.cfg, head_split=True)
-    es.step(x, y, opt, args.warmup + args.steps + 1)  # warmup of the hi + lo head
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    es.step(x, y, opt, args.warmup + args.steps + 2)
-    torch.cuda.synchronize()
-    hs = time.perf_counter() - t0
-    out['head_split'] = {'ms_per_step': hs * 1e3, 'value': members * T / hs, 'unit': 'member-tokens/s',
-                         'steps': 1, 'warmup': 1,
-                         'note': 'one step with the head product on fp32-accurate weights (bf16 hi + lo halves)'}
+    if not args.no_extra:
+        out['mlp_only'] = mlp_only_roofline()
+        from noise_amd.population import PreparedWeights
+        es.weights = PreparedWeights(es.params, es.cfg, head_split=True)
+        es.step(x, y, opt, args.warmup + args.steps + 1)  # warmup of the hi + lo head
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        es.step(x, y, opt, args.warmup + args.steps + 2)
+        torch.cuda.synchronize()
+        hs = time.perf_counter() - t0
+        out['head_split'] = {'ms_per_step': hs * 1e3, 'value': members * T / hs, 'unit': 'member-tokens/s',
+                             'steps': 1, 'warmup': 1,
+                             'note': 'one step with the head product on fp32-accurate weights (bf16 hi + lo halves)'}
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline()
     print(json.dumps(out), flush=True)
