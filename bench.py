@@ -591,11 +591,23 @@ def mlp_only_roofline(reps=5):
         e1.record(stream)
     torch.cuda.synchronize()
     ms = sum(e0.elapsed_time(e1) for e0, e1 in events) / reps
+    # the two-wave (producer/consumer) form of the same launch, bit-identical and opt-in
+    os.environ['NOISE_MLP_TWO_WAVE'] = '1'
+    try:
+        launch()
+        for e0, e1 in events:
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ms2 = sum(e0.elapsed_time(e1) for e0, e1 in events) / reps
+    finally:
+        del os.environ['NOISE_MLP_TWO_WAVE']
     rows = a['x'].shape[0]
     flops = mlp_flops(rows, attn=False)
     del a
     torch.cuda.empty_cache()
-    return {'launch_ms': ms, 'flops_per_launch': flops, 'rows_per_launch': rows,
+    return {'launch_ms': ms, 'two_wave_launch_ms': ms2, 'flops_per_launch': flops, 'rows_per_launch': rows,
             'achieved': flops / (ms / 1e3) / 1e12, 'unit': 'TFLOP/s', 'frac': flops / (ms / 1e3) / PEAK_BF16,
             'kernel': 'mlp_fused alone (norm, c_fc, relu^2, c_proj, residual; no attention c_proj, no next norm)'}
 

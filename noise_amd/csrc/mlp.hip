@@ -25,9 +25,17 @@
 //     the other c_fc accumulator set: the epilogue of one chunk overlaps the MFMAs of the next.
 // Per row the kernel moves 2 KB in and 2 KB out (fp32), against 18 KB through HBM for the separate
 // norm, c_fc and c_proj launches.
+#include <stdlib.h>
+
 #include <utility>
 
 #include "mma_tile.h"
+
+namespace noise {
+// The two-wave (producer/consumer) form of the plain MLP (mlp_pc.hip): launched, and true, where it
+// applies.
+bool mlp_pc_launch(const noise_mlp_t& g, hipStream_t st);
+}  // namespace noise
 
 namespace {
 
@@ -898,6 +906,11 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
     }
     return noise::check_launch("mlp_fused (with the next mix_norm)");
   }
+  // NOISE_MLP_TWO_WAVE=1 in the environment runs the plain normed residual MLP in the two-wave
+  // (producer/consumer) form: bit-identical rows, measured slower on MI355X (4.9 against 4.46 ms
+  // at 512 members x 2048 tokens), so not the default.
+  const char* two_wave = getenv("NOISE_MLP_TWO_WAVE");
+  if (two_wave && two_wave[0] == '1' && noise::mlp_pc_launch(g, st)) return noise::check_launch("mlp_fused");
   switch (g.flags) {
     case NOISE_MLP_NORM | NOISE_MLP_RESIDUAL:
       if (g.attn_y) mlp_fused_kernel<true, true, 0, true><<<grid, 256, 0, st>>>(g, none);

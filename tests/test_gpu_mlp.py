@@ -113,6 +113,40 @@ def test_mlp_fused_in_place_equals_out_of_place(device):
     assert torch.equal(out, xi)
 
 
+@pytest.mark.parametrize('T,members,shift,pert', [
+    (256, 4, 1, True), (100, 3, 0, True), (37, 5, 0, False), (2048, 2, 1, True),
+    (300, 9, 2, True),   # members past the groups of 8 of the workgroup numbering, ragged rows
+    (128, 16, 3, False)])
+def test_mlp_two_wave_form_matches_one_wave_form(device, monkeypatch, T, members, shift, pert):
+    """The producer/consumer form (two waves per SIMD, mlp_pc.hip; NOISE_MLP_TWO_WAVE=1) against
+    the one-wave form on the same inputs: every output value accumulates in the same order with the
+    same arithmetic, so the rows are bit-identical; in place as well."""
+    g = torch.Generator().manual_seed(900 + T + members)
+    w1, w2 = _weights(g)
+    rows = (members >> shift) + 1
+    x = (torch.randn(members * T, D, generator=g) * 1.5).to(device)
+    sign = (torch.randn(members, generator=g) * 0.02).to(device) if pert else None
+    fc = NoiseRows(a=torch.randn(rows, F, generator=g).to(device), b=torch.randn(rows, D, generator=g).to(device),
+                   shift=shift)
+    pr = NoiseRows(a=torch.randn(rows, D, generator=g).to(device), b=torch.randn(rows, F, generator=g).to(device),
+                   shift=shift)
+    w1p, w2p = _packed(w1, w2, device)
+    flags = _lib.MLP_NORM | _lib.MLP_RESIDUAL
+    want = torch.full_like(x, float('nan'))
+    K.mlp_fused(x, want, T, members, w1p, w2p, flags, sign, fc if pert else None, pr if pert else None)
+    monkeypatch.setenv('NOISE_MLP_TWO_WAVE', '1')
+    got = torch.full_like(x, float('nan'))
+    K.mlp_fused(x, got, T, members, w1p, w2p, flags, sign, fc if pert else None, pr if pert else None)
+    inplace = x.clone()
+    K.mlp_fused(inplace, inplace, T, members, w1p, w2p, flags, sign, fc if pert else None, pr if pert else None)
+    torch.cuda.synchronize()
+    diff = (got - want).abs()
+    print(f'T={T} members={members}: max |two-wave - one-wave| {float(diff.max()):.3e}, '
+          f'{int((diff > 0).sum())} values differ')
+    assert torch.equal(got, want)
+    assert torch.equal(inplace, want)
+
+
 @pytest.mark.parametrize('T,members,shift,pert,kind', [
     (256, 4, 1, True, 'mix_gate'),    # a value-embedding layer: mixing, q/k/v dots, gate
     (100, 3, 0, True, 'mix'),         # ragged row blocks, no gate
