@@ -209,6 +209,62 @@ def probe_attention(members=512, T=2048, reps=2):
 PEAK_PROBE_ELEMS = 1024 * 2.4e9 * 64 / (4 * 2 + 3 * 8)
 
 
+def _median_launch_ms(fn, reps=6):
+    fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return sorted(e0.elapsed_time(e1) for e0, e1 in ev)[reps // 2]
+
+
+def power_probe():
+    """The same launches with the bench's random operands and with zeroed ones: the instruction
+    stream is identical, so a shorter time with zeros is the power limit (MFMA switching energy
+    falls with zero operands and the clock rises). Fused MLP alone at 512 members x 2048 tokens
+    (zero packed weights: c_fc and with it the relu^2 operand of c_proj vanish), and the
+    row-resident bf16 head at 1,048,576 rows x V = 4096 (zero weight, then zero rows too)."""
+    from noise_amd import _lib
+    from noise_amd import kernels as K
+    from noise_amd.kernels import NoiseRows
+    a = mlp_inputs()
+    flags = _lib.MLP_NORM | _lib.MLP_RESIDUAL
+    x0 = a['x'].clone()
+
+    def mlp():
+        a['x'].copy_(x0)
+        K.mlp_fused(a['x'], a['x'], a['T'], a['members'], a['w_fc'], a['w_pr'], flags, a['sign'], a['fc'], a['pr'])
+
+    copy = _median_launch_ms(lambda: a['x'].copy_(x0))
+    out = {'kernel': 'mlp_fused_kernel<true, true, 0, false> (the MLP alone)', 'unit': 'ms per launch',
+           'random_operands': _median_launch_ms(mlp) - copy}
+    a['w_fc'].zero_()
+    a['w_pr'].zero_()
+    out['zero_weights'] = _median_launch_ms(mlp) - copy
+    print(json.dumps(out), flush=True)
+    del a, x0
+    torch.cuda.empty_cache()
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(3)
+    M, T, V = 512 * 2048, 2048, 4096
+    h = torch.randn(M, 512, device=dev, generator=g).to(torch.bfloat16)
+    W = (torch.randn(V, 512, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    targets = torch.randint(0, V, (M,), device=dev, generator=g)
+    ce = torch.empty(M, device=dev)
+    sign = torch.tensor([1e-3, -1e-3], device=dev).repeat(256)
+    nz = NoiseRows(a=torch.randn(256, V, device=dev, generator=g), shift=1)
+    u = torch.randn(M, device=dev, generator=g)
+    head = lambda: K.head_ce(h, W, None, T, targets, ce, sign, nz, u, targets_stride=T, ignore_index=-1)
+    out = {'kernel': 'head_rr_kernel<false> (bf16 head)', 'unit': 'ms per launch', 'random_operands': _median_launch_ms(head)}
+    W.zero_()
+    out['zero_weights'] = _median_launch_ms(head)
+    h.zero_()
+    out['zero_weights_and_rows'] = _median_launch_ms(head)
+    print(json.dumps(out), flush=True)
+
+
 def bench_probe_cycle(steps, warmup, no_cpu, n=2048, P=512, V=4096):
     """The readout probe of the current records on one GPU: cycle_derivatives over one 2048-token
     sequence along a full cycle of 512 directions, V = 4096 (train/speedrun/run.py:250-265)."""
@@ -470,6 +526,8 @@ def main():
     ap.add_argument('--probe-step', action='store_true', help='run the whole-step counter-collection workload only')
     ap.add_argument('--probe-cycle', action='store_true', help='bench the readout probe kernels (own JSON line)')
     ap.add_argument('--probe-chain', action='store_true', help='bench chain_chunk (own JSON line)')
+    ap.add_argument('--power-probe', action='store_true',
+                    help='the fused MLP and the head with their real operands and with zeros (own JSON lines)')
     ap.add_argument('--own', choices=['none', 'routed', 'window'], default='none',
                     help='--probe-chain: every attention held, the routed own-query moves, or over key windows')
     args = ap.parse_args()
@@ -492,6 +550,9 @@ def main():
         return
     if args.probe_chain:
         bench_probe_chain(max(args.steps, 5), args.warmup, own=None if args.own == 'none' else args.own)
+        return
+    if args.power_probe:
+        power_probe()
         return
 
     import noise_amd
