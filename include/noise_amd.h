@@ -33,7 +33,7 @@ extern "C" {
 #define NOISE_ENONFINITE 3 /* non-finite value (Python: FloatingPointError) */
 
 const char* noise_last_error(void);
-int noise_abi_version(void);
+int noise_abi_version(void); /* 2: noise_mixnorm_t.gain */
 
 /* ---- rank-1 perturbation of a GEMM's output columns ---------------------------------- */
 typedef struct {
@@ -166,6 +166,8 @@ typedef struct noise_mixnorm_s {
   const float* gate_b;  /* [noise rows, 32] */
   int64_t ld_gate_a, ld_gate_b;
   float* gate;          /* out: 2 sigmoid(h[:32] (Wg + s a b^T)^T) [M, 8] */
+  const float* gain;    /* [512] RMSNorm gain: h = bf16(norm(x) * gain) (F.rms_norm's weight);
+                           NULL = none, as the reference's `norm` (utils/model.py:46-47) */
 } noise_mixnorm_t;
 
 /* Replaces the per-layer mixing (train/val/eggroll.py:77-79), `norm` (eggroll.py:81, 93, 94),

@@ -30,7 +30,7 @@ class MixNorm(C.Structure):
                 ('resid', P), ('mix', P), ('eps_resid', P), ('eps_mix', P), ('ld_eps', I64),
                 ('h', P), ('nb', INT), ('b', P * 3), ('ldb', I64), ('u', P), ('ldu', I64),
                 ('gate_w', P), ('gate_a', P), ('gate_b', P), ('ld_gate_a', I64), ('ld_gate_b', I64),
-                ('gate', P)]
+                ('gate', P), ('gain', P)]
 
 
 class Rope(C.Structure):

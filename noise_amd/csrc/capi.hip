@@ -25,7 +25,7 @@ int check_launch(const char* what) {
 }  // namespace noise
 
 extern "C" const char* noise_last_error(void) { return noise::g_error; }
-extern "C" int noise_abi_version(void) { return 1; }
+extern "C" int noise_abi_version(void) { return 2; }
 
 __global__ void cast_bf16_kernel(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ hi,
                                  uint16_t* __restrict__ lo) {

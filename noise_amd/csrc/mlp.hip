@@ -897,6 +897,8 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
                   "mlp_fused: next gate needs its output and perturbation vectors");
     NOISE_REQUIRE(((uintptr_t)nx.h % 16) == 0, "mlp_fused: next h must be 16-byte aligned");
     NOISE_REQUIRE(nx.member_shift >= 0 && nx.member_shift < 31, "mlp_fused: next mix_norm has a bad member_shift");
+    NOISE_REQUIRE(!nx.gain, "mlp_fused: the next mix_norm's gain is not supported in the fused epilogue "
+                  "(the reference's norm has none); run noise_mix_norm for it");
     if (g.attn_y) {
       if (nx.x0) mlp_fused_kernel<true, true, 2, true><<<grid, 256, 0, st>>>(g, nx);
       else mlp_fused_kernel<true, true, 1, true><<<grid, 256, 0, st>>>(g, nx);

@@ -116,9 +116,17 @@ NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, int row, int lane, float (
   const float rr = rsqrtf(ss * (1.0f / D) + 1.1920928955078125e-07f);
   float h[8];
   uint32_t packed[4];
+  if (g.gain) {  // F.rms_norm's weight: (x rr) gain
+    float gn[8];
+    load8(g.gain + c, gn);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) packed[k] = pack_bf2(v[2 * k] * rr * gn[2 * k], v[2 * k + 1] * rr * gn[2 * k + 1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) packed[k] = pack_bf2(v[2 * k] * rr, v[2 * k + 1] * rr);
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    packed[k] = pack_bf2(v[2 * k] * rr, v[2 * k + 1] * rr);
     h[2 * k] = bf_lo(packed[k]);
     h[2 * k + 1] = bf_hi(packed[k]);
   }
@@ -296,6 +304,7 @@ extern "C" int noise_mix_norm(const noise_mixnorm_t* args, void* stream) {
   NOISE_REQUIRE(!(g.x0 && g.sign) || (g.eps_resid && g.eps_mix), "mix_norm: perturbed mixing needs eps");
   NOISE_REQUIRE(!g.gate_w || (g.gate && (!g.sign || (g.gate_a && g.gate_b && g.ld_gate_b % 4 == 0))),
                 "mix_norm: gate needs output and perturbation vectors");
+  NOISE_REQUIRE(((uintptr_t)g.gain % 16) == 0, "mix_norm: gain must be 16-byte aligned");
   if (g.M == 0) return NOISE_OK;
   mix_norm_kernel<<<(g.M + 3) / 4, 256, 0, (hipStream_t)stream>>>(g);
   return noise::check_launch("mix_norm");

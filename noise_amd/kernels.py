@@ -189,10 +189,12 @@ def embed_norm(table, idx, T, members, sign, nz, x0, x=None, idx_stride=0, next_
 
 
 def mix_norm(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,
-             bs=(), u=None, gate_w=None, gate_nz=None, gate=None):
-    """x = (lr + s er) x + (l0 + s e0) x0 (when x0 is given), h = bf16(norm x), u[:, j] = h . bs[j],
-    gate = 2 sigmoid(h[:32] (Wg + s a b^T)^T) (when gate_w is given), in one launch."""
-    run_mix_norm(mix_norm_args(x, h, T, sign, x0, resid, mix, eps_r, eps_m, shift, bs, u, gate_w, gate_nz, gate))
+             bs=(), u=None, gate_w=None, gate_nz=None, gate=None, gain=None):
+    """x = (lr + s er) x + (l0 + s e0) x0 (when x0 is given), h = bf16(norm x) (times `gain` [512]
+    when given, F.rms_norm's weight), u[:, j] = h . bs[j], gate = 2 sigmoid(h[:32] (Wg + s a b^T)^T)
+    (when gate_w is given), in one launch."""
+    run_mix_norm(mix_norm_args(x, h, T, sign, x0, resid, mix, eps_r, eps_m, shift, bs, u, gate_w, gate_nz, gate,
+                               gain))
 
 
 def run_mix_norm(g):
@@ -200,9 +202,13 @@ def run_mix_norm(g):
 
 
 def mix_norm_args(x, h, T, sign=None, x0=None, resid=None, mix=None, eps_r=None, eps_m=None, shift=0,
-                  bs=(), u=None, gate_w=None, gate_nz=None, gate=None):
+                  bs=(), u=None, gate_w=None, gate_nz=None, gate=None, gain=None):
     """The MixNorm launch record of `mix_norm`, for run_mix_norm or mlp_fused(next_norm=...)."""
     g = MixNorm()
+    if gain is not None:
+        _need(gain.dtype == torch.float32 and gain.shape == (512,) and gain.is_contiguous() and gain.device == x.device,
+              'mix_norm: gain must be a contiguous float32 [512] tensor on the rows\' device')
+        g.gain = gain.data_ptr()
     g.x, g.x0, g.M, g.T, g.member_shift = x.data_ptr(), _ptr(x0), x.shape[0], T, shift
     g.sign = _ptr(sign)
     g.resid, g.mix = _ptr(resid), _ptr(mix)
@@ -284,6 +290,11 @@ def head_ce(h, w_hi, w_lo, T, targets, ce, sign=None, nz=None, u=None, targets_s
     if sign is not None:
         g.sign, g.a, g.lda, g.u, g.member_shift = (sign.data_ptr(), nz.a.data_ptr(), nz.a.stride(0),
                                                    u.data_ptr(), nz.shift)
+    members = -(-g.M // T) if g.M else 0
+    _need(targets.dtype == torch.int64 and targets.is_contiguous() and ce.numel() >= g.M and
+          (members == 0 or targets.numel() >= (members - 1) * targets_stride + T),
+          'head_ce: targets must be contiguous int64 covering (members - 1) * targets_stride + T entries '
+          '(targets_stride 0: one sequence shared by every member), ce [M]')
     g.targets, g.targets_stride, g.ce = targets.data_ptr(), targets_stride, ce.data_ptr()
     g.ignore_index = ignore_index
     if logits is not None:

@@ -14,6 +14,9 @@ from oracle import model_ref as R
 pytestmark = pytest.mark.gpu
 
 
+EPS32 = torch.finfo(torch.float32).eps
+
+
 def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
@@ -732,6 +735,50 @@ def test_config2_attention_full_size(device, window):
         yy = y[p * T:(p + 1) * T, h * 64:(h + 1) * 64].double().cpu()
         want = torch.stack([yy.mean(0), yy.square().mean(0)])
         torch.testing.assert_close(mom[p, h].double().cpu(), want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize('split', [False, True])
+def test_config3_norm_gain_then_head(device, split):
+    """Config 3's RMSNorm with a gain ~ U(0.9, 1.1) (F.rms_norm's weight; the reference's own `norm`,
+    utils/model.py:46-47, has none): mix_norm with `gain` forms h = bf16(norm(x) gain) and the
+    head's dot u = h . b, then the head's CE on h. h against the float64 F.rms_norm within one bf16
+    rounding, u and the CE of 256 sampled rows against float64 on the kernel's h; 64 members x 2048
+    tokens, perturbed (sigma = 1e-3), Zipf targets."""
+    from noise_amd.synthetic import zipf_tokens
+    members, T, V = 64, 2048, 4096
+    M = members * T
+    g = torch.Generator(device=device).manual_seed(31)
+    x = torch.randn(M, 512, device=device, generator=g) * 3.0
+    gc = _gen(34)
+    gain = (torch.rand(512, generator=gc) * 0.2 + 0.9)
+    W = torch.randn(V, 512, generator=gc) / math.sqrt(512)
+    a = torch.randn(members // 2, V, generator=gc)
+    b = torch.randn(members // 2, 512, generator=gc)
+    sign = torch.tensor([1e-3, -1e-3]).repeat(members // 2)
+    targets = zipf_tokens(T, seed=6)
+    h = torch.empty(M, 512, dtype=torch.bfloat16, device=device)
+    u = torch.empty(M, 1, device=device)
+    nk.mix_norm(x, h, T, sign.to(device), shift=1, bs=(b.to(device),), u=u, gain=gain.to(device))
+    hi = torch.empty(V, 512, dtype=torch.bfloat16, device=device)
+    lo = torch.empty_like(hi) if split else None
+    nk.cast_bf16(W.to(device), hi, lo)
+    ce = torch.empty(M, device=device)
+    # one target sequence shared by every member (stride 0)
+    nk.head_ce(h, hi, lo, T, targets.to(device), ce, sign.to(device), NoiseRows(a=a.to(device), shift=1), u.view(-1))
+    torch.cuda.synchronize()
+    rows = torch.randint(0, M, (256,), generator=gc)
+    xr = x[rows.to(device)].double().cpu()
+    want_h = torch.nn.functional.rms_norm(xr, (512,), weight=gain.double(), eps=EPS32)
+    closed = xr * torch.rsqrt(xr.square().mean(1, keepdim=True) + EPS32) * gain.double()
+    torch.testing.assert_close(want_h, closed, rtol=1e-12, atol=0)  # the weight multiplies the normed rows
+    hr = h[rows.to(device)].double().cpu()
+    assert float(((hr - want_h).abs() / want_h.abs().clamp_min(1e-30)).max()) <= 2 ** -8
+    assert float((hr - want_h.to(torch.bfloat16).double()).abs().gt(0).double().mean()) < 0.01
+    p = rows // T
+    torch.testing.assert_close(u[rows.to(device), 0].double().cpu(), (hr * b[p // 2].double()).sum(1), rtol=1e-5, atol=1e-4)
+    Wd = W.double() if split else W.to(torch.bfloat16).double()
+    z = hr @ Wd.t() + (sign[p].double() * u[rows.to(device), 0].double().cpu())[:, None] * a[p // 2].double()
+    torch.testing.assert_close(ce[rows.to(device)].double().cpu(), R.softcap_ce(z, targets[rows % T]), rtol=0, atol=5e-5)
 
 
 @pytest.mark.parametrize('split', [False, True])

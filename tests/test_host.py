@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_lib.exported_symbols())
-    assert lib.noise_abi_version() == 1
+    assert lib.noise_abi_version() == 2  # 2: noise_mixnorm_t.gain
 
 
 def test_argument_errors_raise_before_launch():
@@ -119,6 +119,18 @@ def test_step_entry_points_reject_bad_arguments():
     _rejects(lib.noise_head_ce(C.byref(head), None), 'perturbation needs')
     head.sign, head.M = None, 0
     assert lib.noise_head_ce(C.byref(head), None) == _lib.NOISE_OK
+
+    mn = _lib.MixNorm(x=fake, M=256, T=256, h=fake, gain=odd)
+    _rejects(lib.noise_mix_norm(C.byref(mn), None), 'gain must be 16-byte aligned')
+    mn.gain, mn.M = fake, 0
+    assert lib.noise_mix_norm(C.byref(mn), None) == _lib.NOISE_OK
+    # the fused MLP's epilogue does not take a gain (the reference's norm has none)
+    mn.M, mn.T = 512, 256
+    mlp_next = _lib.Mlp(in_=fake, ld_in=512, member_stride_in=256 * 512, out=fake, ld_out=512,
+                        member_stride_out=256 * 512, T=256, members=2,
+                        flags=_lib.MLP_NORM | _lib.MLP_RESIDUAL, w_fc=fake, w_proj=fake, next=C.pointer(mn))
+    mn.x = fake
+    _rejects(lib.noise_mlp_fused(C.byref(mlp_next), None), 'gain')
 
     att = _lib.Attention(qkv=fake, ldqkv=1536, y=fake, members=2, T=256, heads=4, window=1024, scale=0.125)
     _rejects(lib.noise_window_attention(C.byref(att), None), 'heads == 8')
