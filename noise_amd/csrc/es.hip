@@ -102,9 +102,10 @@ __global__ __launch_bounds__(FT) void fitness_ranks_kernel(const float* __restri
   if (tid == 0 && status) *status = nbad > 0.f ? NOISE_ENONFINITE : NOISE_OK;
 }
 
-// 64 x 64 output tile per workgroup of 256 threads, 4 x 4 outputs per thread, 32 pairs per stage.
-// The next stage's scaled noise goes global -> registers while the current one is summed from
-// one of two LDS buffers (one barrier per stage). Every output sums its pairs in ascending order.
+// 64 x 64 output tile per workgroup of 256 threads (four waves of 32 x 32, fp32 MFMA), 32 pairs
+// per stage. The next stage's scaled noise goes global -> registers while the current one is
+// summed from one of two LDS buffers (one barrier per stage). Every output sums its pairs in a
+// fixed order (ascending pairs, two per MFMA).
 // With splits > 1, workgroup z sums pairs [z per, (z + 1) per) into its own slice of `partial`
 // and es_gradient_reduce_kernel adds the slices in order: the same sums on every run.
 __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restrict__ w, int n,
@@ -120,8 +121,11 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
   __shared__ __attribute__((aligned(16))) float Bs[2][SJ][64];
   const int tid = threadIdx.x;
   const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
-  const int tx = tid & 15, ty = tid >> 4;
-  float acc[4][4] = {};
+  // wave (wo, wi) owns the 32 x 32 output block (o0 + 32 wo, i0 + 32 wi): v_mfma_f32_32x32x2_f32,
+  // fp32 products and fp32 sums, two pairs per MFMA (lane l: A row l % 32 / B column l % 32 at
+  // pair 2 kk + l / 32; accumulator v: row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32)
+  const int lane = tid & 63, wv = tid >> 6, wo = wv >> 1, wi = wv & 1;
+  floatx16 acc = {};
   // loader: pair lj of the stage, columns lc .. lc + 7
   const int lj = tid >> 3, lc = (tid & 7) * 8;
   const int jb = blockIdx.z * per, je = min(n, jb + per);  // this workgroup's pairs
@@ -149,32 +153,22 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
     stash(buf);
     if (j0 + SJ < je) fetch(j0 + SJ);
     __syncthreads();
-#pragma unroll 8
-    for (int jj = 0; jj < SJ; ++jj) {
-      const float4 a4 = *reinterpret_cast<const float4*>(&As[buf][jj][ty * 4]);
-      const float4 b4 = *reinterpret_cast<const float4*>(&Bs[buf][jj][tx * 4]);
-      const float ar[4] = {a4.x, a4.y, a4.z, a4.w}, br[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] += ar[r] * br[c];
-    }
+    for (int kk = 0; kk < SJ / 2; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[buf][2 * kk + (lane >> 5)][wo * 32 + (lane & 31)],
+                                                  Bs[buf][2 * kk + (lane >> 5)][wi * 32 + (lane & 31)], acc, 0, 0, 0);
   }
+  const int i = i0 + wi * 32 + (lane & 31);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int o = o0 + ty * 4 + r;
-    if (o >= out) continue;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int i = i0 + tx * 4 + c;
-      if (i >= in) continue;
-      if (partial) {
-        partial[((int64_t)blockIdx.z * out + o) * in + i] = acc[r][c];
-      } else {
-        float* dst = G + (int64_t)o * in + i;
-        const float v = scale * acc[r][c];
-        *dst = accumulate ? *dst + v : v;
-      }
+  for (int v = 0; v < 16; ++v) {
+    const int o = o0 + wo * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+    if (o >= out || i >= in) continue;
+    if (partial) {
+      partial[((int64_t)blockIdx.z * out + o) * in + i] = acc[v];
+    } else {
+      float* dst = G + (int64_t)o * in + i;
+      const float x = scale * acc[v];
+      *dst = accumulate ? *dst + x : x;
     }
   }
 }
