@@ -96,6 +96,10 @@ NOISE_DEV void load_stage(const noise_mlp_t& g, unsigned char* lds, int wave, in
   }
 }
 
+// Zero-initialised device memory: the source of the staged vectors a launch does not have
+// (unperturbed members, absent dots or gate), so that every piece is one direct load.
+__device__ __align__(16) float kZeroRow[256];
+
 // A copy of an accumulator register the compiler cannot reuse: without it the prologue kept VGPR
 // copies of all 256 input values alive between its two passes over them and spilled.
 NOISE_DEV float agpr_read(float a) {
@@ -544,6 +548,35 @@ mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
     load_stage(g, lds, wave, lane, 0, 0, -1, c0);
   }
 
+  // The member's perturbation rows (a_fc | b_proj | a_proj | b_fc, 20 pieces of 256 floats, five
+  // a wave; zeros when unperturbed, so the rank-1 terms vanish without a branch in the main loop)
+  // and, with NEXT, the next norm's vectors (b[0..2], gate W, gate b) go straight into LDS by
+  // direct loads issued before anything else: they land under the row loads and the attention
+  // c_proj, and the waits that complete those cover them (vector memory loads retire in order);
+  // the barriers that follow (the attention chunks' or the one after the norm) publish them.
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const int pc = 5 * wave + k;
+    const float* src = !pert   ? kZeroRow
+                       : pc < 8  ? g.a_fc + pn * g.ld_a_fc + 256 * pc
+                       : pc < 16 ? g.b_proj + pn * g.ld_b_proj + 256 * (pc - 8)
+                       : pc < 18 ? g.a_proj + pn * g.ld_a_proj + 256 * (pc - 16)
+                                 : g.b_fc + pn * g.ld_b_fc + 256 * (pc - 18);
+    __builtin_amdgcn_global_load_lds((const void*)(src + 4 * lane), (void*)(lds + NOISE_OFS + pc * 1024), 16, 0, 0);
+  }
+  if constexpr (NEXT != 0) {
+    const int64_t pnx = (int64_t)(p >> nx.member_shift);
+    for (int k = wave; k < 7; k += 4) {  // pieces 0-5: b[k / 2], piece 6: gate W
+      const float* src = k < 6 ? (k / 2 < nx.nb ? nx.b[k / 2] + pnx * nx.ldb + 256 * (k & 1) : kZeroRow)
+                               : (nx.gate_w ? nx.gate_w : kZeroRow);
+      __builtin_amdgcn_global_load_lds((const void*)(src + 4 * lane), (void*)(lds + NEXT_OFS + k * 1024), 16, 0, 0);
+    }
+    if (wave == 3 && lane < 8) {  // gate b: 32 floats
+      const float* src = nx.gate_w && nx.sign ? nx.gate_b + pnx * nx.ld_gate_b : kZeroRow;
+      __builtin_amdgcn_global_load_lds((const void*)(src + 4 * lane), (void*)(lds + NEXT_OFS + (3 * D + 256) * 4), 16,
+                                       0, 0);
+    }
+  }
   // ---- prologue, one pass over the input: the wave's 32 rows land in the c_proj accumulator
   // layout (lane l holds column 32 nb + l % 32 of rows 8 (j / 4) + 4 (l / 32) + j % 4), where they
   // also start the residual sum.
@@ -620,41 +653,6 @@ mlp_fused_kernel(const noise_mlp_t g, const noise_mixnorm_t nx) {
       for (int nb = 0; nb < 16; ++nb) {
         const float v = agpr_read(acc[nb][j]);
         ps[j] += v * v;
-      }
-    }
-  }
-
-  // The member's perturbation rows, 5120 floats (20 per thread); zeros when unperturbed, so the
-  // rank-1 terms vanish without a branch in the main loop.
-#pragma unroll
-  for (int k = 0; k < 5; ++k) {
-    const int e = (k * 256 + tid) * 4;  // 0 .. 5116
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (pert) {
-      const float* src = e < F ? g.a_fc + pn * g.ld_a_fc + e
-                       : e < 2 * F ? g.b_proj + pn * g.ld_b_proj + (e - F)
-                       : e < 2 * F + D ? g.a_proj + pn * g.ld_a_proj + (e - 2 * F)
-                                       : g.b_fc + pn * g.ld_b_fc + (e - 2 * F - D);
-      v = *reinterpret_cast<const float4*>(src);
-    }
-    *reinterpret_cast<float4*>(s_afc + e) = v;
-  }
-  if constexpr (NEXT != 0) {  // the next mix_norm's vectors (zeros where absent)
-    float* s_next = reinterpret_cast<float*>(lds + NEXT_OFS);
-    const int64_t pnx = (int64_t)(p >> nx.member_shift);
-#pragma unroll
-    for (int k = 0; k < (NEXT_FLOATS + 255) / 256; ++k) {
-      const int e = k * 256 + tid;
-      if (e < NEXT_FLOATS) {
-        float v = 0.f;
-        if (e < 3 * D) {
-          if (e / D < nx.nb) v = nx.b[e / D][pnx * nx.ldb + e % D];
-        } else if (e < 3 * D + 256) {
-          if (nx.gate_w) v = nx.gate_w[e - 3 * D];
-        } else if (nx.gate_w && nx.sign) {
-          v = nx.gate_b[pnx * nx.ld_gate_b + (e - 3 * D - 256)];
-        }
-        s_next[e] = v;
       }
     }
   }
@@ -890,7 +888,12 @@ extern "C" int noise_mlp_fused(const noise_mlp_t* args, void* stream) {
                   "mlp_fused: the next mix_norm must cover exactly the output rows, [members * T, 512] contiguous");
     NOISE_REQUIRE(nx.nb >= 0 && nx.nb <= 3 && (nx.nb == 0 || (nx.u && nx.ldu >= nx.nb && nx.ldb >= D)),
                   "mlp_fused: next mix_norm dots need u, ldu >= nb and ldb >= 512");
-    for (int j = 0; j < nx.nb; ++j) NOISE_REQUIRE(nx.b[j], "mlp_fused: next mix_norm has a null b[%d]", j);
+    for (int j = 0; j < nx.nb; ++j)
+      NOISE_REQUIRE(nx.b[j] && ((uintptr_t)nx.b[j] % 16) == 0 && nx.ldb % 4 == 0,
+                    "mlp_fused: next mix_norm b[%d] must be non-null with 16-byte aligned rows", j);
+    NOISE_REQUIRE(((uintptr_t)nx.gate_w % 16) == 0 && (!nx.gate_w || !nx.sign ||
+                                                      (((uintptr_t)nx.gate_b % 16) == 0 && nx.ld_gate_b % 4 == 0)),
+                  "mlp_fused: next gate W and b must be 16-byte aligned");
     NOISE_REQUIRE(!nx.x0 || (nx.resid && nx.mix && (!nx.sign || (nx.eps_resid && nx.eps_mix))),
                   "mlp_fused: next mixing needs the lambda scalars (and eps when perturbed)");
     NOISE_REQUIRE(!nx.gate_w || (nx.gate && (!nx.sign || (nx.gate_a && nx.gate_b))),
