@@ -43,7 +43,126 @@ NOISE_DEV void store8(float* p, const float (&v)[8]) {
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, int row, int lane, float (&v)[8], const float (&v0)[8]);
+// The values mix_norm needs besides the row itself, all of them the same for every row of a member
+// (or of the launch): loaded at the start of a row's wave, next to the row's own loads, so that
+// their latency overlaps instead of following the row's stores.
+struct MixPre {
+  float s, lr, l0;     // sign; the mixing factors (lr + s er), (l0 + s e0)
+  float bv[3][8];      // the dot vectors' columns 8 lane .. + 7
+  float gn[8];         // the gain's columns (1 without a gain)
+  float wv[8];         // gate: W row lane / 4, block lane % 4 (lanes < 32), or b_gate (lanes >= 32)
+  float ga;            // gate: a_gate[q] of lane q * 4 (lanes < 32)
+};
+
+NOISE_DEV MixPre mix_pre(const noise_mixnorm_t& g, int row, int lane) {
+  MixPre m;
+  const int p = row / g.T;
+  const int64_t pn = p >> g.member_shift;
+  const int c = lane * 8;
+  m.s = g.sign ? g.sign[p] : 0.f;
+  m.lr = 1.f;
+  m.l0 = 0.f;
+  if (g.x0) {
+    m.lr = *g.resid;
+    m.l0 = *g.mix;
+    if (g.sign) {
+      m.lr += m.s * g.eps_resid[pn * g.ld_eps];
+      m.l0 += m.s * g.eps_mix[pn * g.ld_eps];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (j < g.nb) {
+      load8(g.b[j] + pn * g.ldb + c, m.bv[j]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m.bv[j][k] = 0.f;
+    }
+  }
+  if (g.gain) {
+    load8(g.gain + c, m.gn);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m.gn[k] = 1.f;
+  }
+  m.ga = 0.f;
+  if (g.gate_w) {
+    const int blk = lane & 3;
+    if (lane < 32) {
+      load8(g.gate_w + (lane >> 2) * 32 + blk * 8, m.wv);
+      if (g.sign) m.ga = g.gate_a[pn * g.ld_gate_a + (lane >> 2)];
+    } else if (g.sign) {
+      load8(g.gate_b + pn * g.ld_gate_b + blk * 8, m.wv);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m.wv[k] = 0.f;
+    }
+  }
+  return m;
+}
+
+// mix_norm of one row (one wavefront, lane l: columns 8 l .. 8 l + 7) from its x values v and, when
+// mixing, its x0 values v0.
+NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, const MixPre& m, int row, int lane, float (&v)[8],
+                            const float (&v0)[8]) {
+  const int c = lane * 8;
+  if (g.x0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = m.lr * v[k] + m.l0 * v0[k];
+    store8(g.x + (int64_t)row * D + c, v);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ss += v[k] * v[k];
+  ss = wave_sum_dpp(ss);
+  const float rr = rsqrtf(ss * (1.0f / D) + 1.1920928955078125e-07f);
+  float h[8];
+  uint32_t packed[4];
+  if (g.gain) {  // F.rms_norm's weight: (x rr) gain
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      packed[k] = pack_bf2(v[2 * k] * rr * m.gn[2 * k], v[2 * k + 1] * rr * m.gn[2 * k + 1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) packed[k] = pack_bf2(v[2 * k] * rr, v[2 * k + 1] * rr);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    h[2 * k] = bf_lo(packed[k]);
+    h[2 * k + 1] = bf_hi(packed[k]);
+  }
+  *reinterpret_cast<uint4*>(g.h + (int64_t)row * D + c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (j >= g.nb) break;
+    float d = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d += h[k] * m.bv[j][k];
+    d = wave_sum_dpp(d);
+    if (lane == 0) g.u[(int64_t)row * g.ldu + j] = d;
+  }
+  if (g.gate_w) {
+    // Channels 0..31 live in lanes 0..3 (8 each). Lane l < 32 forms the partial logit of gate
+    // l / 4 over channel block l % 4; lanes 32..63 form the same block's partial dot with the
+    // gate's noise vector b (replicated eight times). Both are summed over the 4 lanes of a group.
+    const int blk = lane & 3;
+    float hb[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) hb[k] = __shfl(h[k], blk, 64);
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) part += hb[k] * m.wv[k];
+    part = group_sum(part, 4);
+    const float nd = __shfl(part, 32, 64);  // h[:32] . b_gate
+    if (lane < 32 && blk == 0) {
+      const int q = lane >> 2;
+      float z = part;
+      if (g.sign) z += m.s * nd * m.ga;
+      g.gate[(int64_t)row * 8 + q] = 2.0f / (1.0f + expf(-z));
+    }
+  }
+}
+
 
 // NEXT: the first layer's mix_norm (noise_mixnorm_t `nx`, mixing with x0 = this row) follows on
 // the row still in registers; it writes the stream nx.x instead of the plain copy x.
@@ -56,6 +175,8 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
+  MixPre m;
+  if constexpr (NEXT) m = mix_pre(nx, row, lane);
   const int p = row / T, t = row - p * T;
   const int64_t tok = idx[p * idx_stride + t];
   const int c = lane * 8;
@@ -86,89 +207,9 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(
     float w[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) w[k] = v[k];
-    mix_norm_row(nx, row, lane, w, v);
+    mix_norm_row(nx, m, row, lane, w, v);
   } else {
     if (x) store8(x + (int64_t)row * D + c, v);
-  }
-}
-
-// mix_norm of one row (one wavefront, lane l: columns 8 l .. 8 l + 7) from its x values v and, when
-// mixing, its x0 values v0.
-NOISE_DEV void mix_norm_row(const noise_mixnorm_t& g, int row, int lane, float (&v)[8], const float (&v0)[8]) {
-  const int p = row / g.T;
-  const int64_t pn = p >> g.member_shift;
-  const float s = g.sign ? g.sign[p] : 0.f;
-  const int c = lane * 8;
-  if (g.x0) {
-    float r = *g.resid, m = *g.mix;
-    if (g.sign) {
-      r += s * g.eps_resid[pn * g.ld_eps];
-      m += s * g.eps_mix[pn * g.ld_eps];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = r * v[k] + m * v0[k];
-    store8(g.x + (int64_t)row * D + c, v);
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) ss += v[k] * v[k];
-  ss = wave_sum_dpp(ss);
-  const float rr = rsqrtf(ss * (1.0f / D) + 1.1920928955078125e-07f);
-  float h[8];
-  uint32_t packed[4];
-  if (g.gain) {  // F.rms_norm's weight: (x rr) gain
-    float gn[8];
-    load8(g.gain + c, gn);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) packed[k] = pack_bf2(v[2 * k] * rr * gn[2 * k], v[2 * k + 1] * rr * gn[2 * k + 1]);
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) packed[k] = pack_bf2(v[2 * k] * rr, v[2 * k + 1] * rr);
-  }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    h[2 * k] = bf_lo(packed[k]);
-    h[2 * k + 1] = bf_hi(packed[k]);
-  }
-  *reinterpret_cast<uint4*>(g.h + (int64_t)row * D + c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  for (int j = 0; j < g.nb; ++j) {
-    float bv[8];
-    load8(g.b[j] + pn * g.ldb + c, bv);
-    float d = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) d += h[k] * bv[k];
-    d = wave_sum_dpp(d);
-    if (lane == 0) g.u[(int64_t)row * g.ldu + j] = d;
-  }
-  if (g.gate_w) {
-    // Channels 0..31 live in lanes 0..3 (8 each). Lane l < 32 forms the partial logit of gate
-    // l / 4 over channel block l % 4; lanes 32..63 form the same block's partial dot with the
-    // gate's noise vector b (replicated eight times). Both are summed over the 4 lanes of a group.
-    const int blk = lane & 3;
-    float hb[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) hb[k] = __shfl(h[k], blk, 64);
-    const bool noise_lane = lane >= 32;
-    float wv[8];
-    if (!noise_lane) {
-      load8(g.gate_w + (lane >> 2) * 32 + blk * 8, wv);
-    } else if (g.sign) {
-      load8(g.gate_b + pn * g.ld_gate_b + blk * 8, wv);
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) wv[k] = 0.f;
-    }
-    float part = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) part += hb[k] * wv[k];
-    part = group_sum(part, 4);
-    const float nd = __shfl(part, 32, 64);  // h[:32] . b_gate
-    if (!noise_lane && blk == 0) {
-      const int q = lane >> 2;
-      float z = part;
-      if (g.sign) z += s * nd * g.gate_a[pn * g.ld_gate_a + q];
-      g.gate[(int64_t)row * 8 + q] = 2.0f / (1.0f + expf(-z));
-    }
   }
 }
 
@@ -176,10 +217,11 @@ __global__ __launch_bounds__(256) void mix_norm_kernel(const noise_mixnorm_t g) 
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= g.M) return;
+  const MixPre m = mix_pre(g, row, lane);
   float v[8], v0[8];
   load8(g.x + (int64_t)row * D + lane * 8, v);
   if (g.x0) load8(g.x0 + (int64_t)row * D + lane * 8, v0);
-  mix_norm_row(g, row, lane, v, v0);
+  mix_norm_row(g, m, row, lane, v, v0);
 }
 
 // One wavefront per row of the [M, 1536] fp32 q | k | v block.
