@@ -47,7 +47,7 @@ def test_step_kernels_spill_within_budget_and_never_in_a_loop(name, tmp_path):
                 checked += 1
     assert checked > 0
     loops, bad = A.loop_scratch(asm)
-    assert loops > 0
+    assert loops > 0 or name == 'norm'  # norm.hip's row kernels are straight-line code
     assert [b for b in bad if any(key in b[0] for key in SPILL_BUDGET)] == []
 
 
