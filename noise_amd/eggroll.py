@@ -30,6 +30,7 @@ SEED = 0
 SIGMA = 0.002
 CHUNK = 256
 NOISE = 2 ** 28
+GRAD_STREAMS = 8
 
 
 class Eggroll:
@@ -58,7 +59,11 @@ class Eggroll:
             self.grads[name] = self.grad_flat[off:off + n].view(shape)
             off += n
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self.grad_work = None  # es_gradient's split-sum workspace, sized on the first step
+        # The parameters' gradients are independent launches of small grids: they go round-robin
+        # to GRAD_STREAMS side streams (default priority), each with its own split-sum workspace,
+        # sized on the first step, and join the step's stream before the host sync.
+        self.grad_streams = [torch.cuda.Stream(device=self.device) for _ in range(GRAD_STREAMS)]
+        self.grad_work = [None] * GRAD_STREAMS
         self._layout = None    # column layout of the per-chunk noise gather
 
     def offsets(self, step):
@@ -116,6 +121,34 @@ class Eggroll:
                                 losses[lo:lo + n])
         return losses
 
+    def gradient(self, weight, offsets, n):
+        """grads[name] = -1/n sum_p weight[p] a_p^T b_p (or eps_p) for every parameter (eggroll.py:155-166).
+
+        The launches are issued after the work already on the current stream (the fitness weights)
+        and the current stream waits for all of them before its next work."""
+        pairs = self.pairs
+        need = max(K.es_gradient_work(pairs, s[0], s[1] if len(s) == 2 else 1) for s in self.shapes.values())
+        for i, w in enumerate(self.grad_work):
+            if w is None or w.numel() < need:
+                self.grad_work[i] = torch.empty(max(need, 1), device=self.device)
+        main = torch.cuda.current_stream(self.device)
+        ready = torch.cuda.Event()
+        ready.record(main)  # the fitness weights
+        for i, (name, shape) in enumerate(self.shapes.items()):
+            side = self.grad_streams[i % len(self.grad_streams)]
+            side.wait_event(ready)
+            with torch.cuda.stream(side):
+                off = offsets[name]
+                work = self.grad_work[i % len(self.grad_streams)]
+                if len(shape) == 2:
+                    K.es_gradient(weight, self.buffer, off, self.buffer, off + shape[0], shape[0], shape[1],
+                                  -1.0 / n, self.grads[name], work=work)
+                else:
+                    K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name],
+                                  work=work)
+        for side in self.grad_streams:
+            main.wait_stream(side)
+
     @torch.no_grad()
     def step(self, x, y, optimizer, step):
         """Evaluate this rank's share of the population, gather the losses, rebuild the update."""
@@ -131,17 +164,7 @@ class Eggroll:
         weight = torch.empty(pairs, device=self.device)
         ranked = torch.empty(n, device=self.device) if self.fitness == 'ranks' else None
         K.fitness(losses, pairs, weight, self.status, self.fitness, ranked)
-        need = max(K.es_gradient_work(pairs, s[0], s[1] if len(s) == 2 else 1) for s in self.shapes.values())
-        if self.grad_work is None or self.grad_work.numel() < need:
-            self.grad_work = torch.empty(max(need, 1), device=self.device)
-        for name, shape in self.shapes.items():
-            off = offsets[name]
-            if len(shape) == 2:
-                K.es_gradient(weight, self.buffer, off, self.buffer, off + shape[0], shape[0], shape[1], -1.0 / n,
-                              self.grads[name], work=self.grad_work)
-            else:
-                K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name],
-                              work=self.grad_work)
+        self.gradient(weight, offsets, n)
         # One host sync per step: the status and the mean loss come back together, before the
         # weights move (the reference reads only the mean, eggroll.py:168).
         status, mean = torch.stack([self.status[0].to(torch.float32), losses.mean()]).tolist()

@@ -372,3 +372,22 @@ def test_eggroll_step_multi_sequence(device, init_params, mode):
         ref = before[name].clone()
         es_ref.adamw_step(ref, es.grads[name].cpu(), torch.zeros_like(ref), torch.zeros_like(ref), 1, 1e-3, (0.5, 0.95))
         torch.testing.assert_close(p.detach().cpu(), ref, rtol=0, atol=2e-6)
+
+
+def test_eggroll_gradient_side_streams_match_one_stream(device, init_params):
+    """Eggroll.gradient spreads the per-parameter launches over side streams, each with its own
+    split-sum workspace; the result is bit-identical to issuing them all on the current stream,
+    and the current stream sees every gradient (read right after the call, with no extra sync)."""
+    model = noise_amd.make_model(device, 0)
+    es = noise_amd.Eggroll(model, pairs=512, noise_size=1 << 24)
+    assert len(es.grad_streams) > 1
+    offsets = es.offsets(3)
+    weight = torch.randn(512, generator=torch.Generator().manual_seed(5)).to(device)
+    es.grad_flat.fill_(float('nan'))
+    es.gradient(weight, offsets, 512)
+    spread = es.grad_flat.clone()
+    es.grad_streams, es.grad_work = [torch.cuda.current_stream(device)], [None]
+    es.grad_flat.fill_(float('nan'))
+    es.gradient(weight, offsets, 512)
+    assert torch.isfinite(spread).all()
+    assert torch.equal(spread, es.grad_flat)
