@@ -69,6 +69,9 @@ struct AttnSmem {
   float mom[NW][2][64];                // per-wave moment partials
 };
 
+// MOM: the per-(member, head) moments of y are requested (the population step asks for none, and
+// then the kernel forms none).
+template <bool MOM>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void window_attention_kernel(const noise_attention_t g) {
   __shared__ __attribute__((aligned(16))) AttnSmem sm;
@@ -276,9 +279,9 @@ void window_attention_kernel(const noise_attention_t g) {
   // ---- epilogue: normalise, stage bf16 y through LDS for whole-row stores, dot with b_proj,
   // moments. Wave w stages its 32 x 64 tile at 4 KB offset w.
   uint16_t* ys = &sm.kv[0][0][0] + w * 32 * LDK;
-  float mom[64];
+  float mom[MOM ? 64 : 1];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) mom[i] = 0.f;
+  for (int i = 0; i < (MOM ? 64 : 1); ++i) mom[i] = 0.f;
   const int64_t pn = p >> g.member_shift;
   {
     const int qi = wq0 + q32;
@@ -306,10 +309,12 @@ void window_attention_kernel(const noise_attention_t g) {
             const float4 bv = *reinterpret_cast<const float4*>(g.b_proj + pn * g.ld_b_proj + h * 64 + dim);
             dot += y[0] * bv.x + y[1] * bv.y + y[2] * bv.z + y[3] * bv.w;
           }
+          if constexpr (MOM) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            mom[db * 16 + jg * 4 + e] += y[e];
-            mom[32 + db * 16 + jg * 4 + e] += y[e] * y[e];
+            for (int e = 0; e < 4; ++e) {
+              mom[db * 16 + jg * 4 + e] += y[e];
+              mom[32 + db * 16 + jg * 4 + e] += y[e] * y[e];
+            }
           }
         }
       }
@@ -327,7 +332,7 @@ void window_attention_kernel(const noise_attention_t g) {
       *reinterpret_cast<u32x4*>(g.y + (rowbase + wq0 + row) * 512 + h * 64 + c8) =
           *reinterpret_cast<const u32x4*>(&ys[swz(row, c8)]);
   }
-  if (g.moments) {
+  if constexpr (MOM) {
     halfwave_transpose_sum(mom, lane);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -375,7 +380,8 @@ extern "C" int noise_window_attention(const noise_attention_t* args, void* strea
   NOISE_REQUIRE(blocks < (1ll << 31), "window_attention: too many workgroups");
   if (blocks == 0) return NOISE_OK;
   hipStream_t st = (hipStream_t)stream;
-  window_attention_kernel<<<(int)blocks, NTH, 0, st>>>(g);
+  if (g.moments) window_attention_kernel<true><<<(int)blocks, NTH, 0, st>>>(g);
+  else window_attention_kernel<false><<<(int)blocks, NTH, 0, st>>>(g);
   int rc = noise::check_launch("window_attention");
   if (rc || !g.moments) return rc;
   moments_finalize_kernel<<<g.members * g.heads, 128, 0, st>>>(g.scratch, nqb, g.T, g.moments);
