@@ -151,10 +151,10 @@ void window_attention_kernel(const noise_attention_t g) {
         : "memory");                                                                          \
   }
   // Wave w fetches rows 8w .. 8w + 7 of the K and the V tile of a block, one instruction each.
-#define NOISE_ATT_LOAD(BLK)                                                                    \
+#define NOISE_ATT_LOAD(BLK, ST)                                                                \
   {                                                                                           \
     const int blk_ = (BLK);                                                                   \
-    const int st_ = blk_ % NSTAGE;                                                            \
+    constexpr int st_ = (ST);                                                                 \
     const int r_ = 8 * w + (lane >> 3), pc_ = lane & 7;                                       \
     int key_ = kfirst + blk_ * BKEY + r_;                                                     \
     key_ = key_ < T ? key_ : T - 1;                                                           \
@@ -194,16 +194,16 @@ void window_attention_kernel(const noise_attention_t g) {
     for (int db = 0; db < 2; ++db) vf[kk][db] = pf[kk];
   }
 
-  auto kbase = [&](int hh) { return &sm.kv[(hh >> 1) % NSTAGE][0][(hh & 1) * 32 * LDK]; };
-  auto vbase = [&](int hh) { return &sm.kv[(hh >> 1) % NSTAGE][1][(hh & 1) * 32 * LDK]; };
-  auto read_k = [&](int hh) {
-    const uint16_t* kb_ = kbase(hh);
+  // The ring stage of every read is a compile-time constant (the block loop below is unrolled over
+  // the NSTAGE stages), so each fragment address is the lane's offset plus an immediate.
+  auto read_k = [&]<int ST, int HF>() {
+    const uint16_t* kb_ = &sm.kv[ST][0][HF * 32 * LDK];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       kf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(kb_ + kfo[ks]));
   };
-  auto read_v = [&](int hh) {
-    const uint16_t* vb_ = vbase(hh);
+  auto read_v = [&]<int ST, int HF>() {
+    const uint16_t* vb_ = &sm.kv[ST][1][HF * 32 * LDK];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -219,19 +219,21 @@ void window_attention_kernel(const noise_attention_t g) {
         vf[kk][db] = __builtin_bit_cast(bf16x8, u);
       }
   };
-  // One half-block: QK of hh with the pending PV between its accumulation steps, the fragment
-  // reads for what follows, then the softmax of hh (its P V is issued with the next half-block,
-  // or by the drain after the loop).
-  auto step = [&](int hh, bool kpre) {
-    if (!kpre) read_k(hh);
+  // One half-block hh (= 2 b + HF of a block b in stage ST): QK of hh with the pending PV between
+  // its accumulation steps, the fragment reads for what follows, then the softmax of hh (its P V is
+  // issued with the next half-block, or by the drain after the loop).
+  auto step = [&]<int ST, int HF>(int hh, bool kpre) {
+    if (!kpre) read_k.template operator()<ST, HF>();
     floatx16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], (floatx16){}, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       o[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[i >> 1][i & 1], pf[i >> 1], o[i & 1], 0, 0, 0);
       if (i < 3) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i + 1], qf[i + 1], s, 0, 0, 0);
     }
-    read_v(hh);
-    if (!(hh & 1) && hh + 1 <= hlast) read_k(hh + 1);
+    read_v.template operator()<ST, HF>();
+    if constexpr (HF == 0) {
+      if (hh + 1 <= hlast) read_k.template operator()<ST, 1>();
+    }
     const int khalf = kfirst + hh * 32;
     const bool full = khalf + 31 <= wq0 && wq0 + 31 - khalf <= window && khalf + 32 <= T;
     if (!full) {
@@ -255,18 +257,26 @@ void window_attention_kernel(const noise_attention_t g) {
       pf[kk] = __builtin_bit_cast(bf16x8, pk);
     }
   };
-
-  NOISE_ATT_LOAD(0)
-  if (nblk > 1) NOISE_ATT_LOAD(1)
-  for (int b = 0; b < nblk; ++b) {
-    // Block b has landed for this wave (the 2 loads of block b + 1 may still fly), then for every
-    // wave; every wave is past the reads of block b - 2, whose stage takes block b + 2.
+  // Block b (in stage ST = b % NSTAGE): it has landed for this wave (the 2 loads of block b + 1 may
+  // still fly), then for every wave; every wave is past the reads of block b - 2, whose stage takes
+  // block b + 2.
+  auto block = [&]<int ST>(int b) {
     if (b + 1 < nblk) __asm__ volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
     else __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (b + 2 < nblk) NOISE_ATT_LOAD(b + 2)
+    if (b + 2 < nblk) NOISE_ATT_LOAD(b + 2, (ST + 2) % NSTAGE)
     const bool run0 = 2 * b >= hfirst && 2 * b <= hlast;
-    if (run0) step(2 * b, false);
-    if (2 * b + 1 >= hfirst && 2 * b + 1 <= hlast) step(2 * b + 1, run0);
+    if (run0) step.template operator()<ST, 0>(2 * b, false);
+    if (2 * b + 1 >= hfirst && 2 * b + 1 <= hlast) step.template operator()<ST, 1>(2 * b + 1, run0);
+  };
+
+  NOISE_ATT_LOAD(0, 0)
+  if (nblk > 1) NOISE_ATT_LOAD(1, 1)
+  static_assert(NSTAGE == 4, "the block loop is unrolled over four stages");
+  for (int b = 0; b < nblk; b += NSTAGE) {
+    block.template operator()<0>(b);
+    if (b + 1 < nblk) block.template operator()<1>(b + 1);
+    if (b + 2 < nblk) block.template operator()<2>(b + 2);
+    if (b + 3 < nblk) block.template operator()<3>(b + 3);
   }
   // the last pending P V
 #pragma unroll
