@@ -277,12 +277,14 @@ def test_qkv_rope_gemm_matches_unfused(device, T, members, shift, ve, pert):
 
 
 @pytest.mark.parametrize('T,members,shift,ve', [(256, 4, 1, True), (128, 3, 0, False), (2048, 1, 0, True),
+                                                 (512, 3, 1, False), (384, 2, 0, True),
                                                  (32, 5, 0, False), (96, 3, 1, False), (64, 8, 1, False)])
 def test_qkv_row_resident_matches_oracle(device, T, members, shift, ve):
     """The q|k|v projection against the float64 oracle directly: R.lowrank for each of q, k, v
     (rank-1 through the given x . b dots), R.rotary and R.rms_norm per head for q and k, and
-    v + gate * R.lowrank_embed. The row-resident kernel runs where T and the row count are
-    multiples of 128, the 256 x 256 tile GEMM with the same epilogue elsewhere (T = 32, 96, 64)."""
+    v + gate * R.lowrank_embed. The two-waves-per-SIMD row-resident kernel runs where T and the
+    row count are multiples of 256 (T = 256, 2048, 512), the one-wave form where they are multiples
+    of 128 (T = 128, 384), the 256 x 256 tile GEMM with the same epilogue elsewhere (T = 32, 96, 64)."""
     g = _gen(T + 31 * members)
     M, K, V = T * members, 512, 4096
     rows = (members >> shift) + 1
