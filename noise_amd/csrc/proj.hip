@@ -439,7 +439,7 @@ qkv_proj_kernel(const ProjArgs g) {
 // identical bits. Chunks alternate between two accumulator sets; the epilogue of chunk c - 1 runs
 // in small pieces between the MFMAs of chunk c and, with a second wave on the SIMD, under the
 // other wave's MFMAs.
-constexpr int QR_ROWS = 256, QR_THREADS = 512, QR_CH = 32, QR_NCH = 48;
+constexpr int QR_ROWS = 256, QR_THREADS = 512, QR_CH = 32;  // 48 chunks: 1536 / QR_CH
 constexpr int QR_STAGE = QR_CH * PW_ROW;                    // 33280
 constexpr int QR_A_OFS = 2 * QR_STAGE;                      // a [1536] fp32
 constexpr int QR_BVE_OFS = QR_A_OFS + 1536 * 4;             // b_ve [512] fp32
