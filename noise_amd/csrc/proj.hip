@@ -462,9 +462,9 @@ struct QRLane {
   float su[3];     // sign * (row . b) per rank-1 segment
   uint32_t cs[16]; // rotary cos (high half) and sin (low half) as bf16 of the row's position for
                    // pair 8 (k / 4) + 4 half + k % 4 (the tables hold bf16 values)
-  float sa;              // with the value embedding: sign * a_ve[token]
+  float sa;              // with the value embedding: sign * a_ve[token]; NaN for an invalid token,
+                         // which makes every value-embedding term of the row NaN
   int64_t ve_row;        // element offset of the token's table row (0 for an invalid token)
-  bool tok_ok;
 };
 
 // Weight row of chunk-row r of chunk c (see above).
@@ -477,7 +477,9 @@ template <bool FCP, int PAR, int EK, bool VEPF>
 NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[32], floatx16 (&acc)[2],
                        floatx4 (&pf)[4], float& ss0, unsigned char* lds, uint32_t lds_base, int lane, int wave,
                        int c, bool load_next) {
-  constexpr int NA = QR_AHEAD + 1, NM = 32;
+  // the value-embedding epilogue holds 16 more values; its steps read one fragment less ahead
+  constexpr int AH = EK == EK_VE ? QR_AHEAD - 1 : QR_AHEAD;
+  constexpr int NA = AH + 1, NM = 32;
   constexpr int SP = 1 - PAR;  // parity of chunk cp: 0 = a head's first chunk, 1 = its second
   constexpr bool ROT = EK == EK_ROTQ || EK == EK_ROTK;
   const int half = lane >> 5;
@@ -489,14 +491,23 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
   const float su = ln.su[SEG];
   floatx4 av[4], bv[4];
   float gt = 0.f;
-  if constexpr (EK != EK_NONE) {
-    const uint32_t ab = lds_base + QR_A_OFS + (uint32_t)(64 * hd + 16 * SP + 4 * half) * 4;
+  // The v kinds use groups 2 and 3 only from piece 4 on: they are read after MFMA 2 (SPLIT_READ),
+  // so that fewer values are live at once.
+  constexpr bool SPLIT_READ = !ROT && EK != EK_NONE;
+  const uint32_t ab = lds_base + QR_A_OFS + (uint32_t)(64 * hd + 16 * SP + 4 * half) * 4;
+  const uint32_t bb = lds_base + QR_BVE_OFS + (uint32_t)(64 * (hd & 7) + 16 * SP + 4 * half) * 4;
+  auto read_groups = [&av, &bv, ab, bb]<int J0, int J1>() __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) PROJ_DSREAD(av[j], ab, 32 * (j & 1) + 128 * (j >> 1));
+    for (int j = J0; j < J1; ++j) PROJ_DSREAD(av[j], ab, 32 * (j & 1) + 128 * (j >> 1));
     if constexpr (EK == EK_VE) {
-      const uint32_t bb = lds_base + QR_BVE_OFS + (uint32_t)(64 * (hd & 7) + 16 * SP + 4 * half) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) PROJ_DSREAD(bv[j], bb, 32 * (j & 1) + 128 * (j >> 1));
+      for (int j = J0; j < J1; ++j) PROJ_DSREAD(bv[j], bb, 32 * (j & 1) + 128 * (j >> 1));
+    }
+  };
+  if constexpr (EK != EK_NONE) {
+    if constexpr (SPLIT_READ) read_groups.template operator()<0, 2>();
+    else read_groups.template operator()<0, 4>();
+    if constexpr (EK == EK_VE) {
       const uint32_t ga = lds_base + QR_GATE_OFS + (uint32_t)(((wave * 32 + (lane & 31)) * 8 + (hd & 7)) * 4);
       __asm__ volatile("ds_read_b32 %0, %1" : "=v"(gt) : "v"(ga));
     }
@@ -522,7 +533,7 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
   if constexpr (FCP) {
     [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
       (read.template operator()<S>(), ...);
-    }(std::make_integer_sequence<int, QR_AHEAD>{});
+    }(std::make_integer_sequence<int, AH>{});
   }
   // next chunk: wave w loads its chunk-rows 4 w .. 4 w + 3 (1 KB each)
   unsigned char* wdst = lds + (1 - PAR) * QR_STAGE + 4 * wave * PW_ROW;
@@ -586,7 +597,7 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
         const int j = v >> 2, q = v & 3;
         float x = ea[v] + su * av[j][q];
         if constexpr (EK == EK_VE) {
-          const float e = ln.tok_ok ? pf[j][q] + ln.sa * bv[j][q] : __builtin_nanf("");
+          const float e = pf[j][q] + ln.sa * bv[j][q];
           x += gt * e;
         }
         ea[v] = x;
@@ -606,13 +617,22 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
     }
   };
   auto tie_epi_inputs = [&]() __attribute__((always_inline)) {
-    __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]));
-    if constexpr (EK == EK_VE) __asm__ volatile("" : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(gt));
+    if constexpr (SPLIT_READ) {
+      __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]));
+      if constexpr (EK == EK_VE) __asm__ volatile("" : "+v"(bv[0]), "+v"(bv[1]), "+v"(gt));
+    } else {
+      __asm__ volatile("" : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]));
+    }
   };
 
   if constexpr (!FCP) {  // the last chunk's epilogue on its own
+    if constexpr (SPLIT_READ) read_groups.template operator()<2, 4>();
     PROJ_LGKM(0);
     tie_epi_inputs();
+    if constexpr (SPLIT_READ) {
+      __asm__ volatile("" : "+v"(av[2]), "+v"(av[3]));
+      if constexpr (EK == EK_VE) __asm__ volatile("" : "+v"(bv[2]), "+v"(bv[3]));
+    }
     [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
       (epi.template operator()<E>(), ...);
     }(std::make_integer_sequence<int, NPIECE>{});
@@ -628,8 +648,8 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
                                          (void*)(wdst + k * PW_ROW), 16, 0, 0);
       }
     }
-    if constexpr (S + QR_AHEAD < NM) read.template operator()<S + QR_AHEAD>();
-    PROJ_LGKM(NM - 1 - S < QR_AHEAD ? NM - 1 - S : QR_AHEAD);
+    if constexpr (S + AH < NM) read.template operator()<S + AH>();
+    PROJ_LGKM(NM - 1 - S < AH ? NM - 1 - S : AH);
     const bf16x8 f = fr[S % NA];
     if constexpr (S == 0)
       __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc[PAR]) : "v"(f), "a"(hB[S]));
@@ -641,6 +661,11 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
     // epilogue piece E after MFMA E + 1 (the LDS values it reads were waited for with fragment 0);
     // the quarters' stores after MFMAs 16, 18, 20, 22, behind the step's last weight load, so that
     // the next step's opening wait can leave exactly them in flight
+    if constexpr (SPLIT_READ && S == 2) read_groups.template operator()<2, 4>();
+    if constexpr (SPLIT_READ && S == 5) {
+      __asm__ volatile("" : "+v"(av[2]), "+v"(av[3]));
+      if constexpr (EK == EK_VE) __asm__ volatile("" : "+v"(bv[2]), "+v"(bv[3]));
+    }
     if constexpr (VEPF && S == QR_PF_AFTER) {
       __builtin_amdgcn_sched_barrier(0);
       prefetch();
@@ -739,13 +764,12 @@ qkv_rr_kernel(const ProjArgs g) {
   }
   ln.sa = 0.f;
   ln.ve_row = 0;
-  ln.tok_ok = true;
   if constexpr (HAS_VE) {
     const noise_rope_t& rp = g.rope;
-    ln.tok_ok = tok >= 0 && tok < rp.vocab;
-    ln.ve_row = ln.tok_ok ? tok * 512 : 0;
+    const bool tok_ok = tok >= 0 && tok < rp.vocab;
+    ln.ve_row = tok_ok ? tok * 512 : 0;
     const int64_t pv = (int64_t)(p >> rp.member_shift);
-    ln.sa = (ln.tok_ok && rp.sign) ? rp.sign[p] * rp.ve_a[pv * rp.ld_ve_a + tok] : 0.f;
+    ln.sa = !tok_ok ? __builtin_nanf("") : rp.sign ? rp.sign[p] * rp.ve_a[pv * rp.ld_ve_a + tok] : 0.f;
   }
   const float s = pert ? g.r1.sign[p] : 0.f;
 #pragma unroll
