@@ -455,7 +455,8 @@ constexpr int QR_LS = 4;                                    // MFMAs between two
 constexpr int QR_PF_AFTER = 10;  // MFMA after which the value-embedding prefetch issues (past the
                                  // epilogue's reads of the previous values, before the stores)
 static_assert(QR_LDS <= 160 * 1024, "LDS budget");
-static_assert(3 * QR_LS + 1 < 16 && QR_PF_AFTER > 9 && QR_PF_AFTER < 16, "the loads precede the stores");
+static_assert(3 * QR_LS < 17 && QR_PF_AFTER > 9 && QR_PF_AFTER < 17, "the loads precede the stores");
+static_assert(QR_AHEAD <= 3, "an LDS read issued after MFMA S is used after MFMA S + 3");
 
 struct QRLane {
   int64_t row;
@@ -540,13 +541,19 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
 
   // ---- the epilogue of chunk cp ----
   // rotary kinds: pieces 0-7 pair j (rank-1 term, rotation, squares); SP 0: 8 into the hold;
-  // SP 1: 8 the head's norm factor, 9-10 this chunk normalised into the tile, 11-12 the held chunk
-  // likewise, two groups each, 13-16 four whole-row quarters out. v kinds: pieces 0-7 values 2 k,
-  // 2 k + 1, 8 into the tile, SP 1: 9-12 the quarters.
-  constexpr int NPIECE = EK == EK_NONE ? 0 : ROT ? (SP == 0 ? 9 : 17) : (SP == 0 ? 9 : 13);
-  constexpr int QFIRST = NPIECE - 4;  // first quarter piece (SP 1)
-  constexpr int NBODY = SP == 1 ? QFIRST : NPIECE;
+  // SP 1: 8 the head's norm factor and the hold's reads, 9-10 this chunk normalised into the tile,
+  // 11-12 the held chunk likewise, two groups each. v kinds: pieces 0-7 values 2 k, 2 k + 1, 8 into
+  // the tile. SP 1 then reads four whole-row quarters of the tile (pieces NBODY .. + 3) and stores
+  // them (NBODY + 4 .. + 7). The hold's and the quarters' LDS reads are asm, issued three MFMAs
+  // before their use: the fragment waits in between cover them, so no wait drains the fragment
+  // reads in flight.
+  constexpr int NBODY = EK == EK_NONE ? 0 : ROT ? (SP == 0 ? 9 : 13) : 9;
+  constexpr int NPIECE = SP == 1 && EK != EK_NONE ? NBODY + 8 : NBODY;
   floatx16& ea = acc[1 - PAR];
+  floatx4 hv[4];  // the held chunk (SP 1 rotary kinds)
+  u32x4 qd[4];    // the quarters
+  const uint32_t hold_a = lds_base + QR_HOLD_OFS + wave * 4096 + 16 * lane;
+  const uint32_t quarter_a = lds_base + QR_OUT_OFS + wave * 32 * POUT_ROW + (lane >> 3) * POUT_ROW + 16 * (lane & 7);
   float ss = SP == 0 ? 0.f : ss0, rr = 1.f;
   uint32_t w[8];
   unsigned char* tile = lds + QR_OUT_OFS + wave * 32 * POUT_ROW + (lane & 31) * POUT_ROW + 8 * half;
@@ -554,6 +561,11 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<u32x2*>(tile + 32 * s + 16 * (j & 1) + 64 * (j >> 1)) = u32x2{w[2 * j], w[2 * j + 1]};
+  };
+  auto hold_reads = [&hv, hold_a]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(hv[j]) : "v"(hold_a), "n"(1024 * j) : "memory");
   };
   auto epi = [&]<int E>() __attribute__((always_inline)) {
     if constexpr (ROT && E < 8) {
@@ -577,6 +589,7 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
       // the head's 64 squares: both chunks of this lane plus those of lane l ^ 32 (same row)
       const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
       rr = rsqrtf((__uint_as_float(r[0]) + __uint_as_float(r[1])) * (1.0f / 64) + PRMS_EPS);
+      hold_reads();
     } else if constexpr (ROT && E == 9) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) w[k] = pack_bf2(ea[2 * k] * rr, ea[2 * k + 1] * rr);
@@ -584,10 +597,11 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
       to_tile(1);
     } else if constexpr (ROT && (E == 11 || E == 12)) {
       // groups 2 (E - 11) and 2 (E - 11) + 1 of the held chunk
-      const float* hold = reinterpret_cast<const float*>(lds + QR_HOLD_OFS + wave * 4096) + 4 * lane;
+      constexpr int j0 = 2 * (E - 11);
+      __asm__ volatile("" : "+v"(hv[j0]), "+v"(hv[j0 + 1]));
 #pragma unroll
-      for (int j = 2 * (E - 11); j < 2 * (E - 11) + 2; ++j) {
-        const floatx4 h = *reinterpret_cast<const floatx4*>(hold + 256 * j);
+      for (int j = j0; j < j0 + 2; ++j) {
+        const floatx4 h = hv[j];
         const u32x2 pw{pack_bf2(h[0] * rr, h[1] * rr), pack_bf2(h[2] * rr, h[3] * rr)};
         *reinterpret_cast<u32x2*>(tile + 16 * (j & 1) + 64 * (j >> 1)) = pw;
       }
@@ -606,14 +620,18 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
 #pragma unroll
       for (int k = 0; k < 8; ++k) w[k] = pack_bf2(ea[2 * k], ea[2 * k + 1]);
       to_tile(SP);
-    } else if constexpr (SP == 1 && E >= QFIRST && E < QFIRST + 4) {
-      // one quarter of the tile out as whole rows: lane l copies 16 bytes of row 8 q + l / 8 (the
-      // wave's tile writes are complete for its own reads: LDS operations of a wave run in order)
-      const int r_ = 8 * (E - QFIRST) + (lane >> 3);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(lds + QR_OUT_OFS + wave * 32 * POUT_ROW + r_ * POUT_ROW +
-                                                      16 * (lane & 7));
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(g.rope.out + (ln.row - (lane & 31) + r_) * 1536 +
-                                                              hd * 64 + 8 * (lane & 7)));
+    } else if constexpr (SP == 1 && E >= NBODY && E < NBODY + 4) {
+      // quarter q of the tile: lane l reads 16 bytes of row 8 q + l / 8 (the wave's tile writes are
+      // complete for its own reads: LDS operations of a wave run in order)
+      constexpr int q = E - NBODY;
+      __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(qd[q]) : "v"(quarter_a), "n"(8 * q * POUT_ROW) : "memory");
+    } else if constexpr (SP == 1 && E >= NBODY + 4 && E < NBODY + 8) {
+      // ... and out as whole rows
+      constexpr int q = E - NBODY - 4;
+      __asm__ volatile("" : "+v"(qd[q]));
+      const int r_ = 8 * q + (lane >> 3);
+      __builtin_nontemporal_store(qd[q], reinterpret_cast<u32x4*>(g.rope.out + (ln.row - (lane & 31) + r_) * 1536 +
+                                                                  hd * 64 + 8 * (lane & 7)));
     }
   };
   auto tie_epi_inputs = [&]() __attribute__((always_inline)) {
@@ -633,8 +651,13 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
       __asm__ volatile("" : "+v"(av[2]), "+v"(av[3]));
       if constexpr (EK == EK_VE) __asm__ volatile("" : "+v"(bv[2]), "+v"(bv[3]));
     }
+    // (no fragment waits here: every piece waits for all LDS reads before it)
+    auto one = [&]<int E>() __attribute__((always_inline)) {
+      PROJ_LGKM(0);
+      epi.template operator()<E>();
+    };
     [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
-      (epi.template operator()<E>(), ...);
+      (one.template operator()<E>(), ...);
     }(std::make_integer_sequence<int, NPIECE>{});
     return;
   }
@@ -659,8 +682,8 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
       __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                        : "+v"(acc[PAR]) : "v"(f), "a"(hB[S]));
     // epilogue piece E after MFMA E + 1 (the LDS values it reads were waited for with fragment 0);
-    // the quarters' stores after MFMAs 16, 18, 20, 22, behind the step's last weight load, so that
-    // the next step's opening wait can leave exactly them in flight
+    // quarter q read after MFMA 14 + 2 q and stored after MFMA 17 + 2 q, behind the step's last
+    // weight load, so that the next step's opening wait can leave exactly the stores in flight
     if constexpr (SPLIT_READ && S == 2) read_groups.template operator()<2, 4>();
     if constexpr (SPLIT_READ && S == 5) {
       __asm__ volatile("" : "+v"(av[2]), "+v"(av[3]));
@@ -677,9 +700,13 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
         __builtin_amdgcn_sched_barrier(0);
         epi.template operator()<S - 1>();
         __builtin_amdgcn_sched_barrier(0);
-      } else if constexpr (SP == 1 && S >= 16 && S % 2 == 0 && (S - 16) / 2 < 4) {
+      } else if constexpr (SP == 1 && S >= 14 && S % 2 == 0 && (S - 14) / 2 < 4) {
         __builtin_amdgcn_sched_barrier(0);
-        epi.template operator()<QFIRST + (S - 16) / 2>();
+        epi.template operator()<NBODY + (S - 14) / 2>();
+        __builtin_amdgcn_sched_barrier(0);
+      } else if constexpr (SP == 1 && S >= 17 && S % 2 == 1 && (S - 17) / 2 < 4) {
+        __builtin_amdgcn_sched_barrier(0);
+        epi.template operator()<NBODY + 4 + (S - 17) / 2>();
         __builtin_amdgcn_sched_barrier(0);
       }
     }

@@ -29,15 +29,12 @@ def test_inline_asm_kernels_are_hazard_free(name, tmp_path):
 # plain one bench.py times alone): the fused MLP spills a few prologue/epilogue values (its waves
 # hold 512 registers), its two-wave form (256 registers a wave) some around its edge steps, the
 # two-wave q|k|v projection some addresses around its prologue and between its chunk loops, the
-# others none or a few.
+# others none or a few; none inside a loop.
 SPILL_BUDGET = {'mlp_fused_kernelILb1ELb1ELi2ELb1E': 16, 'mlp_fused_kernelILb1ELb1ELi1ELb1E': 16,
                 'mlp_fused_kernelILb1ELb1ELi0ELb0E': 16, 'qkv_proj_kernel': 0, 'window_attention_kernel': 2,
-                'qkv_rr_kernelILb0E': 24, 'qkv_rr_kernelILb1E': 28, 'head_rr_kernel': 4,
+                'qkv_rr_kernelILb0E': 20, 'qkv_rr_kernelILb1E': 24, 'head_rr_kernel': 4,
                 'head_ce_kernelILb1ELb0E': 0, 'embed_norm_kernel': 0, 'es_gradient_kernel': 0,
                 'mlp_pc_kernel': 128}
-# Scratch operations allowed inside a loop: none, but for one reload per iteration of the two-wave
-# q|k|v projection's value-embedding loop (two chunk steps of 32 MFMAs each).
-LOOP_SCRATCH_ALLOWANCE = {'qkv_rr_kernelILb1E': 1}
 
 
 @pytest.mark.parametrize('name', ['mlp', 'mlp_pc', 'proj', 'attention', 'head', 'norm', 'es'])
@@ -53,8 +50,7 @@ def test_step_kernels_spill_within_budget_and_never_in_a_loop(name, tmp_path):
     assert checked > 0
     loops, bad = A.loop_scratch(asm)
     assert loops > 0 or name == 'norm'  # norm.hip's row kernels are straight-line code
-    for key in SPILL_BUDGET:
-        assert sum(1 for b in bad if key in b[0]) <= LOOP_SCRATCH_ALLOWANCE.get(key, 0), (key, bad)
+    assert [b for b in bad if any(key in b[0] for key in SPILL_BUDGET)] == []
 
 
 @pytest.mark.parametrize('name', ['proj', 'head', 'mlp_pc'])

@@ -322,6 +322,37 @@ def test_qkv_row_resident_matches_oracle(device, T, members, shift, ve):
     _close_bf16(got[:, 1024:], v)
 
 
+@pytest.mark.parametrize('T,members,pert', [(256, 2, True), (256, 2, False), (128, 2, True)])
+def test_qkv_row_resident_invalid_tokens(device, T, members, pert):
+    """A token outside [0, vocab) makes the value-embedding term, and so the row's v, NaN; its q and
+    k and every other row stay finite. T = 256 runs the two-waves-per-SIMD kernel, T = 128 the
+    one-wave form."""
+    g = _gen(T + 7 * members + pert)
+    M, K, V = T * members, 512, 4096
+    A = _bf(torch.randn(M, K, generator=g)).to(device)
+    W = _bf(torch.randn(1536, K, generator=g) / math.sqrt(K)).to(device)
+    sign = (torch.randn(members, generator=g) * 0.3).to(device) if pert else None
+    a = [torch.randn(members, 512, generator=g).to(device) for _ in range(3)]
+    u = [torch.randn(M, 1, generator=g).to(device) for _ in range(3)]
+    r1 = nk.rank1(sign, T, a, u, 1, 1, 0) if pert else None
+    cos, sin = (x.to(device) for x in R.rotary_tables(T))
+    gate = (torch.rand(M, 8, generator=g) * 2).to(device)
+    table = torch.randn(V, 512, generator=g).to(device)
+    idx = torch.randint(0, V, (T,), generator=g)
+    bad = torch.tensor([0, 5, T // 2, T - 1])
+    idx[bad] = torch.tensor([-1, V, V + 7, -100])
+    nz = NoiseRows(a=torch.randn(members, V, generator=g).to(device), b=torch.randn(members, 512, generator=g).to(device),
+                   shift=0)
+    out = torch.empty(M, 1536, dtype=torch.bfloat16, device=device)
+    nk.qkv_rope_gemm(A, W, r1, out, T, cos, sin, sign, gate, table, idx.to(device), nz)
+    got = out.cpu().float().view(members, T, 1536)
+    is_bad = torch.zeros(T, dtype=torch.bool)
+    is_bad[bad] = True
+    assert torch.isfinite(got[:, :, :1024]).all()
+    assert torch.isnan(got[:, is_bad, 1024:]).all()
+    assert torch.isfinite(got[:, ~is_bad, 1024:]).all()
+
+
 @pytest.mark.parametrize('T,window,members,unit', [
     (96, 16, 2, True), (128, 64, 3, True), (256, 1024, 2, True), (300, 100, 2, True),
     (2048, 1024, 1, True), (2048, 2048, 1, True), (520, 0, 1, True), (700, 300, 2, False),
