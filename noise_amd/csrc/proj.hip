@@ -455,7 +455,7 @@ constexpr int QR_LS = 4;                                    // MFMAs between two
 constexpr int QR_PF_AFTER = 10;  // MFMA after which the value-embedding prefetch issues (past the
                                  // epilogue's reads of the previous values, before the stores)
 static_assert(QR_LDS <= 160 * 1024, "LDS budget");
-static_assert(3 * QR_LS < 17 && QR_PF_AFTER > 9 && QR_PF_AFTER < 17, "the loads precede the stores");
+static_assert(3 * QR_LS < 26 && QR_PF_AFTER > 9 && QR_PF_AFTER < 26, "the loads precede the stores");
 static_assert(QR_AHEAD <= 3, "an LDS read issued after MFMA S is used after MFMA S + 3");
 
 struct QRLane {
@@ -662,6 +662,24 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
     return;
   }
 
+  // MFMA after which piece E runs. Rotary kinds: the pairs after every second MFMA, the norm
+  // factor (with the hold's reads) after MFMA 16 and the held chunk from MFMA 20 on (three MFMAs
+  // later). v kinds: one piece after every MFMA from the first, so that the value-embedding values
+  // are free for the next prefetch early. The tile reads after 22-25, the stores after 26-29.
+  auto slot = [](int E) constexpr {
+    if (!ROT) return E < 9 ? E + 1 : E < 13 ? 22 + (E - 9) : 26 + (E - 13);
+    if (E < 8) return 2 * E + 1;
+    if (SP == 0) return 17;
+    constexpr int tail[5] = {16, 17, 18, 20, 21};
+    return E < 13 ? tail[E - 8] : E < 17 ? 22 + (E - 13) : 26 + (E - 17);
+  };
+  auto run_at = [&]<int E, int S>() __attribute__((always_inline)) {
+    if constexpr (slot(E) == S) {
+      __builtin_amdgcn_sched_barrier(0);
+      epi.template operator()<E>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   auto op = [&]<int S>() __attribute__((always_inline)) {
     if constexpr (S % QR_LS == 0 && S / QR_LS < 4) {
       if (load_next) {
@@ -681,9 +699,10 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
     else
       __asm__ volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                        : "+v"(acc[PAR]) : "v"(f), "a"(hB[S]));
-    // epilogue piece E after MFMA E + 1 (the LDS values it reads were waited for with fragment 0);
-    // quarter q read after MFMA 14 + 2 q and stored after MFMA 17 + 2 q, behind the step's last
-    // weight load, so that the next step's opening wait can leave exactly the stores in flight
+    // epilogue piece E after MFMA slot(E) (the LDS values it reads were waited for with fragment
+    // 0), one every second MFMA; quarter q read after MFMA 22 + q and stored after MFMA 26 + q,
+    // behind the step's last weight load, so that the next step's opening wait can leave exactly
+    // the stores in flight
     if constexpr (SPLIT_READ && S == 2) read_groups.template operator()<2, 4>();
     if constexpr (SPLIT_READ && S == 5) {
       __asm__ volatile("" : "+v"(av[2]), "+v"(av[3]));
@@ -695,20 +714,10 @@ NOISE_DEV void qr_step(const ProjArgs& g, const QRLane& ln, const bf16x8 (&hB)[3
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (EK != EK_NONE) {
-      if constexpr (S >= 1 && S - 1 < NBODY) {
-        if constexpr (S == 1) tie_epi_inputs();
-        __builtin_amdgcn_sched_barrier(0);
-        epi.template operator()<S - 1>();
-        __builtin_amdgcn_sched_barrier(0);
-      } else if constexpr (SP == 1 && S >= 14 && S % 2 == 0 && (S - 14) / 2 < 4) {
-        __builtin_amdgcn_sched_barrier(0);
-        epi.template operator()<NBODY + (S - 14) / 2>();
-        __builtin_amdgcn_sched_barrier(0);
-      } else if constexpr (SP == 1 && S >= 17 && S % 2 == 1 && (S - 17) / 2 < 4) {
-        __builtin_amdgcn_sched_barrier(0);
-        epi.template operator()<NBODY + 4 + (S - 17) / 2>();
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      if constexpr (S == 1) tie_epi_inputs();
+      [&]<int... E>(std::integer_sequence<int, E...>) __attribute__((always_inline)) {
+        (run_at.template operator()<E, S>(), ...);
+      }(std::make_integer_sequence<int, NPIECE>{});
     }
   };
   [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
