@@ -67,6 +67,7 @@ constexpr int NW = NTH / 64;
 struct AttnSmem {
   uint16_t kv[NSTAGE][2][BKEY * LDK];  // [stage][K | V] row-major [key][dim], swizzled, 64 KB
   float mom[NW][2][64];                // per-wave moment partials
+  float bproj[64];                     // the head's c_proj b row (b_proj[member, 64 h ..])
 };
 
 // MOM: the per-(member, head) moments of y are requested (the population step asks for none, and
@@ -114,6 +115,7 @@ void window_attention_kernel(const noise_attention_t g) {
   // Wait for Q here, in the compiler's own accounting: otherwise it guards the first use inside the
   // loop with a vmcnt that would also wait for the key blocks in flight.
   __asm__ volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]));
+  const int64_t pn = p >> g.member_shift;
 
   floatx16 o[2];
 #pragma unroll
@@ -269,6 +271,17 @@ void window_attention_kernel(const noise_attention_t g) {
     if (2 * b + 1 >= hfirst && 2 * b + 1 <= hlast) step.template operator()<ST, 1>(2 * b + 1, run0);
   };
 
+  // The head's c_proj b row for the epilogue's u_proj dots, straight into LDS by wave 0 (a direct
+  // load like the key blocks': no register waits for it; their waits and barriers cover it, vector
+  // memory operations retiring in order).
+  if (g.b_proj && w == 0) {
+    uint32_t m0save_;
+    __asm__ volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(m0save_)
+                     : "v"(g.b_proj + pn * g.ld_b_proj + h * 64 + lane),
+                       "s"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&sm.bproj[0])
+                     : "memory");
+  }
   NOISE_ATT_LOAD(0, 0)
   if (nblk > 1) NOISE_ATT_LOAD(1, 1)
   static_assert(NSTAGE == 4, "the block loop is unrolled over four stages");
@@ -292,7 +305,6 @@ void window_attention_kernel(const noise_attention_t g) {
   float mom[MOM ? 64 : 1];
 #pragma unroll
   for (int i = 0; i < (MOM ? 64 : 1); ++i) mom[i] = 0.f;
-  const int64_t pn = p >> g.member_shift;
   {
     const int qi = wq0 + q32;
     float lt = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
@@ -316,7 +328,7 @@ void window_attention_kernel(const noise_attention_t g) {
         *reinterpret_cast<u32x2*>(&ys[swz(q32, dim)]) = pk;
         if (valid) {
           if (g.b_proj) {
-            const float4 bv = *reinterpret_cast<const float4*>(g.b_proj + pn * g.ld_b_proj + h * 64 + dim);
+            const float4 bv = *reinterpret_cast<const float4*>(&sm.bproj[dim]);
             dot += y[0] * bv.x + y[1] * bv.y + y[2] * bv.z + y[3] * bv.w;
           }
           if constexpr (MOM) {
