@@ -58,13 +58,17 @@ def step_flops(members, T=2048, d=512, f=2048, V=4096, layers=8, windows=(1024, 
     return members * T * per_tok
 
 
-def mlp_traffic():
-    """HBM bytes per fused-MLP launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-    (scaled by the same counters on a copy of known size), as recorded in the profile summary."""
+def mlp_traffic(rows):
+    """HBM bytes per fused-MLP launch of `rows` rows: the bytes per launch measured with rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE (scaled by the same counters on a copy of known size) at the row
+    count recorded beside them in the profile summary, scaled to `rows` (a workgroup moves the same
+    bytes per row at any launch size)."""
     if not TRAFFIC_FILE.exists():
         return None
-    m = re.search(r'^traffic_bytes_per_launch:\s*([0-9]+)', TRAFFIC_FILE.read_text(), re.M)
-    return int(m.group(1)) if m else None
+    text = TRAFFIC_FILE.read_text()
+    m = re.search(r'^traffic_bytes_per_launch:\s*([0-9]+)', text, re.M)
+    n = re.search(r'^traffic_rows_per_launch:\s*([0-9]+)', text, re.M)
+    return round(int(m.group(1)) * rows / int(n.group(1))) if m and n else None
 
 
 def mlp_inputs(rows=512 * 2048, d=512, f=2048, seed=0):
@@ -517,7 +521,8 @@ def main():
     ap.add_argument('--warmup', type=int, default=1)
     ap.add_argument('--members', type=int, default=3072)
     ap.add_argument('--tokens', type=int, default=2048)
-    ap.add_argument('--chunk', type=int, default=256, help='pairs per batched forward')
+    ap.add_argument('--chunk', type=int, default=512,
+                    help='pairs per batched forward (a member\'s loss does not depend on it)')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--no-extra', action='store_true',
                     help='skip the measurements after the timed steps (MLP alone, fp32-accurate head step)')
@@ -604,7 +609,7 @@ def main():
                    'members': members, 'pairs': pairs, 'seq_len': T, 'sigma': 1e-3, 'model': '37.7M (8x512, V=4096)',
                    'members_per_forward': 2 * args.chunk, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'mfma', 'achieved': achieved, 'peak': PEAK_BF16 / 1e12, 'unit': 'TFLOP/s',
-                     'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(),
+                     'frac': achieved * 1e12 / PEAK_BF16, 'traffic': mlp_traffic(rows),
                      'kernel': 'mlp_fused: attention c_proj + rank-1 into the residual rows, then norm + c_fc + '
                                'rank-1 + relu^2 + c_proj + rank-1 + residual, hidden on chip, then the next '
                                "layer's mix_norm (x0 mixing, norm, q/k/v dots, gate) in the epilogue",
