@@ -246,7 +246,7 @@ def test_rope_norm_ve(device):
 
 @pytest.mark.parametrize('T,members,shift,ve,pert', [
     (256, 4, 1, True, True), (100, 5, 0, True, True), (2048, 1, 0, False, True), (64, 8, 1, True, False),
-    (300, 2, 1, False, False)])
+    (300, 2, 1, False, False), (256, 2, 0, True, False), (512, 2, 0, False, False)])
 def test_qkv_rope_gemm_matches_unfused(device, T, members, shift, ve, pert):
     """The fused q|k|v projection equals lowrank_gemm (fp32 out) followed by rope_norm_ve on the
     same inputs: the same fp32 arithmetic up to the order of the norm's sum of squares."""
