@@ -293,6 +293,20 @@ int noise_es_gradient(const float* w, int n, const float* a_base, const int64_t*
                       const float* b_base, const int64_t* b_off, int out, int in, float scale,
                       int accumulate, float* G, float* work, int64_t work_elems, void* stream);
 
+/* The gradients of up to 64 parameters in one launch (train/val/eggroll.py:155-163: the loop over
+ * every parameter of the model, scale = -1/n). Parameter k, shape [outs[k], ins[k]] (ins[k] == 1
+ * for a vector), takes pair j's noise from the slice buffer[o .. o + outs[k] + ins[k]) with
+ * o = offsets[k * ld_offsets + j] (the reference's noise(), eggroll.py:122-128): a_j is its first
+ * outs[k] values, b_j the next ins[k] (b_j = 1 for a vector), and
+ * grads[k][o, i] = scale * sum_j w_j a_j[o] b_j[i] (+= with accumulate). One pass over the pairs
+ * per 64 x 64 tile: each parameter's result is bit-identical to noise_es_gradient's with no
+ * workspace. A slice outside the buffer makes its pair's terms NaN. outs, ins and grads are host
+ * arrays of nparams entries (grads: device pointers, row-major [outs[k], ins[k]]). */
+int noise_es_gradient_params(const float* w, int n, const float* buffer, int64_t buffer_len,
+                             const int64_t* offsets, int64_t ld_offsets, int nparams, const int* outs,
+                             const int* ins, float* const* grads, float scale, int accumulate,
+                             void* stream);
+
 /* Floats of `work` with which noise_es_gradient splits the pair sum over more workgroups (a
  * fixed split and a fixed-order reduction: the same result on every call); with less (or NULL)
  * it makes one pass over every pair. No counterpart in the reference: workspace sizing. */

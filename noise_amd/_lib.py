@@ -113,6 +113,7 @@ SIGNATURES = {
     'noise_fitness_ranks': [P, INT, INT, P, P, P, P],
     'noise_es_gradient': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P, I64, P],
     'noise_es_gradient_work': [INT, INT, INT],
+    'noise_es_gradient_params': [P, INT, P, I64, P, I64, INT, P, P, P, F32, INT, P],
     'noise_es_gradient_noalloc': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
     'noise_es_gradient_noalloc_capacity': [],
     'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],

@@ -318,6 +318,145 @@ extern "C" int noise_es_gradient_noalloc(const float* w, int n, const float* a_b
   return noise_es_gradient(w, n, a_base, a_off, b_base, b_off, out, in, scale, accumulate, G, work, need, stream);
 }
 
+// ---- every parameter's gradient in one launch -------------------------------------------------
+// One workgroup per 64 x 64 tile of any parameter (parameter k owns tiles tile0[k] .. tile0[k + 1]
+// - 1, row-major over its [out, in] grid); each sums all n pairs in one pass, in the order of
+// es_gradient_kernel without a split (ascending pairs, two per MFMA, the same products), so
+// parameter k's result is bit-identical to noise_es_gradient's one-pass result for it. Pair j's
+// noise for parameter k is the slice buffer[o .. o + out + in), o = offsets[k, j]: a_j its first
+// out values, b_j the next in (b_j = 1 for a vector parameter, in == 1); a slice outside the
+// buffer makes the pair's terms NaN instead of a read.
+namespace {
+constexpr int GP_MAX = 64;
+__device__ const float kOne = 1.0f;
+struct GradLayout {
+  float* G[GP_MAX];
+  int out[GP_MAX];
+  int in[GP_MAX];
+  int tiles_x[GP_MAX];
+  int tile0[GP_MAX + 1];
+};
+
+__global__ __launch_bounds__(256) void es_gradient_params_kernel(const float* __restrict__ w, int n,
+                                                                 const float* __restrict__ buffer,
+                                                                 int64_t buffer_len,
+                                                                 const int64_t* __restrict__ offsets,
+                                                                 int64_t ld_offsets, int nparams,
+                                                                 const GradLayout lay, float scale,
+                                                                 int accumulate) {
+  constexpr int SJ = 32;
+  __shared__ __attribute__((aligned(16))) float As[2][SJ][64];
+  __shared__ __attribute__((aligned(16))) float Bs[2][SJ][64];
+  // Consecutive workgroups are dealt to the 8 XCDs in turn; XCD x takes the x-th contiguous run of
+  // tiles, so the workgroups sharing an L2 mostly share a parameter and its noise rows.
+  const int nb = gridDim.x, bx = blockIdx.x, q = nb >> 3, rem = nb & 7, xcd = bx & 7;
+  const int t = xcd * q + (xcd < rem ? xcd : rem) + (bx >> 3);
+  int lo = 0, hi = nparams;  // tile0[lo] <= t < tile0[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (lay.tile0[mid] <= t) lo = mid;
+    else hi = mid;
+  }
+  const int k = lo, out = lay.out[k], in = lay.in[k], tt = t - lay.tile0[k];
+  const int o0 = (tt / lay.tiles_x[k]) * 64, i0 = (tt % lay.tiles_x[k]) * 64;
+  const int64_t* off = offsets + (int64_t)k * ld_offsets;
+  const int64_t last = buffer_len - ((int64_t)out + (in > 1 ? in : 0));  // the largest valid slice start
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wo = wv >> 1, wi = wv & 1;
+  // loader: wave wv fetches pairs wv, wv + 4, .., wv + 28 of a stage, lane = column (each load
+  // instruction reads 64 consecutive floats of one pair's row). Branch-free, so that a stage's 16
+  // loads are in flight together: the pair index and the columns are clamped into range (the host
+  // checks that the buffer holds a slice), a vector parameter's b (the constant 1) is read from
+  // kOne like a noise value, and the pair's status enters through its multipliers: 0 past the last
+  // pair, NaN for a slice outside the buffer.
+  const bool vec = in == 1, a_col = o0 + lane < out, b_col = vec ? lane == 0 : i0 + lane < in;
+  const int ac = a_col ? o0 + lane : out - 1;
+  const int bc = vec ? 0 : (b_col ? out + i0 + lane : out + in - 1);
+  // fetch only issues a stage's loads (and forms its multipliers); stash, after the stage before
+  // has run its MFMAs, applies them and writes LDS, so the loads' latency hides under those MFMAs
+  float av[8], bv[8], am[8], bm[8];
+  auto fetch = [&](int j0) {
+    int64_t o[8];
+    float wj[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = j0 + wv + 4 * e;
+      o[e] = off[j < n ? j : n - 1];
+      wj[e] = w[j < n ? j : n - 1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool live = j0 + wv + 4 * e < n, ok = o[e] >= 0 && o[e] <= last;
+      const float* src = buffer + (ok ? o[e] : 0);
+      av[e] = src[ac];
+      bv[e] = *(vec ? &kOne : src + bc);
+      am[e] = !live ? 0.f : ok ? wj[e] : __builtin_nanf("");
+      bm[e] = !live ? 0.f : ok ? 1.0f : __builtin_nanf("");
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      As[buf][wv + 4 * e][lane] = a_col ? am[e] * av[e] : 0.f;
+      Bs[buf][wv + 4 * e][lane] = b_col ? bm[e] * bv[e] : 0.f;
+    }
+  };
+  floatx16 acc = {};
+  if (n > 0) fetch(0);
+  for (int j0 = 0, buf = 0; j0 < n; j0 += SJ, buf ^= 1) {
+    stash(buf);
+    if (j0 + SJ < n) fetch(j0 + SJ);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < SJ / 2; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[buf][2 * kk + (lane >> 5)][wo * 32 + (lane & 31)],
+                                                  Bs[buf][2 * kk + (lane >> 5)][wi * 32 + (lane & 31)], acc, 0, 0, 0);
+  }
+  float* const G = lay.G[k];
+  const int i = i0 + wi * 32 + (lane & 31);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int o = o0 + wo * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+    if (o >= out || i >= in) continue;
+    float* dst = G + (int64_t)o * in + i;
+    const float x = scale * acc[v];
+    *dst = accumulate ? *dst + x : x;
+  }
+}
+}  // namespace
+
+extern "C" int noise_es_gradient_params(const float* w, int n, const float* buffer, int64_t buffer_len,
+                                        const int64_t* offsets, int64_t ld_offsets, int nparams, const int* outs,
+                                        const int* ins, float* const* grads, float scale, int accumulate,
+                                        void* stream) {
+  NOISE_REQUIRE((w || n == 0) && buffer && offsets && outs && ins && grads, "es_gradient_params: null argument");
+  NOISE_REQUIRE(nparams > 0 && nparams <= GP_MAX, "es_gradient_params: nparams=%d must be in 1..%d", nparams, GP_MAX);
+  NOISE_REQUIRE(n >= 0 && ld_offsets >= n && buffer_len > 0,
+                "es_gradient_params: bad sizes (n=%d ld_offsets=%lld buffer_len=%lld)", n, (long long)ld_offsets,
+                (long long)buffer_len);
+  GradLayout lay;
+  int64_t tiles = 0;
+  for (int k = 0; k < nparams; ++k) {
+    NOISE_REQUIRE(grads[k] && outs[k] > 0 && ins[k] > 0, "es_gradient_params: parameter %d: [%d, %d] at %p", k,
+                  outs[k], ins[k], (void*)grads[k]);
+    NOISE_REQUIRE((int64_t)outs[k] + (ins[k] > 1 ? ins[k] : 0) <= buffer_len,
+                  "es_gradient_params: parameter %d: a [%d, %d] slice is longer than the buffer (%lld)", k, outs[k],
+                  ins[k], (long long)buffer_len);
+    lay.G[k] = grads[k];
+    lay.out[k] = outs[k];
+    lay.in[k] = ins[k];
+    lay.tiles_x[k] = (ins[k] + 63) / 64;
+    lay.tile0[k] = (int)tiles;
+    tiles += (int64_t)lay.tiles_x[k] * ((outs[k] + 63) / 64);
+    NOISE_REQUIRE(tiles < (int64_t)1 << 31, "es_gradient_params: more than 2^31 tiles");
+  }
+  for (int k = nparams; k <= GP_MAX; ++k) lay.tile0[k] = (int)tiles;
+  es_gradient_params_kernel<<<(unsigned)tiles, 256, 0, (hipStream_t)stream>>>(w, n, buffer, buffer_len, offsets,
+                                                                               ld_offsets, nparams, lay, scale,
+                                                                               accumulate);
+  return noise::check_launch("es_gradient_params");
+}
+
 // One workgroup per (parameter k, pair row d): out[d, start_k + i] = buffer[o + min(i, w_k - 1)]
 // for i < pad4(w_k), o = offsets[k, directions[d]] -- a contiguous slice copied with coalesced
 // 4-byte reads (o is any index) into a 16-byte-aligned column range. Indices that fall outside

@@ -30,7 +30,6 @@ SEED = 0
 SIGMA = 0.002
 CHUNK = 256
 NOISE = 2 ** 28
-GRAD_STREAMS = 8
 
 
 class Eggroll:
@@ -59,11 +58,7 @@ class Eggroll:
             self.grads[name] = self.grad_flat[off:off + n].view(shape)
             off += n
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
-        # The parameters' gradients are independent launches of small grids: they go round-robin
-        # to GRAD_STREAMS side streams (default priority), each with its own split-sum workspace,
-        # sized on the first step, and join the step's stream before the host sync.
-        self.grad_streams = [torch.cuda.Stream(device=self.device) for _ in range(GRAD_STREAMS)]
-        self.grad_work = [None] * GRAD_STREAMS
+        self._grad_list = [self.grads[name] for name in self.shapes]
         self._layout = None    # column layout of the per-chunk noise gather
 
     def offsets(self, step):
@@ -122,32 +117,10 @@ class Eggroll:
         return losses
 
     def gradient(self, weight, offsets, n):
-        """grads[name] = -1/n sum_p weight[p] a_p^T b_p (or eps_p) for every parameter (eggroll.py:155-166).
-
-        The launches are issued after the work already on the current stream (the fitness weights)
-        and the current stream waits for all of them before its next work."""
-        pairs = self.pairs
-        need = max(K.es_gradient_work(pairs, s[0], s[1] if len(s) == 2 else 1) for s in self.shapes.values())
-        for i, w in enumerate(self.grad_work):
-            if w is None or w.numel() < need:
-                self.grad_work[i] = torch.empty(max(need, 1), device=self.device)
-        main = torch.cuda.current_stream(self.device)
-        ready = torch.cuda.Event()
-        ready.record(main)  # the fitness weights
-        for i, (name, shape) in enumerate(self.shapes.items()):
-            side = self.grad_streams[i % len(self.grad_streams)]
-            side.wait_event(ready)
-            with torch.cuda.stream(side):
-                off = offsets[name]
-                work = self.grad_work[i % len(self.grad_streams)]
-                if len(shape) == 2:
-                    K.es_gradient(weight, self.buffer, off, self.buffer, off + shape[0], shape[0], shape[1],
-                                  -1.0 / n, self.grads[name], work=work)
-                else:
-                    K.es_gradient(weight, self.buffer, off, None, None, shape[0], 1, -1.0 / n, self.grads[name],
-                                  work=work)
-        for side in self.grad_streams:
-            main.wait_stream(side)
+        """grads[name] = -1/n sum_p weight[p] a_p^T b_p (or eps_p) for every parameter (eggroll.py:155-166):
+        one launch over the tiles of every parameter (noise_es_gradient_params), on the current stream."""
+        table = torch.stack([offsets[name] for name in self.shapes])  # [params, pairs]
+        K.es_gradient_params(weight, self.buffer, table, list(self.shapes.values()), self._grad_list, -1.0 / n)
 
     @torch.no_grad()
     def step(self, x, y, optimizer, step):

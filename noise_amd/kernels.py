@@ -364,6 +364,32 @@ def es_gradient(w, a_base, a_off, b_base, b_off, out, inn, scale, G, accumulate=
               _stream())
 
 
+def es_gradient_params(w, buffer, offsets, shapes, grads, scale, accumulate=False):
+    """grads[k] = scale * sum_j w_j a_kj b_kj^T for every parameter k in one launch
+    (eggroll.py:155-163): pair j's noise for parameter k is buffer[offsets[k, j]:][:out + in], split
+    into a (out) and b (in; b = 1 for a vector parameter, shape (out,)). offsets: int64
+    [params, >= pairs] rows; shapes: one (out,) or (out, in) per parameter; grads: contiguous fp32
+    device tensors of those shapes."""
+    _on_gpu(w, buffer, offsets, *grads)
+    _need(w.dtype == torch.float32 and w.is_contiguous(), 'es_gradient_params: contiguous fp32 w')
+    _need(buffer.dtype == torch.float32 and buffer.is_contiguous(), 'es_gradient_params: contiguous fp32 buffer')
+    _need(offsets.dtype == torch.int64 and offsets.dim() == 2 and offsets.stride(1) == 1 and
+          offsets.shape[0] == len(shapes) and offsets.shape[1] >= w.numel(),
+          'es_gradient_params: offsets must be int64 [params, >= pairs] rows')
+    _need(len(grads) == len(shapes), 'es_gradient_params: one gradient per shape')
+    for g, s in zip(grads, shapes):
+        _need(g.dtype == torch.float32 and g.is_contiguous() and tuple(g.shape) == tuple(s),
+              f'es_gradient_params: gradient {tuple(g.shape)} for shape {tuple(s)}')
+        _need(len(s) == 1 or (len(s) == 2 and s[1] > 1),
+              f'es_gradient_params: shape {tuple(s)}: a vector is (out,), a matrix (out, in > 1)')
+    k = len(shapes)
+    outs = (C.c_int * k)(*[s[0] for s in shapes])
+    ins = (C.c_int * k)(*[s[1] if len(s) == 2 else 1 for s in shapes])
+    ptrs = (C.c_void_p * k)(*[g.data_ptr() for g in grads])
+    _lib.call('noise_es_gradient_params', _ptr(w), w.numel(), _ptr(buffer), buffer.numel(), _ptr(offsets),
+              offsets.stride(0), k, outs, ins, ptrs, scale, int(accumulate), _stream())
+
+
 def adamw(param, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, step):
     for t in (param, grad, exp_avg, exp_avg_sq):
         _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), 'adamw: contiguous fp32 device tensors')

@@ -34,6 +34,7 @@ SPILL_BUDGET = {'mlp_fused_kernelILb1ELb1ELi2ELb1E': 16, 'mlp_fused_kernelILb1EL
                 'mlp_fused_kernelILb1ELb1ELi0ELb0E': 16, 'qkv_proj_kernel': 0, 'window_attention_kernel': 2,
                 'qkv_rr_kernelILb0E': 20, 'qkv_rr_kernelILb1E': 24, 'head_rr_kernel': 4,
                 'head_ce_kernelILb1ELb0E': 0, 'embed_norm_kernel': 0, 'es_gradient_kernel': 0,
+                'es_gradient_params_kernel': 0,
                 'mlp_pc_kernel': 128}
 
 

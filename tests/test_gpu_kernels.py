@@ -747,6 +747,50 @@ def test_es_gradient_split_pairs(device, out, inn):
     torch.testing.assert_close(G1, G0, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize('pairs', [1536, 37, 0])
+def test_es_gradient_params_one_launch(device, pairs):
+    """Every parameter's gradient in one launch (ragged matrices, a vector, one shape spanning many
+    tiles) against float64 sums of the reference's noise() slices (eggroll.py:122-128, 155-163);
+    bit-identical to the one-pass noise_es_gradient of each; accumulate adds; a slice past the
+    buffer's end makes that parameter's gradient NaN and leaves the others finite."""
+    from oracle import es_ref
+    g = _gen(pairs + 11)
+    shapes = [(8,), (70, 90), (512, 512), (300,), (129, 65), (2048, 512)]
+    buf = torch.randn(300000, generator=g)
+    table = torch.stack([torch.randint(0, buf.numel() - sum(s), (max(pairs, 1),), generator=g) for s in shapes])
+    w_in = torch.randn(pairs, generator=g)
+    dbuf, dtab, dw = buf.to(device), table.to(device), w_in.to(device)
+    grads = [torch.full(s, float('nan'), device=device) for s in shapes]
+    nk.es_gradient_params(dw, dbuf, dtab, shapes, grads, -1.0 / max(pairs, 1))
+    for k, s in enumerate(shapes):
+        rows = torch.stack([buf[o:o + sum(s)] for o in table[k, :pairs].tolist()]) if pairs else \
+            torch.zeros(0, sum(s))
+        v = (rows[:, :s[0]], rows[:, s[0]:]) if len(s) == 2 else rows
+        ref = es_ref.gradient(w_in.double(), {'p': v}, max(pairs, 1))['p']
+        torch.testing.assert_close(grads[k].cpu().double(), ref, rtol=1e-5, atol=1e-6)
+        if pairs == 0:  # noise_es_gradient takes no empty pair list: the sum is zero
+            assert not grads[k].any()
+            continue
+        one = torch.full(s, float('nan'), device=device)
+        off = dtab[k, :pairs].contiguous()
+        if len(s) == 2:
+            nk.es_gradient(dw, dbuf, off, dbuf, off + s[0], s[0], s[1], -1.0 / max(pairs, 1), one)
+        else:
+            nk.es_gradient(dw, dbuf, off, None, None, s[0], 1, -1.0 / max(pairs, 1), one)
+        assert torch.equal(one, grads[k]), s
+    if pairs == 0:
+        return
+    twice = [t.clone() for t in grads]
+    nk.es_gradient_params(dw, dbuf, dtab, shapes, twice, -1.0 / pairs, accumulate=True)
+    for a, b in zip(twice, grads):
+        torch.testing.assert_close(a, 2 * b, rtol=1e-6, atol=1e-7)
+    bad = dtab.clone()
+    bad[1, pairs // 2] = buf.numel() - sum(shapes[1]) + 1  # one float past the end
+    nk.es_gradient_params(dw, dbuf, bad, shapes, grads, -1.0 / pairs)
+    assert torch.isnan(grads[1]).all()
+    assert all(torch.isfinite(t).all() for k, t in enumerate(grads) if k != 1)
+
+
 @pytest.mark.parametrize('window', [1024, 2048])
 def test_config2_attention_full_size(device, window):
     """Config 2 at its full shape: q, k, v [256 members, 8 heads, 2048 tokens, 64] ~ N(0, 1) bf16.

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import noise_amd
+from noise_amd import kernels as nk
 from noise_amd.synthetic import antithetic, pair_noise, sequence
 from oracle import es_ref
 from oracle import model_ref as R
@@ -374,20 +375,22 @@ def test_eggroll_step_multi_sequence(device, init_params, mode):
         torch.testing.assert_close(p.detach().cpu(), ref, rtol=0, atol=2e-6)
 
 
-def test_eggroll_gradient_side_streams_match_one_stream(device, init_params):
-    """Eggroll.gradient spreads the per-parameter launches over side streams, each with its own
-    split-sum workspace; the result is bit-identical to issuing them all on the current stream,
+def test_eggroll_gradient_one_launch_matches_per_parameter(device, init_params):
+    """Eggroll.gradient forms every parameter's gradient in one launch (noise_es_gradient_params);
+    each is bit-identical to that parameter's own one-pass noise_es_gradient over the same slices,
     and the current stream sees every gradient (read right after the call, with no extra sync)."""
     model = noise_amd.make_model(device, 0)
     es = noise_amd.Eggroll(model, pairs=512, noise_size=1 << 24)
-    assert len(es.grad_streams) > 1
     offsets = es.offsets(3)
     weight = torch.randn(512, generator=torch.Generator().manual_seed(5)).to(device)
     es.grad_flat.fill_(float('nan'))
     es.gradient(weight, offsets, 512)
-    spread = es.grad_flat.clone()
-    es.grad_streams, es.grad_work = [torch.cuda.current_stream(device)], [None]
-    es.grad_flat.fill_(float('nan'))
-    es.gradient(weight, offsets, 512)
-    assert torch.isfinite(spread).all()
-    assert torch.equal(spread, es.grad_flat)
+    assert torch.isfinite(es.grad_flat).all()
+    for name, shape in es.shapes.items():
+        off = offsets[name]
+        G = torch.full(shape, float('nan'), device=device)
+        if len(shape) == 2:
+            nk.es_gradient(weight, es.buffer, off, es.buffer, off + shape[0], shape[0], shape[1], -1.0 / 512, G)
+        else:
+            nk.es_gradient(weight, es.buffer, off, None, None, shape[0], 1, -1.0 / 512, G)
+        assert torch.equal(G, es.grads[name]), name

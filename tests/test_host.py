@@ -200,6 +200,20 @@ def test_step_entry_points_reject_bad_arguments():
     rope.M = 0
     assert lib.noise_rope_norm_ve(C.byref(rope), None) == _lib.NOISE_OK
 
+    # The one-launch gradient of many parameters checks its table before launching.
+    outs, ins = (C.c_int * 65)(*([512] * 65)), (C.c_int * 65)(*([512] * 65))
+    ptrs = (C.c_void_p * 65)(*([fake] * 65))
+    _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1536, 65, outs, ins, ptrs, -1.0, 0, None),
+             'nparams=65')
+    _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1024, 2, outs, ins, ptrs, -1.0, 0, None),
+             'bad sizes')
+    ins[1] = 0
+    _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1536, 2, outs, ins, ptrs, -1.0, 0, None),
+             'parameter 1')
+    ins[1], ptrs[0] = 512, None
+    _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1536, 2, outs, ins, ptrs, -1.0, 0, None),
+             'parameter 0')
+
     # The allocation-free gradient refuses a split that would not fit its fixed array.
     need = lib.noise_es_gradient_work(1536, 4096, 768)
     assert need > lib.noise_es_gradient_noalloc_capacity()
