@@ -18,6 +18,7 @@
 namespace {
 
 constexpr int FT = 1024;
+__device__ const float kOne = 1.0f;  // the b value of a vector parameter, read like a noise value
 
 NOISE_DEV float block_sum(float v, float* red) {
   const int tid = threadIdx.x;
@@ -124,29 +125,41 @@ __global__ __launch_bounds__(256) void es_gradient_kernel(const float* __restric
   // wave (wo, wi) owns the 32 x 32 output block (o0 + 32 wo, i0 + 32 wi): v_mfma_f32_32x32x2_f32,
   // fp32 products and fp32 sums, two pairs per MFMA (lane l: A row l % 32 / B column l % 32 at
   // pair 2 kk + l / 32; accumulator v: row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32)
-  const int lane = tid & 63, wv = tid >> 6, wo = wv >> 1, wi = wv & 1;
+  const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), wo = wv >> 1, wi = wv & 1;
   floatx16 acc = {};
-  // loader: pair lj of the stage, columns lc .. lc + 7
-  const int lj = tid >> 3, lc = (tid & 7) * 8;
   const int jb = blockIdx.z * per, je = min(n, jb + per);  // this workgroup's pairs
-  float ra[8], rb[8];
+  // loader: wave wv fetches pairs wv, wv + 4, .., wv + 28 of a stage, lane = column. Branch-free
+  // (the pair index and the columns clamped into range, padding pairs entering with multiplier 0,
+  // a missing b read as 1 from kOne), so a stage's loads are in flight together; fetch only issues them and
+  // stash, after the stage before has run its MFMAs, applies the multipliers and writes LDS.
+  const bool a_col = o0 + lane < out, b_col = b_base ? i0 + lane < in : lane == 0;
+  const int ac = a_col ? o0 + lane : out - 1, bc = b_col ? i0 + lane : in - 1;
+  float av[8], bv[8], am[8], bm[8];
   auto fetch = [&](int j0) {
-    const int j = j0 + lj;
-    const bool live = j < je;
-    const float wj = live ? w[j] : 0.f;
-    const int64_t ao = live ? a_off[j] : 0, bo = live && b_base ? b_off[j] : 0;
+    int64_t ao[8], bo[8];
+    float wj[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int o = o0 + lc + e, i = i0 + lc + e;
-      ra[e] = live && o < out ? wj * a_base[ao + o] : 0.f;
-      rb[e] = live && i < in ? (b_base ? b_base[bo + i] : 1.0f) : 0.f;
+      const int j = j0 + wv + 4 * e, jc = j < je ? j : je - 1;
+      ao[e] = a_off[jc];
+      bo[e] = b_base ? b_off[jc] : 0;
+      wj[e] = w[jc];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool live = j0 + wv + 4 * e < je;
+      av[e] = a_base[ao[e] + ac];
+      bv[e] = *(b_base ? b_base + bo[e] + bc : &kOne);
+      am[e] = live ? wj[e] : 0.f;
+      bm[e] = live ? 1.0f : 0.f;
     }
   };
   auto stash = [&](int buf) {
-    *reinterpret_cast<float4*>(&As[buf][lj][lc]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-    *reinterpret_cast<float4*>(&As[buf][lj][lc + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
-    *reinterpret_cast<float4*>(&Bs[buf][lj][lc]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-    *reinterpret_cast<float4*>(&Bs[buf][lj][lc + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      As[buf][wv + 4 * e][lane] = a_col ? am[e] * av[e] : 0.f;
+      Bs[buf][wv + 4 * e][lane] = b_col ? bm[e] * bv[e] : 0.f;
+    }
   };
   if (jb < je) fetch(jb);
   for (int j0 = jb, buf = 0; j0 < je; j0 += SJ, buf ^= 1) {
@@ -328,7 +341,6 @@ extern "C" int noise_es_gradient_noalloc(const float* w, int n, const float* a_b
 // buffer makes the pair's terms NaN instead of a read.
 namespace {
 constexpr int GP_MAX = 64;
-__device__ const float kOne = 1.0f;
 struct GradLayout {
   float* G[GP_MAX];
   int out[GP_MAX];
