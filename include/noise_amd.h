@@ -336,6 +336,13 @@ int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_
 /* bf16 copy of an fp32 buffer (hi), and optionally the residual bf16(x - hi) (lo). */
 int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, void* stream);
 
+/* noise_cast_bf16 over `count` (<= 64) buffers in one launch: hi[k][i] = bf16(x[k][i]) and, where lo
+ * and lo[k] are non-NULL, lo[k][i] = bf16(x[k][i] - hi[k][i]), for i < n[k]. x, n, hi, lo are host
+ * arrays of device pointers / sizes. Bit-identical to one noise_cast_bf16 per buffer. No
+ * counterpart in the reference: the bf16 weight copies its autocast forms inside each product. */
+int noise_cast_bf16_many(int count, const float* const* x, const int64_t* n, uint16_t* const* hi,
+                         uint16_t* const* lo, void* stream);
+
 /* ---- Soft-capped log-sum-exp probes of the readout head ----------------------------------
  * cap(v) = 15 tanh(v / 15). A target y < 0 masks its token (output 0); a target >= V makes the
  * token's outputs NaN (the reference's gather would fault). */

@@ -27,10 +27,11 @@ int check_launch(const char* what) {
 extern "C" const char* noise_last_error(void) { return noise::g_error; }
 extern "C" int noise_abi_version(void) { return 2; }
 
-__global__ void cast_bf16_kernel(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ hi,
-                                 uint16_t* __restrict__ lo) {
-  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
+namespace {
+// hi = bf16(x), lo = bf16(x - hi) (lo optional) for the elements i, i + stride, .. of x[0, n), four at
+// a time (x 16-byte, hi and lo 8-byte aligned)
+__device__ void cast_span(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ hi,
+                          uint16_t* __restrict__ lo, int64_t i, int64_t stride) {
   for (; i < n; i += stride) {
     if (i + 4 <= n) {
       float4 v = *reinterpret_cast<const float4*>(x + i);
@@ -56,6 +57,27 @@ __global__ void cast_bf16_kernel(const float* __restrict__ x, int64_t n, uint16_
   }
 }
 
+constexpr int CAST_MAX = 64;
+struct CastList {
+  const float* x[CAST_MAX];
+  uint16_t* hi[CAST_MAX];
+  uint16_t* lo[CAST_MAX];
+  int64_t n[CAST_MAX];
+};
+}  // namespace
+
+__global__ void cast_bf16_kernel(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ hi,
+                                 uint16_t* __restrict__ lo) {
+  cast_span(x, n, hi, lo, ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4, (int64_t)gridDim.x * blockDim.x * 4);
+}
+
+// blockIdx.y = the buffer; the blocks along x stride over it
+__global__ void cast_bf16_many_kernel(const CastList l) {
+  const int k = blockIdx.y;
+  cast_span(l.x[k], l.n[k], l.hi[k], l.lo[k], ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4,
+            (int64_t)gridDim.x * blockDim.x * 4);
+}
+
 extern "C" int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, void* stream) {
   NOISE_REQUIRE(n >= 0 && x && hi, "cast_bf16: bad arguments (n=%lld)", (long long)n);
   NOISE_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)hi % 8) == 0 && (!lo || ((uintptr_t)lo % 8) == 0),
@@ -65,6 +87,30 @@ extern "C" int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t
   if (blocks > 16384) blocks = 16384;
   cast_bf16_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(x, n, hi, lo);
   return noise::check_launch("cast_bf16");
+}
+
+extern "C" int noise_cast_bf16_many(int count, const float* const* x, const int64_t* n, uint16_t* const* hi,
+                                    uint16_t* const* lo, void* stream) {
+  NOISE_REQUIRE(count > 0 && count <= CAST_MAX, "cast_bf16_many: count=%d must be in 1..%d", count, CAST_MAX);
+  NOISE_REQUIRE(x && n && hi, "cast_bf16_many: null argument");
+  CastList l;
+  int64_t blocks = 1;
+  for (int k = 0; k < count; ++k) {
+    uint16_t* lk = lo ? lo[k] : nullptr;
+    NOISE_REQUIRE(n[k] >= 0 && (n[k] == 0 || (x[k] && hi[k])), "cast_bf16_many: buffer %d: bad arguments (n=%lld)",
+                  k, (long long)n[k]);
+    NOISE_REQUIRE(((uintptr_t)x[k] % 16) == 0 && ((uintptr_t)hi[k] % 8) == 0 && ((uintptr_t)lk % 8) == 0,
+                  "cast_bf16_many: buffer %d misaligned", k);
+    l.x[k] = x[k];
+    l.hi[k] = hi[k];
+    l.lo[k] = lk;
+    l.n[k] = n[k];
+    const int64_t b = (n[k] / 4 + 255) / 256 + 1;
+    blocks = b > blocks ? b : blocks;
+  }
+  if (blocks > 512) blocks = 512;
+  cast_bf16_many_kernel<<<dim3((unsigned)blocks, (unsigned)count), 256, 0, (hipStream_t)stream>>>(l);
+  return noise::check_launch("cast_bf16_many");
 }
 
 // One workgroup per member: fixed-order tree sum of its T per-token losses.

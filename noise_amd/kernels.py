@@ -315,6 +315,22 @@ def cast_bf16(x, hi, lo=None):
     _lib.call('noise_cast_bf16', _ptr(x), x.numel(), _ptr(hi), _ptr(lo), _stream())
 
 
+def cast_bf16_many(items):
+    """cast_bf16 over up to 64 (x, hi, lo or None) triples in one launch."""
+    _need(0 < len(items) <= 64, 'cast_bf16_many: 1..64 buffers')
+    for x, hi, lo in items:
+        _on_gpu(x, hi, lo)
+        _need(x.dtype == torch.float32 and x.is_contiguous() and hi.is_contiguous() and
+              (lo is None or lo.is_contiguous()), 'cast_bf16_many: contiguous fp32')
+        _need(hi.numel() == x.numel() and (lo is None or lo.numel() == x.numel()), 'cast_bf16_many: sizes')
+    k = len(items)
+    xs = (C.c_void_p * k)(*[x.data_ptr() for x, _, _ in items])
+    ns = (C.c_int64 * k)(*[x.numel() for x, _, _ in items])
+    his = (C.c_void_p * k)(*[hi.data_ptr() for _, hi, _ in items])
+    los = (C.c_void_p * k)(*[None if lo is None else lo.data_ptr() for _, _, lo in items])
+    _lib.call('noise_cast_bf16_many', k, xs, ns, his, los, _stream())
+
+
 def pair_gather(buffer, offsets, directions, widths, starts, out):
     """out[d, starts[k] + i] = buffer[offsets[k, directions[d]] + min(i, widths[k] - 1)] for
     i < widths[k] rounded up to 4: every parameter's noise slice of the pairs `directions`, side by

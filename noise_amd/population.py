@@ -69,16 +69,19 @@ class PreparedWeights:
     def refresh(self):
         """Re-derive the bf16 copies from the fp32 parameters (after every optimizer step)."""
         p, d = self.params, self.cfg.n_embd
+        casts = []  # one launch for every plain copy
         for i in range(self.cfg.n_layer):
             pre = f'transformer.h.{i}.'
             for j, name in enumerate(('c_q', 'c_k', 'c_v')):
-                K.cast_bf16(p[pre + f'attn.{name}.weight'].contiguous(), self.qkv[i][j * d:(j + 1) * d])
-            K.cast_bf16(p[pre + 'attn.c_proj.weight'].contiguous(), self.o[i])
-            K.cast_bf16(p[pre + 'mlp.c_fc.weight'].contiguous(), self.fc[i])
-            K.cast_bf16(p[pre + 'mlp.c_proj.weight'].contiguous(), self.mp[i])
+                casts.append((p[pre + f'attn.{name}.weight'].contiguous(), self.qkv[i][j * d:(j + 1) * d], None))
+            casts.append((p[pre + 'attn.c_proj.weight'].contiguous(), self.o[i], None))
+            casts.append((p[pre + 'mlp.c_fc.weight'].contiguous(), self.fc[i], None))
+            casts.append((p[pre + 'mlp.c_proj.weight'].contiguous(), self.mp[i], None))
             K.mlp_pack(p[pre + 'mlp.c_fc.weight'].contiguous(), self.fc_packed[i],
                        p[pre + 'mlp.c_proj.weight'].contiguous(), self.mp_packed[i])
-        K.cast_bf16(p['lm_head.weight'].contiguous(), self.head_hi, self.head_lo)
+        casts.append((p['lm_head.weight'].contiguous(), self.head_hi, self.head_lo))
+        for k in range(0, len(casts), 64):
+            K.cast_bf16_many(casts[k:k + 64])
 
     def gate(self, i):
         return self.params[f'transformer.h.{i}.attn.ve_gate.weight']

@@ -516,6 +516,29 @@ def test_cast_bf16_round_to_nearest_even(device):
     assert torch.equal(lo.cpu(), (x - x.to(torch.bfloat16).float()).to(torch.bfloat16))
 
 
+def test_cast_bf16_many_matches_single_casts(device):
+    """One launch over ragged buffers (sizes not multiples of 4, one empty, one much larger, lo on
+    some) gives bit for bit what one cast_bf16 per buffer gives, and nothing past each buffer."""
+    g = _gen(18)
+    sizes = [5, 0, 1 << 20, 4099, 262144, 3]
+    xs = [(torch.randn(n, generator=g) * 10).to(device) for n in sizes]
+    los = [i % 2 == 0 for i in range(len(sizes))]
+    his = [torch.full((n + 8,), float('nan'), dtype=torch.bfloat16, device=device) for n in sizes]
+    lo_t = [torch.full((n + 8,), float('nan'), dtype=torch.bfloat16, device=device) if l else None
+            for n, l in zip(sizes, los)]
+    nk.cast_bf16_many([(x, h[:x.numel()], l[:x.numel()] if l is not None else None)
+                       for x, h, l in zip(xs, his, lo_t)])
+    for x, h, l in zip(xs, his, lo_t):
+        n = x.numel()
+        h1 = torch.empty(n, dtype=torch.bfloat16, device=device)
+        l1 = torch.empty_like(h1)
+        if n:
+            nk.cast_bf16(x, h1, l1)
+        assert torch.equal(h[:n], h1) and torch.isnan(h[n:]).all()
+        if l is not None:
+            assert torch.equal(l[:n], l1) and torch.isnan(l[n:]).all()
+
+
 def _gather_layout(shapes):
     widths = [sum(s) for s in shapes.values()]
     padded = [-(-w // 4) * 4 for w in widths]

@@ -214,6 +214,13 @@ def test_step_entry_points_reject_bad_arguments():
     _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1536, 2, outs, ins, ptrs, -1.0, 0, None),
              'parameter 0')
 
+    # The grouped bf16 cast checks its list: at most 64 buffers, each aligned.
+    xs, his = (C.c_void_p * 65)(*([fake] * 65)), (C.c_void_p * 65)(*([fake] * 65))
+    ns = (C.c_int64 * 65)(*([16] * 65))
+    _rejects(lib.noise_cast_bf16_many(65, xs, ns, his, None, None), 'count=65')
+    xs[1] = odd
+    _rejects(lib.noise_cast_bf16_many(2, xs, ns, his, None, None), 'buffer 1 misaligned')
+
     # The allocation-free gradient refuses a split that would not fit its fixed array.
     need = lib.noise_es_gradient_work(1536, 4096, 768)
     assert need > lib.noise_es_gradient_noalloc_capacity()
