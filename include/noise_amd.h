@@ -333,6 +333,14 @@ int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_
                 float lr, float beta1, float beta2, float eps, float weight_decay, int step,
                 void* stream);
 
+/* noise_adamw that leaves param, exp_avg and exp_avg_sq untouched when *status != NOISE_OK
+ * (status: a device int, such as the one noise_fitness writes), read on the device, so the update
+ * can be queued before the status is read back. No counterpart in the reference, whose step has
+ * no non-finite check. */
+int noise_adamw_unless(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                       float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                       const int* status, void* stream);
+
 /* bf16 copy of an fp32 buffer (hi), and optionally the residual bf16(x - hi) (lo). */
 int noise_cast_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, void* stream);
 

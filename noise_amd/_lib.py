@@ -117,6 +117,7 @@ SIGNATURES = {
     'noise_es_gradient_noalloc': [P, INT, P, P, P, P, INT, INT, F32, INT, P, P],
     'noise_es_gradient_noalloc_capacity': [],
     'noise_adamw': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P],
+    'noise_adamw_unless': [P, P, P, P, I64, F32, F32, F32, F32, F32, INT, P, P],
     'noise_cast_bf16': [P, I64, P, P, P],
     'noise_cast_bf16_many': [INT, P, P, P, P, P],
     'noise_coordinate_differences': [P, INT, I64, P, INT, INT, F32, P, I64, P],

@@ -215,7 +215,9 @@ NOISE_DEV float lerp_torch(float start, float end, float weight) {
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ param, const float* __restrict__ grad,
                                                     float* __restrict__ m, float* __restrict__ v, int64_t n,
                                                     float decay, float w1, float beta2, float w2,
-                                                    float step_size, float bc2_sqrt, float eps) {
+                                                    float step_size, float bc2_sqrt, float eps,
+                                                    const int* __restrict__ skip) {
+  if (skip && *skip != NOISE_OK) return;  // the caller's status says the gradient is not to be applied
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {
@@ -522,9 +524,9 @@ extern "C" int noise_pair_gather(const float* buffer, int64_t buffer_len, const 
   return noise::check_launch("pair_gather");
 }
 
-extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
-                           float lr, float beta1, float beta2, float eps, float weight_decay, int step,
-                           void* stream) {
+static int adamw_launch(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n, float lr,
+                        float beta1, float beta2, float eps, float weight_decay, int step, const int* skip,
+                        void* stream) {
   NOISE_REQUIRE(param && grad && exp_avg && exp_avg_sq && n >= 0, "adamw: bad arguments");
   NOISE_REQUIRE(step >= 1, "adamw: step=%d must count from 1", step);
   if (n == 0) return NOISE_OK;
@@ -536,6 +538,19 @@ extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, floa
   if (blocks > 8192) blocks = 8192;
   adamw_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(param, grad, exp_avg, exp_avg_sq, n,
                                                               1.0f - lr * weight_decay, 1.0f - beta1, beta2,
-                                                              1.0f - beta2, step_size, bc2_sqrt, eps);
+                                                              1.0f - beta2, step_size, bc2_sqrt, eps, skip);
   return noise::check_launch("adamw");
+}
+
+extern "C" int noise_adamw(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                           float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                           void* stream) {
+  return adamw_launch(param, grad, exp_avg, exp_avg_sq, n, lr, beta1, beta2, eps, weight_decay, step, nullptr, stream);
+}
+
+extern "C" int noise_adamw_unless(float* param, const float* grad, float* exp_avg, float* exp_avg_sq, int64_t n,
+                                  float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                                  const int* status, void* stream) {
+  NOISE_REQUIRE(status, "adamw_unless: null status");
+  return adamw_launch(param, grad, exp_avg, exp_avg_sq, n, lr, beta1, beta2, eps, weight_decay, step, status, stream);
 }

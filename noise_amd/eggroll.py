@@ -24,6 +24,7 @@ import torch
 from . import kernels as K
 from .config import GPTConfig, param_shapes
 from .kernels import NoiseRows
+from .optim import AdamW
 from .population import Engine, PreparedWeights
 
 SEED = 0
@@ -138,13 +139,20 @@ class Eggroll:
         ranked = torch.empty(n, device=self.device) if self.fitness == 'ranks' else None
         K.fitness(losses, pairs, weight, self.status, self.fitness, ranked)
         self.gradient(weight, offsets, n)
-        # One host sync per step: the status and the mean loss come back together, before the
-        # weights move (the reference reads only the mean, eggroll.py:168).
-        status, mean = torch.stack([self.status[0].to(torch.float32), losses.mean()]).tolist()
-        if status != 0:
-            raise FloatingPointError('non-finite member loss in the population step')
         optimizer.zero_grad(set_to_none=True)
         for name, p in self.params.items():
             p.grad = self.grads[name]
-        optimizer.step()
+        # One host sync per step: the status and the mean loss come back together (the reference
+        # reads only the mean, eggroll.py:168). This package's AdamW is queued before that read and
+        # skips its update on the device when the status is set; another optimizer steps after it.
+        queued = isinstance(optimizer, AdamW)
+        if queued:
+            optimizer.step(unless=self.status)
+        status, mean = torch.stack([self.status[0].to(torch.float32), losses.mean()]).tolist()
+        if status != 0:
+            if queued:
+                optimizer.rewind()
+            raise FloatingPointError('non-finite member loss in the population step')
+        if not queued:
+            optimizer.step()
         return mean

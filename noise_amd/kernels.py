@@ -406,8 +406,15 @@ def es_gradient_params(w, buffer, offsets, shapes, grads, scale, accumulate=Fals
               offsets.stride(0), k, outs, ins, ptrs, scale, int(accumulate), _stream())
 
 
-def adamw(param, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, step):
+def adamw(param, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, step, unless=None):
+    """One AdamW update; with `unless` (a device int32 status) it is skipped on the device when the
+    status is not NOISE_OK."""
     for t in (param, grad, exp_avg, exp_avg_sq):
         _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), 'adamw: contiguous fp32 device tensors')
-    _lib.call('noise_adamw', _ptr(param), _ptr(grad), _ptr(exp_avg), _ptr(exp_avg_sq), param.numel(), lr, beta1,
-              beta2, eps, weight_decay, step, _stream())
+    if unless is None:
+        _lib.call('noise_adamw', _ptr(param), _ptr(grad), _ptr(exp_avg), _ptr(exp_avg_sq), param.numel(), lr, beta1,
+                  beta2, eps, weight_decay, step, _stream())
+        return
+    _need(unless.is_cuda and unless.dtype == torch.int32 and unless.numel() >= 1, 'adamw: unless is a device int32')
+    _lib.call('noise_adamw_unless', _ptr(param), _ptr(grad), _ptr(exp_avg), _ptr(exp_avg_sq), param.numel(), lr,
+              beta1, beta2, eps, weight_decay, step, _ptr(unless), _stream())

@@ -62,7 +62,11 @@ class AdamW(torch.optim.Optimizer):
         return flats
 
     @torch.no_grad()
-    def step(self, closure=None):
+    def step(self, closure=None, unless=None):
+        """One update of every parameter with a gradient. unless: a device int32 status; when it
+        is not 0 on the device, the launches leave parameters and moments as they are (the host's
+        step counts still advance: `rewind()` takes them back)."""
+        self._advanced = []
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -79,13 +83,22 @@ class AdamW(torch.optim.Optimizer):
             if flats is not None:
                 for p in params:
                     self.state[p]['step'] += 1
-                K.adamw(pflat, gflat, flats[0], flats[1], *args, int(self.state[params[0]]['step']))
+                self._advanced += params
+                K.adamw(pflat, gflat, flats[0], flats[1], *args, int(self.state[params[0]]['step']), unless=unless)
                 continue
             for p in params:
                 st = self._state(p)
                 st['step'] += 1
+                self._advanced.append(p)
                 for key in ('exp_avg', 'exp_avg_sq'):
                     if not st[key].is_contiguous():
                         st[key] = st[key].contiguous()
-                K.adamw(p, p.grad.contiguous(), st['exp_avg'], st['exp_avg_sq'], *args, int(st['step']))
+                K.adamw(p, p.grad.contiguous(), st['exp_avg'], st['exp_avg_sq'], *args, int(st['step']), unless=unless)
         return loss
+
+    def rewind(self):
+        """Take back the step counts the last step() advanced (after its `unless` status skipped
+        the update on the device)."""
+        for p in getattr(self, '_advanced', []):
+            self.state[p]['step'] -= 1
+        self._advanced = []

@@ -647,6 +647,22 @@ def test_fitness_gradient_adamw(device):
     torch.testing.assert_close(dp.cpu(), refp.detach(), rtol=0, atol=1e-6)
 
 
+def test_adamw_unless_status(device):
+    """noise_adamw_unless: with the status at NOISE_OK the same update as noise_adamw, bit for bit;
+    with it set (as noise_fitness sets it for a non-finite loss) parameters and moments unchanged."""
+    g = _gen(23)
+    p0, grad = torch.randn(4099, generator=g), torch.randn(4099, generator=g) * 1e-3
+    m0, v0 = torch.randn(4099, generator=g) * 1e-3, torch.rand(4099, generator=g) * 1e-6
+    ref = [t.to(device) for t in (p0, m0, v0)]
+    nk.adamw(*ref[:1], grad.to(device), *ref[1:], 1e-3, 0.9, 0.95, 1e-8, 0.1, 3)
+    for code, want in ((0, ref), (_lib.NOISE_ENONFINITE, [t.to(device) for t in (p0, m0, v0)])):
+        st = torch.tensor([code], dtype=torch.int32, device=device)
+        got = [t.to(device) for t in (p0, m0, v0)]
+        nk.adamw(got[0], grad.to(device), got[1], got[2], 1e-3, 0.9, 0.95, 1e-8, 0.1, 3, unless=st)
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), code
+
+
 def test_adamw_state_dict_round_trip(device):
     """noise_amd.AdamW keeps torch.optim.AdamW's state format: after two one-launch steps on a GPT
     whose parameters and gradients tile flat buffers, state_dict() holds every moment and the step;

@@ -299,6 +299,36 @@ def test_config1_mlp_block(device):
         assert float((got - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
 
 
+def test_eggroll_step_nonfinite_loss_leaves_weights(device, init_params):
+    """A non-finite member loss makes Eggroll.step raise FloatingPointError; the AdamW update it
+    queued before reading the status back skips itself on the device, so every parameter, moment and
+    step count is as before the call, and the next finite step proceeds normally."""
+    model = noise_amd.make_model(device, 0)
+    es = noise_amd.Eggroll(model, pairs=4, chunk=4, noise_size=1 << 22)
+    opt = noise_amd.AdamW(model.parameters(), lr=1e-3, betas=(0.5, 0.95), eps=1e-8, weight_decay=0.0)
+    idx, targets = sequence(256, seed=52)
+    x, y = idx[None].to(device), targets[None].to(device)
+    es.step(x, y, opt, 1)  # moments and step counts to compare against
+    head = dict(model.named_parameters())['lm_head.weight']
+    keep = head[7].clone()
+    with torch.no_grad():
+        head[7, 0] = float('nan')  # token 7's logit is NaN: every member's loss is
+    bits = {k: v.detach().clone().view(torch.int32) for k, v in model.named_parameters()}
+    state = {k: (float(opt.state[v]['step']), opt.state[v]['exp_avg'].clone(), opt.state[v]['exp_avg_sq'].clone())
+             for k, v in model.named_parameters()}
+    with pytest.raises(FloatingPointError):
+        es.step(x, y, opt, 2)
+    for k, v in model.named_parameters():
+        assert torch.equal(v.detach().view(torch.int32), bits[k]), k
+        st = opt.state[v]
+        assert float(st['step']) == state[k][0]
+        assert torch.equal(st['exp_avg'], state[k][1]) and torch.equal(st['exp_avg_sq'], state[k][2]), k
+    with torch.no_grad():
+        head[7] = keep
+    mean = es.step(x, y, opt, 2)
+    assert math.isfinite(mean) and float(opt.state[head]['step']) == 2.0
+
+
 def test_eggroll_step_matches_oracle(device, init_params):
     """One EGGROLL update (pairs = 4, T = 256), stage by stage against the oracle: member losses on
     the step's noise slices, then fitness + gradient from those losses, then the AdamW update from

@@ -214,6 +214,10 @@ def test_step_entry_points_reject_bad_arguments():
     _rejects(lib.noise_es_gradient_params(fake, 1536, fake, 1 << 20, fake, 1536, 2, outs, ins, ptrs, -1.0, 0, None),
              'parameter 0')
 
+    # The status-guarded AdamW needs its status.
+    _rejects(lib.noise_adamw_unless(fake, fake, fake, fake, 10, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1, None, None),
+             'null status')
+
     # The grouped bf16 cast checks its list: at most 64 buffers, each aligned.
     xs, his = (C.c_void_p * 65)(*([fake] * 65)), (C.c_void_p * 65)(*([fake] * 65))
     ns = (C.c_int64 * 65)(*([16] * 65))
